@@ -1,0 +1,228 @@
+/*
+ * quiver_hip.h -- C ABI of the MI355X-native Quiver query path.
+ *
+ * Plain pointers and sizes only.  Every call returns a QV_* status; on failure
+ * qv_last_error() returns a thread-local message.  Nothing here throws or exits.
+ * Host buffers are owned by the caller and are never registered with the HIP
+ * runtime; device state (graph pages, PQ codes, tables, search scratch) is owned
+ * by the library and freed by qv_index_close().  One search may run per index
+ * handle at a time; calls are blocking.
+ *
+ * Each entry point names the reference interface it replaces
+ * (ruc-system/quiver-ae paths).
+ */
+#ifndef QUIVER_HIP_H
+#define QUIVER_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QV_OK 0
+#define QV_EINVAL -1      /* bad argument or option */
+#define QV_EIO -2         /* file missing, short or malformed */
+#define QV_EHIP -3        /* HIP runtime error */
+#define QV_ETIMEDOUT -4   /* search exceeded qv_search_opts.timeout_s */
+#define QV_EUNSUPPORTED -5/* feature outside this build (SPDK, mmap, R > 64, ...) */
+#define QV_ENOMEM -6      /* host or device allocation failed */
+#define QV_EINDEX -7      /* index content invalid (ids out of range, ...) */
+
+/* Element types: shared::DataType (src/shared/common/data_type.hpp:5-9). */
+#define QV_UINT8 0
+#define QV_FLOAT 1
+#define QV_INT8 2
+
+/* Early-exit policies: quiver::EarlyExitPolicy (src/quiver/io_control.cuh:41-46)
+ * as exposed by the CLI (bin/quiver_search.cu:48-54). */
+#define QV_EXIT_NONE 0
+#define QV_EXIT_GPRUNING 2
+
+/* Admission modes of qv_search. */
+#define QV_ADMIT_STREAMING 0 /* window of num_blocks*Q + prefeed queries, as
+                                run_persistent_search (src/quiver/search.cu:827-1051) */
+#define QV_ADMIT_BATCH 1     /* every query admitted when the clock starts */
+
+typedef struct qv_index qv_index;
+
+/* shared::Layout (src/shared/common/layout.hpp:7-19) plus the PQ shape. */
+typedef struct {
+  int64_t num_data;
+  int64_t num_dims;
+  int64_t max_m0;         /* R */
+  int64_t enter_point;    /* medoid */
+  int64_t data_size;
+  int64_t node_size;
+  int64_t num_pages;
+  int64_t nodes_per_page;
+  int32_t data_type;      /* QV_UINT8 / QV_FLOAT / QV_INT8 */
+  int32_t num_chunks;     /* PQ M */
+  int32_t device;
+  int32_t slots_per_cu;   /* resident search workgroups per CU for this index */
+  int64_t device_bytes;   /* HBM held by the index */
+} qv_index_info;
+
+/* Replaces bin_common::prepare_search_setup (bin/common/search_setup.hpp:73-119):
+ * find_index_file / find_pq_prefix discovery (bin/common/index_discovery.hpp:57-103),
+ * parse_diskann_metadata (bin/common/metadata.hpp:15-72), PQSearch::read_data
+ * (src/shared/index/pq_search.cu:62-114), create_mem_loader_sync heap mode
+ * (src/shared/io/mem_loader.cpp:28-44) and PQSearch::init_device
+ * (src/shared/index/pq_search.cu:116-177).  The page image, the codes and the PQ
+ * tables are placed in HBM of `device`.  memory_backend is "heap"; "mmap" returns
+ * QV_EUNSUPPORTED.  memory_index_file may be NULL (defaults to the discovered
+ * index file, as --memory-index-file does). */
+int qv_index_open(const char* index_dir, const char* data_type,
+                  const char* memory_backend, const char* memory_index_file,
+                  int device, qv_index** out);
+
+int qv_index_get_info(const qv_index* index, qv_index_info* out);
+
+/* Frees every device and host resource of the handle.  NULL is accepted. */
+void qv_index_close(qv_index* index);
+
+/* Options of run_persistent_search (src/quiver/search.cuh:45-66) and of the
+ * quiver_search CLI (bin/quiver_search.cu:61-147). */
+typedef struct {
+  int32_t num_blocks;        /* persistent workgroups (--num-blocks); 0 fills the GPU */
+  int32_t queries_per_block; /* --queries-per-block; only 1 is supported */
+  int32_t pipe_width;        /* --pipe-width, 1..16 */
+  int32_t early_exit;        /* QV_EXIT_NONE / QV_EXIT_GPRUNING */
+  int32_t gpruning_warmup;   /* 10 in the reference CLI */
+  int32_t gpruning_patience; /* 8 in the reference CLI */
+  int32_t prefeed;           /* QUIVER_PREFEED */
+  int32_t admit_min_batch;   /* QUIVER_ADMIT_MIN_BATCH */
+  int32_t admission;         /* QV_ADMIT_STREAMING / QV_ADMIT_BATCH */
+  int32_t device_buffers;    /* 1: queries and outputs are device pointers */
+  double timeout_s;          /* 0: no limit */
+} qv_search_opts;
+
+/* shared::RunReport (src/shared/common/run_report.hpp:32-56) for one search. */
+typedef struct {
+  double qps;
+  double search_time_s;      /* first admission -> results ready */
+  double lat_avg_ms, lat_p50_ms, lat_p90_ms, lat_p99_ms, lat_p999_ms, lat_max_ms;
+  double avg_hops;           /* expanded nodes per query (finish step) */
+  double kernel_ms;          /* search kernel duration from HIP events */
+  int32_t num_blocks;
+  int32_t max_inflight;
+  int32_t early_stopped;     /* queries ended by gpruning */
+  int32_t reserved;
+} qv_search_report;
+
+void qv_search_opts_default(qv_search_opts* opts);
+
+/* Replaces quiver::run_persistent_search (src/quiver/search.cuh:45-66).
+ * queries: [nq][dim] float (uint8/int8 queries are passed as floats, as
+ * load_queries_as_float does, bin/common/data_io.hpp:73-108).
+ * ids [nq][topk] int32 (-1 padded), dists [nq][topk] float (+inf padded),
+ * found [nq] int32 (may be NULL), report may be NULL.
+ * With opts->device_buffers, queries/ids/dists/found are device pointers. */
+int qv_search(qv_index* index, const float* queries, int64_t nq, int32_t dim,
+              int32_t topk, int32_t ef_search, const qv_search_opts* opts,
+              int32_t* ids, float* dists, int32_t* found, qv_search_report* report);
+
+/* Per-query hop counts of the last qv_search on this handle, [nq] int32. */
+int qv_last_hops(const qv_index* index, int32_t* hops, int64_t nq);
+
+/* Thread-local message of the last failing call on this thread. */
+const char* qv_last_error(void);
+
+/* Device count and gfx name of `device` (for diagnostics). */
+int qv_device_info(int device, char* name, int32_t name_len, int32_t* num_cus,
+                   int64_t* total_mem);
+
+/* ---- Device-buffer plumbing (no reference counterpart) ---------------------
+ * For callers that reach the library through a plain FFI (ctypes) and have no
+ * HIP binding of their own: allocate, copy and clear device memory on the
+ * library's HIP runtime.  kind: 0 host->device, 1 device->host, 2 device->device. */
+int qv_device_count(int32_t* count);
+int qv_dev_alloc(int device, int64_t bytes, void** out);
+int qv_dev_free(void* ptr);
+int qv_dev_copy(void* dst, const void* src, int64_t bytes, int32_t kind);
+int qv_dev_clear(void* ptr, int64_t bytes);
+
+/* ---- PQ look-up tables (src/shared/index/pq_device.cuh:9-36) ----------------
+ * Builds LUT[q][m][256] for nq queries on the device.  Tables may come from an
+ * index (qv_lut_build) or be passed raw (qv_lut_build_raw: centroid [dim],
+ * pivots_t [dim][256], chunk_offsets [M+1], all device pointers, as are queries,
+ * luts and q_used).  q_used ([nq][dim], may be NULL) receives fl(fl(q-mu)+mu). */
+int qv_lut_build(qv_index* index, const float* d_queries, int64_t nq,
+                 float* d_luts, float* d_q_used);
+int qv_lut_build_raw(const float* d_centroid, const float* d_pivots_t,
+                     const int32_t* d_chunk_offsets, int32_t dim, int32_t num_chunks,
+                     const float* d_queries, int64_t nq, float* d_luts,
+                     float* d_q_used, int device);
+
+/* ---- ADC gather-sum + top-k microbenchmark ---------------------------------
+ * The fused ADC of persistent_merge_data (src/quiver/kernel_core/
+ * kernel_helpers.cuh:271-287) with top-k maintenance, in isolation:
+ * for each query q and s in [0, ids_per_query): d = sum_m LUT[q][m][codes[id][m]]
+ * (sequential fp32 sum over m) with id = ids[q][s]; keeps the topk smallest
+ * under (d, s), i.e. the reference's first-found-wins insert applied in s order.
+ * All pointers are device pointers: luts [nq][M][256] f32, codes
+ * [num_codes][M] u8, ids [nq][ids_per_query] int32 (each < num_codes),
+ * out_ids [nq][topk] int32, out_dists [nq][topk] f32, dist_sums [nq] f64 (may
+ * be NULL; the sum of all distances of a query).  elapsed_ms (may be NULL)
+ * receives the kernel time from HIP events. */
+int qv_adc_bench(const float* d_luts, int32_t num_chunks, const uint8_t* d_codes,
+                 int64_t num_codes, const int32_t* d_ids, int64_t nq,
+                 int64_t ids_per_query, int32_t topk, int32_t* d_out_ids,
+                 float* d_out_dists, double* d_dist_sums, int device,
+                 float* elapsed_ms);
+
+/* Counter-based fills for synthetic tables: 8-byte word w of the buffer is a
+ * function of (seed, w) only; id i is uniform in [0, num_codes) and a function
+ * of (seed, i) only. */
+int qv_fill_uniform_bytes(uint8_t* d_dst, int64_t nbytes, uint64_t seed, int device);
+int qv_fill_uniform_ids(int32_t* d_dst, int64_t count, int64_t num_codes,
+                        uint64_t seed, int device);
+
+/* ---- Index construction (DiskANN's build_disk_index is absent: this replaces
+ * the build step the reference delegates to deps/DiskANN, CMakeLists.txt:35-39).
+ * Writes <out_prefix>_disk.index, <out_prefix>_pq_pivots.bin and
+ * <out_prefix>_pq_compressed.bin in the formats the reference reads
+ * (bin/common/metadata.hpp:15-72, src/shared/index/pq_search.cu:62-114).
+ * base: host [n][dim] of data_type.  CPU build with OpenMP (`threads`, <=0 all). */
+typedef struct {
+  int32_t R;             /* max degree */
+  int32_t L;             /* build beam width */
+  float alpha;           /* RobustPrune alpha */
+  int32_t num_chunks;    /* PQ M */
+  int32_t kmeans_iters;  /* PQ k-means iterations */
+  int32_t pq_train_max;  /* training sample size for PQ */
+  uint64_t seed;
+  int32_t threads;
+  int32_t passes;        /* 1: alpha only; 2: 1.0 then alpha */
+} qv_build_params;
+
+void qv_build_params_default(qv_build_params* p);
+
+int qv_build_index_cpu(const void* base, int32_t data_type, int64_t n, int32_t dim,
+                       const qv_build_params* params, const char* out_prefix);
+
+/* ---- Synthetic data: the seeded Gaussian mixture of the benchmark configs ----
+ * Host generator (CPU) and device generator (HIP) produce identical values for
+ * the same arguments.  uint8: centres uniform in [lo, hi], per-dim sigma, rounded
+ * and clipped to [0, 255].  float: centres and noise standard normal, rows L2
+ * normalised when normalize != 0.  Normal deviates are Irwin-Hall(12) sums of
+ * counter-based 16-bit uniforms (exact in fp32), so the host and the device
+ * produce the same uint8 rows bit for bit. */
+typedef struct {
+  uint64_t seed;
+  int32_t num_centers;
+  int32_t dim;
+  int32_t data_type;     /* QV_UINT8 or QV_FLOAT */
+  float center_lo, center_hi, sigma;
+  int32_t normalize;
+} qv_mixture;
+
+int qv_mixture_fill_host(const qv_mixture* mix, int64_t first_row, int64_t rows,
+                         void* dst);
+int qv_mixture_fill_device(const qv_mixture* mix, int64_t first_row, int64_t rows,
+                           void* d_dst, int device);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

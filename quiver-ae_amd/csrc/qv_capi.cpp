@@ -1,0 +1,108 @@
+// qv_capi.cpp -- host-only C ABI entry points: error text, index construction,
+// host-side synthetic data.
+#include <cmath>
+#include <cstring>
+#include <exception>
+#include <new>
+#include <string>
+
+#include <omp.h>
+
+#include "qv_common.hpp"
+#include "qv_mixture.hpp"
+
+namespace qv {
+
+namespace {
+thread_local std::string g_last_error;
+
+template <class F>
+int host_guard(F&& f) {
+  try {
+    f();
+    return QV_OK;
+  } catch (const Error& e) {
+    set_last_error(e.what());
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    set_last_error("host allocation failed");
+    return QV_ENOMEM;
+  } catch (const std::exception& e) {
+    set_last_error(e.what());
+    return QV_EIO;
+  }
+}
+}  // namespace
+
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+
+void build_index_cpu(const void* base, int dtype, int64_t n, int dim, const qv_build_params& prm,
+                     const std::string& prefix);
+
+}  // namespace qv
+
+extern "C" {
+
+const char* qv_last_error(void) { return qv::g_last_error.c_str(); }
+
+void qv_build_params_default(qv_build_params* p) {
+  if (!p) return;
+  std::memset(p, 0, sizeof(*p));
+  p->R = 64;
+  p->L = 100;
+  p->alpha = 1.2f;
+  p->num_chunks = 32;
+  p->kmeans_iters = 15;
+  p->pq_train_max = 262144;
+  p->seed = 0x5EED5EEDull;
+  p->threads = 0;
+  p->passes = 2;
+}
+
+int qv_build_index_cpu(const void* base, int32_t data_type, int64_t n, int32_t dim,
+                       const qv_build_params* params, const char* out_prefix) {
+  return qv::host_guard([&] {
+    if (!base || !out_prefix || dim <= 0) qv::fail(QV_EINVAL, "bad argument");
+    if (data_type != QV_UINT8 && data_type != QV_FLOAT && data_type != QV_INT8)
+      qv::fail(QV_EINVAL, "bad data type");
+    qv_build_params p;
+    qv_build_params_default(&p);
+    if (params) p = *params;
+    qv::build_index_cpu(base, data_type, n, dim, p, out_prefix);
+  });
+}
+
+int qv_mixture_fill_host(const qv_mixture* m, int64_t first_row, int64_t rows, void* dst) {
+  return qv::host_guard([&] {
+    if (!m || !dst || rows < 0 || m->dim <= 0 || m->num_centers <= 0) qv::fail(QV_EINVAL, "bad argument");
+    if (m->data_type == QV_UINT8) {
+      uint8_t* out = static_cast<uint8_t*>(dst);
+#pragma omp parallel for schedule(static)
+      for (int64_t r = 0; r < rows; r++)
+        for (int32_t j = 0; j < m->dim; j++)
+          out[r * m->dim + j] = qv::mixture_u8(m->seed, m->num_centers, m->dim, m->center_lo,
+                                               m->center_hi, m->sigma, first_row + r, j);
+    } else if (m->data_type == QV_FLOAT) {
+      float* out = static_cast<float*>(dst);
+#pragma omp parallel for schedule(static)
+      for (int64_t r = 0; r < rows; r++) {
+        float* row = out + r * m->dim;
+        double ss = 0.0;
+        for (int32_t j = 0; j < m->dim; j++) {
+          const float v = qv::mixture_f32_raw(m->seed, m->num_centers, m->dim, m->sigma, first_row + r, j);
+          row[j] = v;
+          const double dv = (double)v;
+          ss = ss + dv * dv;
+        }
+        if (m->normalize) {
+          const double inv = 1.0 / std::sqrt(ss);
+          for (int32_t j = 0; j < m->dim; j++) row[j] = (float)((double)row[j] * inv);
+        }
+      }
+    } else {
+      qv::fail(QV_EINVAL, "mixture data_type must be uint8 or float");
+    }
+  });
+}
+
+}  // extern "C"

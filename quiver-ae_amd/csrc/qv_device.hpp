@@ -1,0 +1,212 @@
+// qv_device.hpp -- wave64 building blocks of the CDNA4 search path.
+//
+// One query is served by one 64-lane wavefront.  Lane l owns neighbour l of the
+// node being expanded (R <= 64), so the ADC gather, the candidate sort and the
+// beam merge are register-resident wave operations; the beam lives in LDS
+// between hops and the per-query LUT lives in LDS for the whole query.
+//
+// Candidate keys are 64-bit: (fp32 bits of the PQ distance) << 32 |
+// (id & 0x7fffffff) << 1 | (unvisited ? 1 : 0).  Distances are sums of squares,
+// hence non-negative, so unsigned key order is the reference's (dist, id) order
+// (pair_less, src/quiver/kernel_core/kernel_helpers.cuh:106-114), with a visited
+// copy of an id ordered before an unvisited copy -- the position the reference's
+// merge gives the beam's own entry (kernel_helpers.cuh:331-335).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace qv {
+namespace dev {
+
+constexpr int kWave = 64;
+constexpr uint64_t kPadKey = ~0ull;
+constexpr int kPivots = 256;
+
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+__device__ __forceinline__ uint64_t make_key(float dist, uint32_t id, bool visited) {
+  return ((uint64_t)__float_as_uint(dist) << 32) | ((uint64_t)(id & 0x7fffffffu) << 1) |
+         (visited ? 0ull : 1ull);
+}
+__device__ __forceinline__ uint32_t key_id(uint64_t k) { return ((uint32_t)k) >> 1; }
+__device__ __forceinline__ bool key_unvisited(uint64_t k) { return (k & 1ull) != 0; }
+__device__ __forceinline__ float key_dist(uint64_t k) { return __uint_as_float((uint32_t)(k >> 32)); }
+
+// Sentinel of an empty neighbour slot: (+inf, 0xffffffff - lane), as the
+// reference pads lanes >= degree (kernel_helpers.cuh:273-277).
+__device__ __forceinline__ uint64_t sentinel_key(int lane) {
+  return make_key(__int_as_float(0x7f800000), 0xffffffffu - (uint32_t)lane, false);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  lo = (uint32_t)__shfl_xor((int)lo, m);
+  hi = (uint32_t)__shfl_xor((int)hi, m);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t umin64(uint64_t a, uint64_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a < b ? b : a; }
+
+// Bitonic sort of one key per lane, descending across the wave.
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int k = 2; k <= kWave; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      uint64_t other = shfl_xor64(key, j);
+      bool up = (lane & k) != 0;         // final pass (k = 64): descending
+      bool lower = (lane & j) == 0;
+      key = (lower == up) ? umin64(key, other) : umax64(key, other);
+    }
+  }
+  return key;
+}
+
+// Bitonic merge of P slots (element i = s*64 + lane) into ascending order.
+// Input: slots 0..P-2 ascending (padded with kPadKey), slot P-1 descending.
+template <int P>
+__device__ __forceinline__ void wave_merge_asc(uint64_t (&b)[P]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int half = P / 2; half >= 1; half >>= 1) {
+#pragma unroll
+    for (int s = 0; s < P; s++) {
+      if ((s & half) == 0) {
+        uint64_t lo = umin64(b[s], b[s + half]);
+        uint64_t hi = umax64(b[s], b[s + half]);
+        b[s] = lo;
+        b[s + half] = hi;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = kWave / 2; j > 0; j >>= 1) {
+#pragma unroll
+    for (int s = 0; s < P; s++) {
+      uint64_t other = shfl_xor64(b[s], j);
+      bool lower = (lane & j) == 0;
+      b[s] = lower ? umin64(b[s], other) : umax64(b[s], other);
+    }
+  }
+}
+
+// Per-query LUT in LDS: PQSearchData::init_query (src/shared/index/
+// pq_device.cuh:9-36).  Chunks are contiguous dimension ranges, so each
+// (chunk, pivot) cell accumulates its dimensions in ascending order, exactly as
+// the reference's i-ordered loop does; the fused multiply-add matches nvcc's
+// contraction of `dist_vec[..] += dist * dist`.  Lane l owns pivots 4l..4l+3.
+__device__ __forceinline__ void build_lut_lds(const float* __restrict__ qc_lds,
+                                              const float* __restrict__ pivots_t,
+                                              const int32_t* __restrict__ chunk_off,
+                                              int num_chunks, float* __restrict__ lut) {
+  const int lane = lane_id();
+  for (int m = 0; m < num_chunks; m++) {
+    const int o0 = chunk_off[m], o1 = chunk_off[m + 1];
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = o0; i < o1; i++) {
+      const float qi = qc_lds[i];
+      const float4 p = reinterpret_cast<const float4*>(pivots_t + (size_t)i * kPivots)[lane];
+      float d0 = qi - p.x, d1 = qi - p.y, d2 = qi - p.z, d3 = qi - p.w;
+      acc.x = __fmaf_rn(d0, d0, acc.x);
+      acc.y = __fmaf_rn(d1, d1, acc.y);
+      acc.z = __fmaf_rn(d2, d2, acc.z);
+      acc.w = __fmaf_rn(d3, d3, acc.w);
+    }
+    reinterpret_cast<float4*>(lut + m * kPivots)[lane] = acc;
+  }
+}
+
+// Sequential fp32 ADC of one code row against an LDS LUT
+// (kernel_helpers.cuh:280-285): dist = 0; dist += LUT[j][code_j] for j = 0..M-1.
+template <int MC>
+__device__ __forceinline__ float adc_row(const uint8_t* __restrict__ row,
+                                         const float* __restrict__ lut, int M) {
+  float dist = 0.f;
+  if constexpr (MC > 0 && MC % 16 == 0) {
+    const uint4* r4 = reinterpret_cast<const uint4*>(row);
+    uint32_t w[MC / 4];
+#pragma unroll
+    for (int t = 0; t < MC / 16; t++) {
+      const uint4 v = r4[t];
+      w[4 * t + 0] = v.x;
+      w[4 * t + 1] = v.y;
+      w[4 * t + 2] = v.z;
+      w[4 * t + 3] = v.w;
+    }
+#pragma unroll
+    for (int j = 0; j < MC; j++) {
+      uint32_t c = (w[j >> 2] >> ((j & 3) * 8)) & 0xffu;
+      dist += lut[j * kPivots + (int)c];
+    }
+  } else {
+    (void)MC;
+    if ((M & 3) == 0) {
+      const uint32_t* r = reinterpret_cast<const uint32_t*>(row);
+      for (int t = 0; t < M / 4; t++) {
+        uint32_t w = r[t];
+#pragma unroll
+        for (int b = 0; b < 4; b++) dist += lut[(4 * t + b) * kPivots + (int)((w >> (8 * b)) & 0xffu)];
+      }
+    } else {
+      for (int j = 0; j < M; j++) dist += lut[j * kPivots + (int)row[j]];
+    }
+  }
+  return dist;
+}
+
+template <class T>
+__device__ __forceinline__ float elem_to_float(const uint8_t* rec, int i) {
+  return (float)reinterpret_cast<const T*>(rec)[i];
+}
+
+// Exact squared L2 in the reference's order: square_sum_32
+// (src/shared/common/gpu_primitives.cuh:26-44).  Lanes 0..31 accumulate the
+// dimensions l, l+32, ... with a fused multiply-add, then a shuffle-down tree
+// over 32 lanes; every lane receives lane 0's value.
+template <class T>
+__device__ __forceinline__ float exact_l2_ref(const uint8_t* __restrict__ rec,
+                                              const float* __restrict__ qu_lds, int dim) {
+  const int lane = lane_id();
+  float val = 0.f;
+  if (lane < 32) {
+    for (int i = lane; i < dim; i += 32) {
+      float diff = qu_lds[i] - elem_to_float<T>(rec, i);
+      val = __fmaf_rn(diff, diff, val);
+    }
+  }
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) val += __shfl_down(val, off, 32);
+  return __shfl(val, 0);
+}
+
+// Stable top-k insert (retset_push_topk_le32, kernel_helpers.cuh:65-104,
+// generalised to k <= 64): lane i < k holds entry i; the value goes after every
+// entry <= value; the caller applies the fc < k || value < D[k-1] guard.
+__device__ __forceinline__ void topk_insert(float& td, int32_t& ti, int& fc, int k,
+                                            float value, int32_t id) {
+  const int lane = lane_id();
+  uint64_t le = __ballot(lane < fc && td <= value);
+  int pos = __popcll(le);
+  int ns = fc < k ? fc + 1 : k;
+  float pd = __shfl_up(td, 1);
+  int32_t pi = __shfl_up(ti, 1);
+  if (lane < ns) {
+    if (lane == pos) {
+      td = value;
+      ti = id;
+    } else if (lane > pos) {
+      td = pd;
+      ti = pi;
+    }
+  }
+  fc = ns;
+}
+
+// Wall clock at 100 MHz (s_memrealtime).
+__device__ __forceinline__ uint64_t wall_ticks() { return wall_clock64(); }
+
+}  // namespace dev
+}  // namespace qv

@@ -1,0 +1,268 @@
+// qv_formats.cpp -- readers and writers of the on-disk formats the reference
+// consumes: the DiskANN disk index (header page + 4 KB node pages), the PQ pivot
+// table and code file, and the int32-headed .bin arrays.
+#include <algorithm>
+#include <cerrno>
+#include <cstring>
+#include <filesystem>
+#include <fstream>
+
+#include "qv_common.hpp"
+
+namespace fs = std::filesystem;
+
+namespace qv {
+
+int parse_data_type(const std::string& s) {
+  // bin/common/cli_shared.hpp:61-74 plus the Python spelling "float32"
+  // (python/quiver/index.py:19-24).
+  if (s == "uint8") return QV_UINT8;
+  if (s == "float" || s == "float32") return QV_FLOAT;
+  if (s == "int8") return QV_INT8;
+  fail(QV_EINVAL, "Unsupported data type '" + s + "'. Expected one of: uint8, int8, float");
+}
+
+const char* data_type_name(int t) {
+  switch (t) {
+    case QV_UINT8: return "uint8";
+    case QV_INT8: return "int8";
+    case QV_FLOAT: return "float";
+  }
+  return "unknown";
+}
+
+// bin/common/metadata.hpp:15-72.  The element size of uint8 and int8 data is 1.
+Layout parse_diskann_metadata(const std::string& path, int data_type) {
+  std::ifstream in(path, std::ios::binary);
+  if (!in.is_open()) fail(QV_EIO, "Failed to open file " + path);
+  uint32_t nr = 0, nc = 0;
+  uint64_t v[8] = {};
+  in.read(reinterpret_cast<char*>(&nr), 4);
+  in.read(reinterpret_cast<char*>(&nc), 4);
+  in.read(reinterpret_cast<char*>(v), sizeof(v));
+  if (!in) fail(QV_EIO, "Truncated DiskANN header in " + path);
+  Layout lay;
+  lay.data_type = data_type;
+  const uint64_t esz = (uint64_t)elem_size(data_type);
+  lay.num_data = (int64_t)v[0];
+  lay.num_dims = (int64_t)v[1];
+  lay.enter_point = (int64_t)v[2];
+  const uint64_t max_node_len = v[3];
+  lay.nodes_per_page = (int64_t)v[4];
+  if (lay.num_data <= 0 || lay.num_dims <= 0 || lay.nodes_per_page <= 0 ||
+      max_node_len <= v[1] * esz + 4 || max_node_len * v[4] > (uint64_t)kPageSize)
+    fail(QV_EIO, "Malformed DiskANN header in " + path);
+  lay.max_m0 = (int64_t)((max_node_len - v[1] * esz) / sizeof(uint32_t)) - 1;
+  lay.num_pages = (lay.num_data + lay.nodes_per_page - 1) / lay.nodes_per_page;
+  lay.node_size = (int64_t)max_node_len;
+  lay.data_size = lay.num_dims * (int64_t)esz;
+  if (lay.enter_point < 0 || lay.enter_point >= lay.num_data)
+    fail(QV_EINDEX, "Medoid out of range in " + path);
+  return lay;
+}
+
+static std::vector<std::string> suffix_matches(const std::string& dir,
+                                               const std::string& suffix) {
+  std::vector<std::string> out;
+  for (const auto& e : fs::directory_iterator(dir)) {
+    if (!fs::is_regular_file(e.path())) continue;
+    const std::string name = e.path().filename().string();
+    if (name.size() >= suffix.size() &&
+        name.compare(name.size() - suffix.size(), suffix.size(), suffix) == 0)
+      out.push_back(e.path().string());
+  }
+  std::sort(out.begin(), out.end());
+  return out;
+}
+
+static std::string join(const std::vector<std::string>& v) {
+  std::string s;
+  for (size_t i = 0; i < v.size(); i++) s += (i ? ", " : "") + v[i];
+  return s;
+}
+
+// bin/common/index_discovery.hpp:57-78
+std::string find_index_file(const std::string& dir) {
+  if (!fs::is_directory(dir))
+    fail(QV_EIO, "--index-dir '" + dir + "' does not exist or is not a directory");
+  auto m = suffix_matches(dir, "_disk.index");
+  if (m.size() == 1) return m.front();
+  if (m.size() > 1)
+    fail(QV_EIO, "Multiple *_disk.index candidates found in " + dir + ": " + join(m));
+  fs::path fb = fs::path(dir) / "disk.index";
+  if (fs::exists(fb) && fs::is_regular_file(fb)) return fb.string();
+  fail(QV_EIO, "No *_disk.index or disk.index found in " + dir);
+}
+
+// bin/common/index_discovery.hpp:80-103
+std::string find_pq_prefix(const std::string& dir) {
+  if (!fs::is_directory(dir))
+    fail(QV_EIO, "--index-dir '" + dir + "' does not exist or is not a directory");
+  auto m = suffix_matches(dir, "_pq_pivots.bin");
+  if (m.size() == 1) return m.front().substr(0, m.front().size() - std::string("_pivots.bin").size());
+  if (m.size() > 1)
+    fail(QV_EIO, "Multiple *_pq_pivots.bin candidates found in " + dir + ": " + join(m));
+  fs::path fb = fs::path(dir) / "pq";
+  if (fs::exists(fb.string() + "_pivots.bin")) return fb.string();
+  fail(QV_EIO, "No PQ pivot files found in " + dir);
+}
+
+// read_bin (src/shared/index/pq_search.cu:179-194): int32 rows, int32 cols, data.
+template <class T>
+static std::vector<T> read_bin_at(const std::string& path, size_t offset, int& nr, int& nc) {
+  std::ifstream in(path, std::ios::binary);
+  if (!in.is_open()) fail(QV_EIO, "Cannot open file: " + path);
+  in.seekg((std::streamoff)offset, std::ios::beg);
+  in.read(reinterpret_cast<char*>(&nr), 4);
+  in.read(reinterpret_cast<char*>(&nc), 4);
+  if (!in || nr < 0 || nc < 0) fail(QV_EIO, "Bad bin header in " + path);
+  std::vector<T> data((size_t)nr * (size_t)nc);
+  in.read(reinterpret_cast<char*>(data.data()), (std::streamsize)(sizeof(T) * data.size()));
+  if (!in) fail(QV_EIO, "Truncated bin section in " + path);
+  return data;
+}
+
+// PQSearch::read_data (src/shared/index/pq_search.cu:62-114).
+void read_pq_tables(const std::string& pivots_file, const std::string& codes_file,
+                    PQTables& t) {
+  int nr = 0, nc = 0;
+  t.codes = read_bin_at<uint8_t>(codes_file, 0, nr, nc);
+  t.num_pts = nr;
+  t.num_chunks = nc;
+  auto offs = read_bin_at<uint64_t>(pivots_file, 0, nr, nc);
+  if (!((nr == 4 || nr == 5) && nc == 1)) fail(QV_EIO, "Bad PQ metadata table in " + pivots_file);
+  const int chunk_index = nr == 5 ? 3 : 2;
+  t.pivots = read_bin_at<float>(pivots_file, offs[0], nr, nc);
+  if (nr != kNumPivots) fail(QV_EIO, "PQ pivots must have 256 rows in " + pivots_file);
+  t.dim = nc;
+  t.pivots_t.assign((size_t)t.dim * kNumPivots, 0.f);
+  for (int i = 0; i < kNumPivots; i++)
+    for (int j = 0; j < t.dim; j++) t.pivots_t[(size_t)j * kNumPivots + i] = t.pivots[(size_t)i * t.dim + j];
+  t.centroid = read_bin_at<float>(pivots_file, offs[1], nr, nc);
+  if (nr != t.dim || nc != 1) fail(QV_EIO, "PQ centroid shape mismatch in " + pivots_file);
+  auto co = read_bin_at<int32_t>(pivots_file, offs[chunk_index], nr, nc);
+  if (nr != t.num_chunks + 1 || nc != 1) fail(QV_EIO, "PQ chunk offsets shape mismatch in " + pivots_file);
+  // chunk_id[j] = i for j in [co[i], co[i+1]) (pq_search.cu:103-109).  Every
+  // dimension must belong to a chunk; the reference would index LUT row -1.
+  if (co[0] != 0 || co[t.num_chunks] != t.dim)
+    fail(QV_EIO, "PQ chunk offsets must cover [0, dim) in " + pivots_file);
+  t.chunk_id.assign((size_t)t.dim, -1);
+  for (int i = 0; i < t.num_chunks; i++) {
+    if (co[i + 1] < co[i]) fail(QV_EIO, "PQ chunk offsets must be non-decreasing in " + pivots_file);
+    for (int j = co[i]; j < co[i + 1]; j++) t.chunk_id[(size_t)j] = i;
+  }
+  t.chunk_offsets = co;
+}
+
+// MemLoaderSync::load_heap (src/shared/io/mem_loader.cpp:28-44): pages
+// 1..num_pages (page 0 is the header) in order.
+void read_index_pages(const std::string& path, int64_t num_pages, uint8_t* dst) {
+  FILE* f = std::fopen(path.c_str(), "rb");
+  if (!f) fail(QV_EIO, "Failed to open Mem Index: " + path);
+  if (std::fseek(f, kPageSize, SEEK_SET) != 0) {
+    std::fclose(f);
+    fail(QV_EIO, "Failed to seek Mem Index: " + path);
+  }
+  int64_t got = (int64_t)std::fread(dst, kPageSize, (size_t)num_pages, f);
+  std::fclose(f);
+  if (got != num_pages)
+    fail(QV_EIO, "Mem Index Load FAILED: " + std::to_string(got) + " pages read from " + path);
+}
+
+// Writer for the same layout: header page (save_bin of nine u64 metadata
+// values: nnodes, ndims, medoid, max_node_len, nnodes_per_sector, frozen count,
+// frozen id, reorder flag, file size) followed by node pages with records
+// [vector | u32 degree | u32 neighbours[R]].
+void write_diskann_index(const std::string& path, const Layout& lay, const void* base,
+                         const std::vector<uint32_t>& adj, const std::vector<uint32_t>& deg) {
+  std::ofstream out(path, std::ios::binary | std::ios::trunc);
+  if (!out.is_open()) fail(QV_EIO, "Failed to open " + path + " for writing");
+  const int64_t R = lay.max_m0;
+  const int64_t file_size = (lay.num_pages + 1) * kPageSize;
+  std::vector<uint8_t> page((size_t)kPageSize, 0);
+  uint32_t hdr[2] = {9, 1};
+  uint64_t meta[9] = {(uint64_t)lay.num_data, (uint64_t)lay.num_dims, (uint64_t)lay.enter_point,
+                      (uint64_t)lay.node_size, (uint64_t)lay.nodes_per_page, 0, 0, 0,
+                      (uint64_t)file_size};
+  std::memcpy(page.data(), hdr, sizeof(hdr));
+  std::memcpy(page.data() + sizeof(hdr), meta, sizeof(meta));
+  out.write(reinterpret_cast<const char*>(page.data()), kPageSize);
+  const uint8_t* b = static_cast<const uint8_t*>(base);
+  for (int64_t p = 0; p < lay.num_pages; p++) {
+    std::fill(page.begin(), page.end(), 0);
+    for (int64_t k = 0; k < lay.nodes_per_page; k++) {
+      const int64_t v = p * lay.nodes_per_page + k;
+      if (v >= lay.num_data) break;
+      uint8_t* rec = page.data() + k * lay.node_size;
+      std::memcpy(rec, b + v * lay.data_size, (size_t)lay.data_size);
+      uint32_t* nb = reinterpret_cast<uint32_t*>(rec + lay.data_size);
+      nb[0] = deg[(size_t)v];
+      std::memcpy(nb + 1, adj.data() + (size_t)v * R, sizeof(uint32_t) * deg[(size_t)v]);
+    }
+    out.write(reinterpret_cast<const char*>(page.data()), kPageSize);
+  }
+  if (!out) fail(QV_EIO, "Failed writing " + path);
+}
+
+// DiskANN pivot file: a 4 KB metadata block holding four u64 offsets
+// (pivots, centroid, chunk offsets, end), then the three bin sections.
+void write_pq_tables(const std::string& pivots_file, const std::string& codes_file,
+                     const PQTables& t) {
+  {
+    std::ofstream out(pivots_file, std::ios::binary | std::ios::trunc);
+    if (!out.is_open()) fail(QV_EIO, "Failed to open " + pivots_file + " for writing");
+    const uint64_t o0 = 4096;
+    const uint64_t o1 = o0 + 8 + 4ull * kNumPivots * (uint64_t)t.dim;
+    const uint64_t o2 = o1 + 8 + 4ull * (uint64_t)t.dim;
+    const uint64_t o3 = o2 + 8 + 4ull * (uint64_t)(t.num_chunks + 1);
+    std::vector<uint8_t> meta(4096, 0);
+    int32_t h[2] = {4, 1};
+    uint64_t offs[4] = {o0, o1, o2, o3};
+    std::memcpy(meta.data(), h, 8);
+    std::memcpy(meta.data() + 8, offs, sizeof(offs));
+    out.write(reinterpret_cast<const char*>(meta.data()), (std::streamsize)meta.size());
+    int32_t hp[2] = {kNumPivots, t.dim};
+    out.write(reinterpret_cast<const char*>(hp), 8);
+    out.write(reinterpret_cast<const char*>(t.pivots.data()), (std::streamsize)(4 * t.pivots.size()));
+    int32_t hc[2] = {t.dim, 1};
+    out.write(reinterpret_cast<const char*>(hc), 8);
+    out.write(reinterpret_cast<const char*>(t.centroid.data()), (std::streamsize)(4 * t.centroid.size()));
+    int32_t ho[2] = {t.num_chunks + 1, 1};
+    out.write(reinterpret_cast<const char*>(ho), 8);
+    out.write(reinterpret_cast<const char*>(t.chunk_offsets.data()), 4 * (std::streamsize)(t.num_chunks + 1));
+    if (!out) fail(QV_EIO, "Failed writing " + pivots_file);
+  }
+  write_typed_bin<uint8_t>(codes_file, t.codes.data(), t.num_pts, t.num_chunks);
+}
+
+template <class T>
+std::vector<T> read_typed_bin(const std::string& path, int64_t& n, int64_t& d) {
+  int nr = 0, nc = 0;
+  auto v = read_bin_at<T>(path, 0, nr, nc);
+  n = nr;
+  d = nc;
+  return v;
+}
+
+// write_typed_bin (bin/common/data_io.hpp:116-140)
+template <class T>
+void write_typed_bin(const std::string& path, const T* data, int64_t n, int64_t d) {
+  if (n > INT32_MAX || d > INT32_MAX) fail(QV_EINVAL, "Binary dimensions exceed int32 range");
+  std::ofstream out(path, std::ios::binary | std::ios::trunc);
+  if (!out.is_open()) fail(QV_EIO, "Failed to open binary result file " + path);
+  int32_t h[2] = {(int32_t)n, (int32_t)d};
+  out.write(reinterpret_cast<const char*>(h), 8);
+  out.write(reinterpret_cast<const char*>(data), (std::streamsize)(sizeof(T) * (size_t)n * (size_t)d));
+  if (!out) fail(QV_EIO, "Failed to write binary result file " + path);
+}
+
+template std::vector<float> read_typed_bin<float>(const std::string&, int64_t&, int64_t&);
+template std::vector<uint8_t> read_typed_bin<uint8_t>(const std::string&, int64_t&, int64_t&);
+template std::vector<int8_t> read_typed_bin<int8_t>(const std::string&, int64_t&, int64_t&);
+template std::vector<int32_t> read_typed_bin<int32_t>(const std::string&, int64_t&, int64_t&);
+template void write_typed_bin<float>(const std::string&, const float*, int64_t, int64_t);
+template void write_typed_bin<uint8_t>(const std::string&, const uint8_t*, int64_t, int64_t);
+template void write_typed_bin<int8_t>(const std::string&, const int8_t*, int64_t, int64_t);
+template void write_typed_bin<int32_t>(const std::string&, const int32_t*, int64_t, int64_t);
+
+}  // namespace qv

@@ -1,0 +1,932 @@
+// qv_search.hip -- persistent beam-search kernel for CDNA4 and its host driver.
+//
+// Reference path (ruc-system/quiver-ae): persistent_search_kernel
+// (src/quiver/kernel_core/kernel_q1.cuh:20-757) driven by run_persistent_search
+// (src/quiver/search.cu:357-1361).  Differences by design:
+//   * one 64-lane wavefront per query; workgroups of one wave; the LUT, the
+//     query and the beam live in LDS; neighbour lists, vectors and PQ codes are
+//     read straight from HBM (no CPU poll threads, no 4 KB page copies);
+//   * candidate sort + beam merge are register bitonic networks over 64-bit
+//     keys instead of merge-path rounds with block barriers;
+//   * a device work queue (atomic ticket) gated by a host-written feed count,
+//     completion published to a host ring so per-query latency is exact.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <numeric>
+#include <thread>
+#include <vector>
+
+#include "qv_common.hpp"
+#include "qv_device.hpp"
+#include "qv_hip_util.hpp"
+
+using namespace qv;
+using namespace qv::dev;
+
+namespace {
+
+struct SearchArgs {
+  // index (HBM)
+  const uint8_t* pages;
+  const uint8_t* codes;
+  const float* centroid;
+  const float* pivots_t;
+  const int32_t* chunk_off;
+  int64_t num_points;
+  int64_t nodes_per_page;
+  int64_t node_size;
+  int64_t data_size;
+  int32_t dim;
+  int32_t num_chunks;
+  int32_t max_m;
+  int32_t medoid;
+  // queries / params
+  const float* queries;
+  int32_t nq;
+  int32_t topk;
+  int32_t ef;
+  int32_t pipe_w;
+  int32_t early_exit;
+  int32_t warmup;
+  int32_t patience;
+  // outputs (device)
+  int32_t* out_ids;
+  float* out_dists;
+  int32_t* out_found;
+  int32_t* out_hops;
+  int32_t* out_stopped;
+  uint64_t* t_start;
+  uint64_t* t_end;
+  // dispatch
+  int32_t* counters;               // [0] next ticket, [1] done count, [2] error bits
+  const int32_t* feed_count;       // host-coherent, may be null (then nq)
+  const int32_t* terminate;        // host-coherent, may be null
+  int32_t* ring;                   // host-coherent completion ring, may be null
+  uint64_t spin_limit_ticks;       // watchdog on feed waits (100 MHz ticks)
+};
+
+enum : int32_t { kErrSpinTimeout = 1 };
+
+// Dynamic LDS carve-up shared by the kernel and its launcher.
+struct LdsPlan {
+  int lut_off, qc_off, qu_off, beam_off, lanes_off, total;
+};
+
+__host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int P) {
+  LdsPlan p;
+  p.lut_off = 0;
+  p.qc_off = p.lut_off + num_chunks * kPivots * 4;
+  int dpad = (dim + 3) & ~3;
+  p.qu_off = p.qc_off + dpad * 4;
+  p.beam_off = (p.qu_off + dpad * 4 + 7) & ~7;
+  p.lanes_off = p.beam_off + (P - 1) * kWave * 8;
+  p.total = p.lanes_off + 16 * 4;
+  return p;
+}
+
+template <class T, int P, int MC>
+struct Query {
+  const SearchArgs& a;
+  float* lut;
+  float* qc;
+  float* qu;
+  uint64_t* beam;
+  int sz;        // beam size (ctx.size)
+  float td;      // top-k entry of this lane
+  int32_t ti;
+  int fc;        // found count
+
+  __device__ Query(const SearchArgs& args, char* smem)
+      : a(args), sz(0), td(__int_as_float(0x7f800000)), ti(-1), fc(0) {
+    LdsPlan pl = lds_plan(a.num_chunks, a.dim, P);
+    lut = reinterpret_cast<float*>(smem + pl.lut_off);
+    qc = reinterpret_cast<float*>(smem + pl.qc_off);
+    qu = reinterpret_cast<float*>(smem + pl.qu_off);
+    beam = reinterpret_cast<uint64_t*>(smem + pl.beam_off);
+  }
+
+  __device__ __forceinline__ const uint8_t* record(int32_t v) const {
+    const int64_t page = (int64_t)v / a.nodes_per_page;
+    const int64_t slot = (int64_t)v - page * a.nodes_per_page;
+    return a.pages + page * 4096 + slot * a.node_size;
+  }
+
+  // One expansion of node v: persistent_merge_data (kernel_helpers.cuh:232-357)
+  // followed by persistent_visit_select_dualwarp (kernel_helpers.cuh:422-489).
+  // Returns the selected next node or -1.
+  __device__ int32_t hop(int32_t v) {
+    const int lane = lane_id();
+    const uint8_t* rec = record(v);
+    const uint32_t* rec32 = reinterpret_cast<const uint32_t*>(rec + a.data_size);
+    const int deg = (int)rec32[0];
+    const bool has = lane < deg;
+    const uint32_t nbr = has ? rec32[1 + lane] : 0u;
+
+    // ADC gather-sum over the neighbour's code row (LUT in LDS).
+    uint64_t nkey = sentinel_key(lane);
+    if (has) {
+      const float d = adc_row<MC>(a.codes + (int64_t)nbr * a.num_chunks, lut, a.num_chunks);
+      nkey = make_key(d, nbr, false);
+    }
+
+    // Exact distance of v and the top-k insert (the reference's second warp).
+    const float e = exact_l2_ref<T>(rec, qu, a.dim);
+    const float dlast = __shfl(td, a.topk - 1);
+    if (fc < a.topk || e < dlast) topk_insert(td, ti, fc, a.topk, e, v);
+
+    // Sort the new candidates (descending) and merge with the beam.
+    nkey = wave_sort_desc(nkey);
+    uint64_t b[P];
+#pragma unroll
+    for (int s = 0; s < P - 1; s++) {
+      const int i = s * kWave + lane;
+      b[s] = i < sz ? beam[i] : kPadKey;
+    }
+    b[P - 1] = nkey;
+    wave_merge_asc<P>(b);
+
+    // Keep min(sz + deg, 2 ef) (kernel_helpers.cuh:350), drop entries equal to
+    // their predecessor (:440-455), truncate to ef and take the first unvisited
+    // entry (:456-472).
+    const int keep_n = min(sz + deg, 2 * a.ef);
+    int base = 0;
+    uint32_t prev_id = 0xffffffffu;
+    int sel_pos = -1;
+    uint64_t sel_key = 0;
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+    for (int s = 0; s < P; s++) {
+      const int i = s * kWave + lane;
+      const uint32_t id = key_id(b[s]);
+      uint32_t pid = (uint32_t)__shfl_up((int)id, 1);
+      if (lane == 0) pid = prev_id;
+      const bool valid = i < keep_n;
+      const bool keep = valid && !(i > 0 && id == pid);
+      const uint64_t km = __ballot(keep);
+      const int pos = base + __popcll(km & lt_mask);
+      if (keep && pos < a.ef) beam[pos] = b[s];
+      if (sel_pos < 0) {
+        const uint64_t cm = __ballot(keep && pos < a.ef && key_unvisited(b[s]));
+        if (cm) {
+          const int l = __ffsll((long long)cm) - 1;
+          sel_pos = __shfl(pos, l);
+          sel_key = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(b[s] >> 32), l) << 32) |
+                    (uint32_t)__shfl((int)(uint32_t)b[s], l);
+        }
+      }
+      base += __popcll(km);
+      prev_id = (uint32_t)__shfl((int)id, kWave - 1);
+    }
+    sz = min(base, a.ef);
+    int32_t next = -1;
+    if (sel_pos >= 0) {
+      if (lane == 0) beam[sel_pos] = sel_key & ~1ull;
+      next = (int32_t)key_id(sel_key);
+    }
+    __syncthreads();
+    return next;
+  }
+
+  // persistent_select_next_no_compact (kernel_helpers.cuh:491-518).
+  __device__ int32_t select_next_no_compact() {
+    const int lane = lane_id();
+    const int n = min(sz, a.ef);
+    sz = n;
+    if (n == 0) return -1;
+#pragma unroll
+    for (int s = 0; s < P - 1; s++) {
+      const int i = s * kWave + lane;
+      const uint64_t k = i < n ? beam[i] : 0ull;
+      const uint64_t cm = __ballot(i < n && key_unvisited(k));
+      if (cm) {
+        const int l = __ffsll((long long)cm) - 1;
+        const int pos = s * kWave + l;
+        const uint64_t sk = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(k >> 32), l) << 32) |
+                            (uint32_t)__shfl((int)(uint32_t)k, l);
+        if (lane == 0) beam[pos] = sk & ~1ull;
+        __syncthreads();
+        return (int32_t)key_id(sk);
+      }
+    }
+    return -1;
+  }
+};
+
+// gpruning bookkeeping (kernel_q1.cuh:294-315, 524-545).
+struct GPrune {
+  int no_improve = 0, last_fc = 0;
+  float last_top1 = __int_as_float(0x7f800000), last_topk = __int_as_float(0x7f800000);
+};
+
+template <class T, int P, int MC>
+__global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  const int lane = lane_id();
+  LdsPlan pl = lds_plan(a.num_chunks, a.dim, P);
+  int32_t* lane_node = reinterpret_cast<int32_t*>(smem + pl.lanes_off);
+
+  while (true) {
+    // ---- acquire (StreamingDispatch, src/quiver/kernel_core/policies/dispatch.cuh:39-79)
+    int32_t qid = -1;
+    if (lane == 0) {
+      qid = atomicAdd(&a.counters[0], 1);
+      if (qid >= a.nq) {
+        qid = -1;
+      } else if (a.terminate &&
+                 __hip_atomic_load(a.terminate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
+        qid = -1;
+      } else if (a.feed_count) {
+        const uint64_t t0 = wall_ticks();
+        while (qid >= __hip_atomic_load(a.feed_count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM)) {
+          if (a.terminate &&
+              __hip_atomic_load(a.terminate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
+            qid = -1;
+            break;
+          }
+          if (wall_ticks() - t0 > a.spin_limit_ticks) {
+            atomicOr(&a.counters[2], kErrSpinTimeout);
+            qid = -1;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(4);
+        }
+      }
+    }
+    qid = __shfl(qid, 0);
+    if (qid < 0) break;
+    if (a.t_start && lane == 0) a.t_start[qid] = wall_ticks();
+
+    Query<T, P, MC> Q(a, smem);
+    // ---- query into LDS: q - mu for the LUT, fl(fl(q - mu) + mu) for the exact
+    // distance (pq_device.cuh:18-20, 33-35).
+    const float* q = a.queries + (int64_t)qid * a.dim;
+    for (int i = lane; i < a.dim; i += kWave) {
+      const float c = q[i] - a.centroid[i];
+      Q.qc[i] = c;
+      Q.qu[i] = c + a.centroid[i];
+    }
+    __syncthreads();
+    build_lut_lds(Q.qc, a.pivots_t, a.chunk_off, a.num_chunks, Q.lut);
+    __syncthreads();
+
+    GPrune g;
+    int step = 0;
+    bool stop = false;
+    const bool gpr = a.early_exit == QV_EXIT_GPRUNING;
+    auto check = [&]() -> bool {
+      const float top1 = __shfl(Q.td, 0);
+      const float topk = __shfl(Q.td, a.topk - 1);
+      const bool improved = Q.fc > g.last_fc || top1 < g.last_top1 || topk < g.last_topk;
+      if (step < a.warmup) g.no_improve = 0;
+      else g.no_improve = improved ? 0 : g.no_improve + 1;
+      g.last_fc = Q.fc;
+      g.last_top1 = top1;
+      g.last_topk = topk;
+      return gpr && step >= a.warmup && a.patience > 0 && g.no_improve >= a.patience;
+    };
+
+    // ---- boot (kernel_q1.cuh:199-397)
+    int32_t first = Q.hop(a.medoid);
+    step = 1;
+    if (check()) {
+      stop = true;
+      first = -1;
+    }
+    const int W = a.pipe_w;
+    uint32_t ready = 0;
+    if (lane == 0) lane_node[0] = first;
+    for (int w = 1; w < W; w++) {
+      const int32_t nx = Q.select_next_no_compact();
+      if (lane == 0) lane_node[w] = nx;
+    }
+    __syncthreads();
+    if (!stop) {
+      for (int w = 0; w < W; w++)
+        if (lane_node[w] != -1) ready |= 1u << w;
+    }
+
+    // ---- pipe loop, every issued lane served at once (kernel_q1.cuh:407-670)
+    while (!stop && ready) {
+      const uint32_t cur = ready;
+      for (int w = 0; w < W; w++) {
+        if (!(cur & (1u << w))) continue;
+        const int32_t v = lane_node[w];
+        int32_t nx = Q.hop(v);
+        ++step;
+        if (check()) {
+          stop = true;
+          nx = -1;
+        }
+        __syncthreads();
+        if (lane == 0) lane_node[w] = nx;
+        __syncthreads();
+      }
+      if (stop) break;
+      for (int w = 0; w < W; w++) {
+        if (cur & (1u << w)) continue;
+        const int32_t nx = Q.select_next_no_compact();
+        if (lane == 0) lane_node[w] = nx;
+      }
+      __syncthreads();
+      ready = 0;
+      for (int w = 0; w < W; w++)
+        if (lane_node[w] != -1) ready |= 1u << w;
+    }
+
+    // ---- finish (kernel_q1.cuh:684-704)
+    if (lane < a.topk) {
+      a.out_ids[(int64_t)qid * a.topk + lane] = Q.ti;
+      a.out_dists[(int64_t)qid * a.topk + lane] = Q.td;
+    }
+    if (lane == 0) {
+      if (a.out_found) a.out_found[qid] = Q.fc;
+      if (a.out_hops) a.out_hops[qid] = step;
+      if (a.out_stopped) a.out_stopped[qid] = stop ? 1 : 0;
+      if (a.t_end) a.t_end[qid] = wall_ticks();
+      atomicAdd(&a.counters[1], 1);
+      if (a.ring) {
+        const int32_t pos = atomicAdd(&a.counters[3], 1);
+        __hip_atomic_store(&a.ring[pos], qid + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Graph check run once at open: degree <= R, neighbour ids < n, no duplicate id
+// inside one adjacency list (the reference's merge-path sort assumes distinct
+// keys, kernel_helpers.cuh:300-329).  One wave per node.
+__global__ __launch_bounds__(256) void validate_kernel(const uint8_t* pages, int64_t n,
+                                                       int64_t npp, int64_t node_size,
+                                                       int64_t data_size, int R,
+                                                       int32_t* err, int64_t* first_bad) {
+  const int lane = lane_id();
+  const int64_t waves = (int64_t)gridDim.x * (blockDim.x / kWave);
+  for (int64_t v = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave; v < n;
+       v += waves) {
+    const int64_t page = v / npp;
+    const uint8_t* rec = pages + page * 4096 + (v - page * npp) * node_size;
+    const uint32_t* r32 = reinterpret_cast<const uint32_t*>(rec + data_size);
+    const uint32_t deg = r32[0];
+    int32_t bits = 0;
+    if (deg > (uint32_t)R) bits |= 1;
+    const uint32_t lim = deg < (uint32_t)R ? deg : (uint32_t)R;
+    const bool has = (uint32_t)lane < lim;
+    const uint32_t nb = has ? r32[1 + lane] : 0u;
+    if (has && (int64_t)nb >= n) bits |= 2;
+    uint64_t key = has ? (uint64_t)nb : ((1ull << 32) + (uint64_t)lane);
+    key = wave_sort_desc(key);
+    const uint64_t up = (uint64_t)__shfl_up((long long)key, 1);
+    if (lane > 0 && up == key) bits |= 4;
+    const uint64_t any = __ballot(bits != 0);
+    if (any) {
+      int32_t all = bits;
+      for (int off = 32; off > 0; off >>= 1) all |= __shfl_xor(all, off);
+      if (lane == 0) {
+        atomicOr(err, all);
+        atomicMin(reinterpret_cast<unsigned long long*>(first_bad), (unsigned long long)v);
+      }
+    }
+  }
+}
+
+using KernelFn = void (*)(SearchArgs);
+
+template <class T, int P>
+KernelFn pick_mc(int M) {
+  if (M == 32) return search_kernel<T, P, 32>;
+  if (M == 48) return search_kernel<T, P, 48>;
+  return search_kernel<T, P, 0>;
+}
+
+template <class T>
+KernelFn pick_p(int P, int M) {
+  if (P == 2) return pick_mc<T, 2>(M);
+  if (P == 4) return pick_mc<T, 4>(M);
+  return pick_mc<T, 8>(M);
+}
+
+KernelFn pick_kernel(int dtype, int P, int M) {
+  if (dtype == QV_UINT8) return pick_p<uint8_t>(P, M);
+  if (dtype == QV_INT8) return pick_p<int8_t>(P, M);
+  return pick_p<float>(P, M);
+}
+
+int merge_slots(int ef) { return ef <= 64 ? 2 : (ef <= 192 ? 4 : 8); }
+
+}  // namespace
+
+// ============================================================== host side ===
+
+struct qv_index {
+  int device = 0;
+  Layout lay;
+  int M = 0;
+  uint8_t* d_pages = nullptr;
+  uint8_t* d_codes = nullptr;
+  float* d_centroid = nullptr;
+  float* d_pivots_t = nullptr;
+  int32_t* d_chunk_off = nullptr;
+  int64_t device_bytes = 0;
+  int num_cus = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  // search scratch (grown on demand, reused across calls)
+  int64_t cap_q = 0;
+  int cap_k = 0;
+  float* d_queries = nullptr;
+  int32_t* d_ids = nullptr;
+  float* d_dists = nullptr;
+  int32_t* d_found = nullptr;
+  int32_t* d_hops = nullptr;
+  int32_t* d_stopped = nullptr;
+  uint64_t* d_tstart = nullptr;
+  uint64_t* d_tend = nullptr;
+  int32_t* d_counters = nullptr;
+  int32_t* h_ctrl = nullptr;   // [0] feed_count, [1] terminate (host-coherent)
+  int32_t* h_ring = nullptr;   // [cap_q] completion ring (host-coherent)
+  std::vector<int32_t> last_hops;
+  std::mutex mu;
+};
+
+namespace qv {
+
+static void free_scratch(qv_index* ix) {
+  hipFree(ix->d_queries);
+  hipFree(ix->d_ids);
+  hipFree(ix->d_dists);
+  hipFree(ix->d_found);
+  hipFree(ix->d_hops);
+  hipFree(ix->d_stopped);
+  hipFree(ix->d_tstart);
+  hipFree(ix->d_tend);
+  hipHostFree(ix->h_ring);
+  ix->d_queries = nullptr;
+  ix->d_ids = ix->d_found = ix->d_hops = ix->d_stopped = nullptr;
+  ix->d_dists = nullptr;
+  ix->d_tstart = ix->d_tend = nullptr;
+  ix->h_ring = nullptr;
+  ix->cap_q = 0;
+  ix->cap_k = 0;
+}
+
+static void ensure_scratch(qv_index* ix, int64_t nq, int k) {
+  if (!ix->d_counters) {
+    HIP_OK(hipMalloc(&ix->d_counters, 64));
+    HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_ctrl), 64, hipHostMallocCoherent));
+  }
+  if (nq <= ix->cap_q && k <= ix->cap_k) return;
+  free_scratch(ix);
+  const int64_t cq = std::max<int64_t>(nq, 1024);
+  const int ck = std::max(k, 16);
+  const int d = (int)ix->lay.num_dims;
+  HIP_OK(hipMalloc(&ix->d_queries, sizeof(float) * (size_t)cq * d));
+  HIP_OK(hipMalloc(&ix->d_ids, sizeof(int32_t) * (size_t)cq * ck));
+  HIP_OK(hipMalloc(&ix->d_dists, sizeof(float) * (size_t)cq * ck));
+  HIP_OK(hipMalloc(&ix->d_found, sizeof(int32_t) * (size_t)cq));
+  HIP_OK(hipMalloc(&ix->d_hops, sizeof(int32_t) * (size_t)cq));
+  HIP_OK(hipMalloc(&ix->d_stopped, sizeof(int32_t) * (size_t)cq));
+  HIP_OK(hipMalloc(&ix->d_tstart, sizeof(uint64_t) * (size_t)cq));
+  HIP_OK(hipMalloc(&ix->d_tend, sizeof(uint64_t) * (size_t)cq));
+  HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_ring), sizeof(int32_t) * (size_t)cq,
+                       hipHostMallocCoherent));
+  ix->cap_q = cq;
+  ix->cap_k = ck;
+}
+
+static void release_index(qv_index* ix) {
+  if (!ix) return;
+  hipSetDevice(ix->device);
+  free_scratch(ix);
+  hipFree(ix->d_counters);
+  hipHostFree(ix->h_ctrl);
+  hipFree(ix->d_pages);
+  hipFree(ix->d_codes);
+  hipFree(ix->d_centroid);
+  hipFree(ix->d_pivots_t);
+  hipFree(ix->d_chunk_off);
+  if (ix->ev0) hipEventDestroy(ix->ev0);
+  if (ix->ev1) hipEventDestroy(ix->ev1);
+  if (ix->stream) hipStreamDestroy(ix->stream);
+  delete ix;
+}
+
+// Copies a host file region to device memory through a pinned staging buffer.
+static void upload_index_pages(const std::string& path, int64_t num_pages, uint8_t* dst) {
+  const int64_t chunk_pages = 16384;  // 64 MB
+  uint8_t* stage = nullptr;
+  HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&stage), (size_t)(chunk_pages * kPageSize),
+                       hipHostMallocDefault));
+  std::unique_ptr<uint8_t, void (*)(uint8_t*)> guard(stage, [](uint8_t* p) { hipHostFree(p); });
+  FILE* f = std::fopen(path.c_str(), "rb");
+  if (!f) fail(QV_EIO, "Failed to open Mem Index: " + path);
+  std::unique_ptr<FILE, int (*)(FILE*)> fg(f, &std::fclose);
+  if (std::fseek(f, kPageSize, SEEK_SET) != 0) fail(QV_EIO, "Failed to seek Mem Index: " + path);
+  for (int64_t p = 0; p < num_pages; p += chunk_pages) {
+    const int64_t cnt = std::min(chunk_pages, num_pages - p);
+    const int64_t got = (int64_t)std::fread(stage, kPageSize, (size_t)cnt, f);
+    if (got != cnt)
+      fail(QV_EIO, "Mem Index Load FAILED: " + std::to_string(p + got) + " pages read from " + path);
+    HIP_OK(hipMemcpy(dst + p * kPageSize, stage, (size_t)(cnt * kPageSize), hipMemcpyHostToDevice));
+  }
+}
+
+static void validate_graph(qv_index* ix) {
+  int32_t* d_err = nullptr;
+  int64_t* d_bad = nullptr;
+  HIP_OK(hipMalloc(&d_err, sizeof(int32_t)));
+  HIP_OK(hipMalloc(&d_bad, sizeof(int64_t)));
+  HIP_OK(hipMemset(d_err, 0, sizeof(int32_t)));
+  HIP_OK(hipMemset(d_bad, 0x7f, sizeof(int64_t)));
+  const Layout& L = ix->lay;
+  const int blocks = (int)std::min<int64_t>((L.num_data + 3) / 4, 65536);
+  hipLaunchKernelGGL(validate_kernel, dim3(blocks), dim3(256), 0, ix->stream, ix->d_pages,
+                     L.num_data, L.nodes_per_page, L.node_size, L.data_size, (int)L.max_m0,
+                     d_err, d_bad);
+  HIP_OK(hipGetLastError());
+  HIP_OK(hipStreamSynchronize(ix->stream));
+  int32_t err = 0;
+  int64_t bad = 0;
+  HIP_OK(hipMemcpy(&err, d_err, sizeof(err), hipMemcpyDeviceToHost));
+  HIP_OK(hipMemcpy(&bad, d_bad, sizeof(bad), hipMemcpyDeviceToHost));
+  hipFree(d_err);
+  hipFree(d_bad);
+  if (err) {
+    std::string what;
+    if (err & 1) what += " degree>R";
+    if (err & 2) what += " neighbour-id>=n";
+    if (err & 4) what += " duplicate-neighbour";
+    fail(QV_EINDEX, "invalid graph (first bad node " + std::to_string(bad) + "):" + what);
+  }
+}
+
+qv_index* open_index(const std::string& index_dir, const std::string& dtype_s,
+                     const std::string& backend, const std::string& mem_file, int device) {
+  const int dtype = parse_data_type(dtype_s);
+  if (backend == "mmap") fail(QV_EUNSUPPORTED, "memory backend 'mmap' is not supported; use heap");
+  if (backend != "heap")
+    fail(QV_EINVAL, "Unsupported --memory-backend '" + backend + "'. Expected one of: heap, mmap");
+  const std::string index_file = find_index_file(index_dir);
+  const std::string pages_file = mem_file.empty() ? index_file : mem_file;
+  const std::string prefix = find_pq_prefix(index_dir);
+  Layout lay = parse_diskann_metadata(index_file, dtype);
+  PQTables pq;
+  read_pq_tables(prefix + "_pivots.bin", prefix + "_compressed.bin", pq);
+  if (pq.dim != lay.num_dims)
+    fail(QV_EIO, "PQ dimension " + std::to_string(pq.dim) + " != index dimension " +
+                     std::to_string(lay.num_dims));
+  if (pq.num_pts != lay.num_data)
+    fail(QV_EIO, "PQ point count " + std::to_string(pq.num_pts) + " != index point count " +
+                     std::to_string(lay.num_data));
+  if (lay.max_m0 > kMaxDegree || lay.max_m0 < 1)
+    fail(QV_EUNSUPPORTED, "max degree " + std::to_string(lay.max_m0) + " outside [1, 64]");
+  if ((lay.data_size & 3) || (lay.node_size & 3))
+    fail(QV_EUNSUPPORTED, "node records must be 4-byte aligned");
+  if (lay.num_data > INT32_MAX) fail(QV_EUNSUPPORTED, "more than 2^31-1 points");
+
+  int ndev = 0;
+  HIP_OK(hipGetDeviceCount(&ndev));
+  if (device < 0 || device >= ndev) fail(QV_EINVAL, "device " + std::to_string(device) + " not present");
+  HIP_OK(hipSetDevice(device));
+  std::unique_ptr<qv_index, void (*)(qv_index*)> ix(new qv_index(), release_index);
+  ix->device = device;
+  ix->lay = lay;
+  ix->M = pq.num_chunks;
+  hipDeviceProp_t prop;
+  HIP_OK(hipGetDeviceProperties(&prop, device));
+  ix->num_cus = prop.multiProcessorCount;
+  HIP_OK(hipStreamCreateWithFlags(&ix->stream, hipStreamNonBlocking));
+  HIP_OK(hipEventCreate(&ix->ev0));
+  HIP_OK(hipEventCreate(&ix->ev1));
+
+  const size_t page_bytes = (size_t)(lay.num_pages * kPageSize);
+  const size_t code_bytes = (size_t)lay.num_data * (size_t)ix->M;
+  HIP_OK(hipMalloc(&ix->d_pages, page_bytes));
+  HIP_OK(hipMalloc(&ix->d_codes, std::max<size_t>(code_bytes, 64)));
+  HIP_OK(hipMalloc(&ix->d_centroid, sizeof(float) * pq.centroid.size()));
+  HIP_OK(hipMalloc(&ix->d_pivots_t, sizeof(float) * pq.pivots_t.size()));
+  HIP_OK(hipMalloc(&ix->d_chunk_off, sizeof(int32_t) * pq.chunk_offsets.size()));
+  ix->device_bytes = (int64_t)(page_bytes + code_bytes + 4 * (pq.centroid.size() + pq.pivots_t.size()));
+  upload_index_pages(pages_file, lay.num_pages, ix->d_pages);
+  HIP_OK(hipMemcpy(ix->d_codes, pq.codes.data(), code_bytes, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(ix->d_centroid, pq.centroid.data(), sizeof(float) * pq.centroid.size(),
+                   hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(ix->d_pivots_t, pq.pivots_t.data(), sizeof(float) * pq.pivots_t.size(),
+                   hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(ix->d_chunk_off, pq.chunk_offsets.data(),
+                   sizeof(int32_t) * pq.chunk_offsets.size(), hipMemcpyHostToDevice));
+  validate_graph(ix.get());
+  return ix.release();
+}
+
+int slots_per_cu(qv_index* ix, int ef) {
+  const int P = merge_slots(ef);
+  KernelFn k = pick_kernel(ix->lay.data_type, P, ix->M);
+  const LdsPlan pl = lds_plan(ix->M, (int)ix->lay.num_dims, P);
+  if (pl.total > 65536)
+    HIP_OK(hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, pl.total));
+  int nb = 0;
+  HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(k), 64,
+                                                      (size_t)pl.total));
+  return nb;
+}
+
+static double percentile_sorted(const std::vector<double>& v, double frac) {
+  if (v.empty()) return 0.0;
+  size_t i = (size_t)((double)v.size() * frac);
+  if (i >= v.size()) i = v.size() - 1;
+  return v[i];
+}
+
+void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, int ef,
+            const qv_search_opts& o, int32_t* ids, float* dists, int32_t* found,
+            qv_search_report* rep) {
+  std::lock_guard<std::mutex> lk(ix->mu);
+  const Layout& L = ix->lay;
+  if (nq <= 0 || nq > INT32_MAX - 1) fail(QV_EINVAL, "number of queries must be in [1, 2^31-2]");
+  if (dim != L.num_dims)
+    fail(QV_EINVAL, "Query dimension mismatch: queries have " + std::to_string(dim) +
+                        " dims, but the index expects " + std::to_string(L.num_dims));
+  if (topk <= 0 || topk > kMaxTopk) fail(QV_EINVAL, "topk must be in [1, 64]");
+  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 448]");
+  if (o.pipe_width < 1 || o.pipe_width > kMaxPipeWidth) fail(QV_EINVAL, "--pipe-width must be in [1, 16]");
+  if (o.queries_per_block != 1)
+    fail(QV_EUNSUPPORTED, "--queries-per-block must be 1 in this build");
+  if (o.early_exit != QV_EXIT_NONE && o.early_exit != QV_EXIT_GPRUNING)
+    fail(QV_EINVAL, "early exit policy must be none or gpruning");
+  if (o.num_blocks < 0) fail(QV_EINVAL, "--num-blocks must be positive");
+
+  HIP_OK(hipSetDevice(ix->device));
+  ensure_scratch(ix, nq, topk);
+  const int P = merge_slots(ef);
+  KernelFn kern = pick_kernel(L.data_type, P, ix->M);
+  const LdsPlan pl = lds_plan(ix->M, (int)L.num_dims, P);
+  const int spc = slots_per_cu(ix, ef);
+  if (spc <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
+  const int num_blocks = o.num_blocks > 0 ? o.num_blocks : spc * ix->num_cus;
+  const int max_inflight = (int)std::min<int64_t>(nq, (int64_t)num_blocks + std::max(0, o.prefeed));
+
+  const float* d_q = queries;
+  if (!o.device_buffers) {
+    HIP_OK(hipMemcpyAsync(ix->d_queries, queries, sizeof(float) * (size_t)nq * dim,
+                          hipMemcpyHostToDevice, ix->stream));
+    d_q = ix->d_queries;
+  }
+  int32_t* d_ids = o.device_buffers ? ids : ix->d_ids;
+  float* d_dists = o.device_buffers ? dists : ix->d_dists;
+  int32_t* d_found = (o.device_buffers && found) ? found : ix->d_found;
+
+  HIP_OK(hipMemsetAsync(ix->d_counters, 0, 64, ix->stream));
+  HIP_OK(hipStreamSynchronize(ix->stream));
+  const bool streaming = o.admission == QV_ADMIT_STREAMING;
+  volatile int32_t* feed = ix->h_ctrl;
+  volatile int32_t* term = ix->h_ctrl + 1;
+  *feed = streaming ? 0 : (int32_t)nq;
+  *term = 0;
+  std::memset(ix->h_ring, 0, sizeof(int32_t) * (size_t)nq);
+  std::atomic_thread_fence(std::memory_order_seq_cst);
+
+  int32_t* dev_ctrl = nullptr;
+  int32_t* dev_ring = nullptr;
+  HIP_OK(hipHostGetDevicePointer(reinterpret_cast<void**>(&dev_ctrl), ix->h_ctrl, 0));
+  HIP_OK(hipHostGetDevicePointer(reinterpret_cast<void**>(&dev_ring), ix->h_ring, 0));
+
+  SearchArgs a{};
+  a.pages = ix->d_pages;
+  a.codes = ix->d_codes;
+  a.centroid = ix->d_centroid;
+  a.pivots_t = ix->d_pivots_t;
+  a.chunk_off = ix->d_chunk_off;
+  a.num_points = L.num_data;
+  a.nodes_per_page = L.nodes_per_page;
+  a.node_size = L.node_size;
+  a.data_size = L.data_size;
+  a.dim = (int32_t)L.num_dims;
+  a.num_chunks = ix->M;
+  a.max_m = (int32_t)L.max_m0;
+  a.medoid = (int32_t)L.enter_point;
+  a.queries = d_q;
+  a.nq = (int32_t)nq;
+  a.topk = topk;
+  a.ef = ef;
+  a.pipe_w = o.pipe_width;
+  a.early_exit = o.early_exit;
+  a.warmup = o.gpruning_warmup;
+  a.patience = o.gpruning_patience;
+  a.out_ids = d_ids;
+  a.out_dists = d_dists;
+  a.out_found = d_found;
+  a.out_hops = ix->d_hops;
+  a.out_stopped = ix->d_stopped;
+  a.t_start = ix->d_tstart;
+  a.t_end = ix->d_tend;
+  a.counters = ix->d_counters;
+  a.feed_count = dev_ctrl;
+  a.terminate = dev_ctrl + 1;
+  a.ring = dev_ring;
+  // Feed waits end on their own after this long even if the host never
+  // admits more work, so a lost host thread cannot leave the kernel spinning.
+  const double spin_s = o.timeout_s > 0 ? o.timeout_s + 5.0 : 60.0;
+  a.spin_limit_ticks = (uint64_t)(spin_s * 1e8);
+
+  using clock = std::chrono::steady_clock;
+  HIP_OK(hipEventRecord(ix->ev0, ix->stream));
+  hipLaunchKernelGGL(kern, dim3(num_blocks), dim3(64), (size_t)pl.total, ix->stream, a);
+  HIP_OK(hipGetLastError());
+  HIP_OK(hipEventRecord(ix->ev1, ix->stream));
+
+  const auto t0 = clock::now();
+  const bool has_deadline = o.timeout_s > 0;
+  const auto deadline = t0 + std::chrono::duration_cast<clock::duration>(
+                                 std::chrono::duration<double>(has_deadline ? o.timeout_s : 0.0));
+  bool timed_out = false;
+  std::vector<double> lat_ms;
+  if (streaming) {
+    // Host admission loop (search.cu:983-1051): keep at most max_inflight
+    // admitted-but-unfinished queries; stamp each completion from the ring.
+    std::vector<clock::time_point> admit((size_t)nq);
+    lat_ms.assign((size_t)nq, 0.0);
+    int64_t fed = max_inflight;
+    for (int64_t i = 0; i < fed; i++) admit[(size_t)i] = t0;
+    __atomic_store_n(ix->h_ctrl, (int32_t)fed, __ATOMIC_RELEASE);
+    int64_t done = 0;
+    const int min_batch = std::max(1, o.admit_min_batch);
+    while (done < nq) {
+      bool progressed = false;
+      while (done < nq) {
+        const int32_t e = __atomic_load_n(ix->h_ring + done, __ATOMIC_ACQUIRE);
+        if (e == 0) break;
+        const auto now = clock::now();
+        lat_ms[(size_t)(e - 1)] = std::chrono::duration<double, std::milli>(now - admit[(size_t)(e - 1)]).count();
+        done++;
+        progressed = true;
+      }
+      const int64_t target = std::min<int64_t>(nq, done + max_inflight);
+      if (target > fed && (target - fed >= min_batch || target == nq || fed - done == 0)) {
+        const auto now = clock::now();
+        for (int64_t i = fed; i < target; i++) admit[(size_t)i] = now;
+        fed = target;
+        __atomic_store_n(ix->h_ctrl, (int32_t)fed, __ATOMIC_RELEASE);
+      }
+      if (!progressed) {
+        if (has_deadline && clock::now() > deadline) {
+          timed_out = true;
+          break;
+        }
+        if (hipStreamQuery(ix->stream) == hipSuccess) break;  // kernel ended early (error path)
+      }
+    }
+  }
+  // Wait for the kernel, honouring the deadline.
+  while (true) {
+    hipError_t st = hipStreamQuery(ix->stream);
+    if (st == hipSuccess) break;
+    if (st != hipErrorNotReady) HIP_OK(st);
+    if (has_deadline && !timed_out && clock::now() > deadline) timed_out = true;
+    if (timed_out) __atomic_store_n(ix->h_ctrl + 1, 1, __ATOMIC_RELEASE);
+    std::this_thread::sleep_for(std::chrono::microseconds(streaming ? 5 : 50));
+  }
+  if (!o.device_buffers) {
+    HIP_OK(hipMemcpyAsync(ids, d_ids, sizeof(int32_t) * (size_t)nq * topk, hipMemcpyDeviceToHost, ix->stream));
+    HIP_OK(hipMemcpyAsync(dists, d_dists, sizeof(float) * (size_t)nq * topk, hipMemcpyDeviceToHost, ix->stream));
+    if (found)
+      HIP_OK(hipMemcpyAsync(found, d_found, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost, ix->stream));
+    HIP_OK(hipStreamSynchronize(ix->stream));
+  }
+  const auto t1 = clock::now();
+
+  int32_t counters[4] = {0, 0, 0, 0};
+  HIP_OK(hipMemcpy(counters, ix->d_counters, sizeof(counters), hipMemcpyDeviceToHost));
+  if (counters[2] & kErrSpinTimeout) fail(QV_ETIMEDOUT, "search kernel watchdog: feed wait exceeded its limit");
+  if (timed_out || counters[1] < nq) {
+    char buf[96];
+    std::snprintf(buf, sizeof(buf), "quiver_search exceeded the %g second timeout", o.timeout_s);
+    fail(QV_ETIMEDOUT, buf);
+  }
+  ix->last_hops.resize((size_t)nq);
+  HIP_OK(hipMemcpy(ix->last_hops.data(), ix->d_hops, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost));
+
+  if (rep) {
+    std::memset(rep, 0, sizeof(*rep));
+    const double secs = std::chrono::duration<double>(t1 - t0).count();
+    rep->search_time_s = secs;
+    rep->qps = (double)nq / secs;
+    float kms = 0.f;
+    HIP_OK(hipEventElapsedTime(&kms, ix->ev0, ix->ev1));
+    rep->kernel_ms = kms;
+    rep->num_blocks = num_blocks;
+    rep->max_inflight = max_inflight;
+    if (!streaming) {
+      std::vector<uint64_t> ts((size_t)nq), te((size_t)nq);
+      HIP_OK(hipMemcpy(ts.data(), ix->d_tstart, sizeof(uint64_t) * (size_t)nq, hipMemcpyDeviceToHost));
+      HIP_OK(hipMemcpy(te.data(), ix->d_tend, sizeof(uint64_t) * (size_t)nq, hipMemcpyDeviceToHost));
+      const uint64_t t_first = *std::min_element(ts.begin(), ts.end());
+      lat_ms.resize((size_t)nq);
+      for (int64_t i = 0; i < nq; i++) lat_ms[(size_t)i] = (double)(te[(size_t)i] - t_first) * 1e-5;
+    }
+    std::vector<int32_t> stopped((size_t)nq);
+    HIP_OK(hipMemcpy(stopped.data(), ix->d_stopped, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost));
+    rep->early_stopped = (int32_t)std::accumulate(stopped.begin(), stopped.end(), 0);
+    double hop_sum = 0;
+    for (int32_t h : ix->last_hops) hop_sum += h;
+    rep->avg_hops = hop_sum / (double)nq;
+    std::sort(lat_ms.begin(), lat_ms.end());
+    rep->lat_avg_ms = std::accumulate(lat_ms.begin(), lat_ms.end(), 0.0) / (double)nq;
+    rep->lat_p50_ms = percentile_sorted(lat_ms, 0.50);
+    rep->lat_p90_ms = percentile_sorted(lat_ms, 0.90);
+    rep->lat_p99_ms = percentile_sorted(lat_ms, 0.99);
+    rep->lat_p999_ms = percentile_sorted(lat_ms, 0.999);
+    rep->lat_max_ms = lat_ms.back();
+  }
+}
+
+}  // namespace qv
+
+// ================================================================ C ABI ====
+
+extern "C" {
+
+void qv_search_opts_default(qv_search_opts* o) {
+  if (!o) return;
+  std::memset(o, 0, sizeof(*o));
+  o->num_blocks = 0;
+  o->queries_per_block = 1;
+  o->pipe_width = 1;
+  o->early_exit = QV_EXIT_GPRUNING;
+  o->gpruning_warmup = 10;
+  o->gpruning_patience = 8;
+  o->prefeed = 0;
+  o->admit_min_batch = 32;
+  o->admission = QV_ADMIT_STREAMING;
+  o->device_buffers = 0;
+  o->timeout_s = 0.0;
+}
+
+int qv_index_open(const char* index_dir, const char* data_type, const char* memory_backend,
+                  const char* memory_index_file, int device, qv_index** out) {
+  return qv::guard([&] {
+    if (!index_dir || !data_type || !out) qv::fail(QV_EINVAL, "null argument");
+    *out = nullptr;
+    *out = qv::open_index(index_dir, data_type, memory_backend ? memory_backend : "heap",
+                          memory_index_file ? memory_index_file : "", device);
+  });
+}
+
+int qv_index_get_info(const qv_index* ix, qv_index_info* info) {
+  return qv::guard([&] {
+    if (!ix || !info) qv::fail(QV_EINVAL, "null argument");
+    const Layout& L = ix->lay;
+    info->num_data = L.num_data;
+    info->num_dims = L.num_dims;
+    info->max_m0 = L.max_m0;
+    info->enter_point = L.enter_point;
+    info->data_size = L.data_size;
+    info->node_size = L.node_size;
+    info->num_pages = L.num_pages;
+    info->nodes_per_page = L.nodes_per_page;
+    info->data_type = L.data_type;
+    info->num_chunks = ix->M;
+    info->device = ix->device;
+    HIP_OK(hipSetDevice(ix->device));
+    info->slots_per_cu = qv::slots_per_cu(const_cast<qv_index*>(ix), 64);
+    info->device_bytes = ix->device_bytes;
+  });
+}
+
+void qv_index_close(qv_index* ix) { qv::release_index(ix); }
+
+int qv_search(qv_index* ix, const float* queries, int64_t nq, int32_t dim, int32_t topk,
+              int32_t ef, const qv_search_opts* opts, int32_t* ids, float* dists,
+              int32_t* found, qv_search_report* rep) {
+  return qv::guard([&] {
+    if (!ix || !queries || !ids || !dists) qv::fail(QV_EINVAL, "null argument");
+    qv_search_opts o;
+    qv_search_opts_default(&o);
+    if (opts) o = *opts;
+    qv::search(ix, queries, nq, dim, topk, ef, o, ids, dists, found, rep);
+  });
+}
+
+int qv_last_hops(const qv_index* ix, int32_t* hops, int64_t nq) {
+  return qv::guard([&] {
+    if (!ix || !hops) qv::fail(QV_EINVAL, "null argument");
+    if ((size_t)nq > ix->last_hops.size()) qv::fail(QV_EINVAL, "nq exceeds the last search");
+    std::memcpy(hops, ix->last_hops.data(), sizeof(int32_t) * (size_t)nq);
+  });
+}
+
+int qv_lut_build(qv_index* ix, const float* d_queries, int64_t nq, float* d_luts, float* d_q_used) {
+  return qv::guard([&] {
+    if (!ix) qv::fail(QV_EINVAL, "null index");
+    int rc = qv_lut_build_raw(ix->d_centroid, ix->d_pivots_t, ix->d_chunk_off, (int32_t)ix->lay.num_dims,
+                              ix->M, d_queries, nq, d_luts, d_q_used, ix->device);
+    if (rc != QV_OK) qv::fail(rc, qv_last_error());
+  });
+}
+
+}  // extern "C"
