@@ -78,6 +78,19 @@ int qv_index_open(const char* index_dir, const char* data_type,
 
 int qv_index_get_info(const qv_index* index, qv_index_info* out);
 
+/* ---- Host-only pieces of the setup path (no GPU needed) ---------------------
+ * qv_find_index_files: find_index_file + find_pq_prefix
+ * (bin/common/index_discovery.hpp:57-103); writes NUL-terminated paths.
+ * qv_read_layout: parse_diskann_metadata (bin/common/metadata.hpp:15-72);
+ * fills the layout fields of `out` (PQ and device fields are zero).
+ * qv_read_index_pages: the heap memory backend's image
+ * (MemLoaderSync::load_heap, src/shared/io/mem_loader.cpp:28-44): page k of
+ * dst is page k+1 of the file, for k < num_pages. */
+int qv_find_index_files(const char* index_dir, char* index_file, char* pq_prefix,
+                        int32_t capacity);
+int qv_read_layout(const char* index_file, const char* data_type, qv_index_info* out);
+int qv_read_index_pages(const char* index_file, int64_t num_pages, uint8_t* dst);
+
 /* Frees every device and host resource of the handle.  NULL is accepted. */
 void qv_index_close(qv_index* index);
 

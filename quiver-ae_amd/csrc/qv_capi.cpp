@@ -72,6 +72,41 @@ int qv_build_index_cpu(const void* base, int32_t data_type, int64_t n, int32_t d
   });
 }
 
+int qv_find_index_files(const char* index_dir, char* index_file, char* pq_prefix, int32_t capacity) {
+  return qv::host_guard([&] {
+    if (!index_dir || !index_file || !pq_prefix || capacity <= 0) qv::fail(QV_EINVAL, "bad argument");
+    const std::string a = qv::find_index_file(index_dir);
+    const std::string b = qv::find_pq_prefix(index_dir);
+    if ((int64_t)a.size() >= capacity || (int64_t)b.size() >= capacity) qv::fail(QV_EINVAL, "path buffer too small");
+    std::memcpy(index_file, a.c_str(), a.size() + 1);
+    std::memcpy(pq_prefix, b.c_str(), b.size() + 1);
+  });
+}
+
+int qv_read_layout(const char* index_file, const char* data_type, qv_index_info* out) {
+  return qv::host_guard([&] {
+    if (!index_file || !data_type || !out) qv::fail(QV_EINVAL, "null argument");
+    const qv::Layout L = qv::parse_diskann_metadata(index_file, qv::parse_data_type(data_type));
+    std::memset(out, 0, sizeof(*out));
+    out->num_data = L.num_data;
+    out->num_dims = L.num_dims;
+    out->max_m0 = L.max_m0;
+    out->enter_point = L.enter_point;
+    out->data_size = L.data_size;
+    out->node_size = L.node_size;
+    out->num_pages = L.num_pages;
+    out->nodes_per_page = L.nodes_per_page;
+    out->data_type = L.data_type;
+  });
+}
+
+int qv_read_index_pages(const char* index_file, int64_t num_pages, uint8_t* dst) {
+  return qv::host_guard([&] {
+    if (!index_file || !dst || num_pages < 0) qv::fail(QV_EINVAL, "bad argument");
+    qv::read_index_pages(index_file, num_pages, dst);
+  });
+}
+
 int qv_mixture_fill_host(const qv_mixture* m, int64_t first_row, int64_t rows, void* dst) {
   return qv::host_guard([&] {
     if (!m || !dst || rows < 0 || m->dim <= 0 || m->num_centers <= 0) qv::fail(QV_EINVAL, "bad argument");

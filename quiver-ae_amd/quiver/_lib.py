@@ -145,6 +145,9 @@ SIGNATURES = {
     "qv_mixture_fill_host": (_I32, [C.POINTER(Mixture), _I64, _I64, _P]),
     "qv_mixture_fill_device": (_I32, [C.POINTER(Mixture), _I64, _I64, _P, C.c_int]),
     "qv_device_count": (_I32, [C.POINTER(_I32)]),
+    "qv_find_index_files": (_I32, [C.c_char_p, C.c_char_p, C.c_char_p, _I32]),
+    "qv_read_layout": (_I32, [C.c_char_p, C.c_char_p, C.POINTER(IndexInfo)]),
+    "qv_read_index_pages": (_I32, [C.c_char_p, _I64, _P]),
     "qv_dev_alloc": (_I32, [C.c_int, _I64, C.POINTER(_P)]),
     "qv_dev_free": (_I32, [_P]),
     "qv_dev_copy": (_I32, [_P, _P, _I64, _I32]),

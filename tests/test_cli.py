@@ -1,0 +1,82 @@
+"""quiver_search command line: flags, validation and error exits
+(bin/quiver_search.cu:58-320, bin/common/cli_*.hpp).  The CPU cases fail
+before any GPU work; the GPU case runs a search and checks the report lines
+and result files."""
+from __future__ import annotations
+
+import struct
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+CLI = ROOT / "quiver-ae_amd" / "bin" / "quiver_search"
+
+
+def run(*args, timeout=120):
+    if not CLI.is_file():
+        pytest.fail(f"{CLI} not built")
+    return subprocess.run([str(CLI), *map(str, args)], capture_output=True, text=True, timeout=timeout)
+
+
+def test_help_and_required_flags():
+    r = run("--help")
+    assert r.returncode == 0 and "--index-dir" in r.stdout
+    r = run("--query", "q.u8bin", "--data-type", "uint8")
+    assert r.returncode == 1 and "--index-dir: required" in r.stderr
+
+
+@pytest.mark.parametrize("flags,msg", [
+    (["--pipe-width", "17"], "--pipe-width must be in [1, 16]"),
+    (["--queries-per-block", "9"], "--queries-per-block must be in [1, 8]"),
+    (["--num-blocks", "0"], "--num-blocks must be positive"),
+    (["--early-exit-policy", "darth"], "invalid --early-exit-policy"),
+    (["--num-blocks-list", "8,x"], "invalid integer in --num-blocks-list"),
+    (["--bogus"], "Unknown argument"),
+])
+def test_validation(tmp_path, flags, msg):
+    r = run("--index-dir", tmp_path, "--query", "q.u8bin", "--data-type", "uint8", *flags)
+    assert r.returncode == 1 and msg in r.stderr
+
+
+def test_spdk_requires_spdk_build(tmp_path):
+    ssd = tmp_path / "ssds.txt"
+    ssd.write_text("0000:01:00.0\n")
+    r = run("--index-dir", tmp_path, "--query", "q.u8bin", "--data-type", "uint8", "--ssd-list-file", ssd)
+    assert r.returncode == 1 and "built without SPDK support" in r.stderr
+
+
+def test_missing_index_is_an_error(tmp_path):
+    r = run("--index-dir", tmp_path / "none", "--query", "q.u8bin", "--data-type", "uint8")
+    assert r.returncode == 1 and "does not exist" in r.stderr
+
+
+@pytest.mark.gpu
+def test_cli_search_report_and_results(small_u8_index, tmp_path):
+    import qv_oracle as O
+
+    ix = small_u8_index
+    q = ix["queries"][:100]
+    qf = tmp_path / "q.u8bin"
+    qf.write_bytes(struct.pack("<ii", *q.shape) + q.tobytes())
+    gf = tmp_path / "gt.ibin"
+    gf.write_bytes(struct.pack("<ii", 100, 10) + np.ascontiguousarray(ix["gt"][:100], np.int32).tobytes())
+    print(f"[gpu] CLI search {ix['dir']}", flush=True)
+    r = run("--index-dir", ix["dir"], "--query", qf, "--data-type", "uint8", "--ef-search", "64",
+            "--repeat", "2", "--pipe-width", "1", "--ground-truth", gf, "--result-prefix", tmp_path / "res",
+            "--early-exit-policy", "none", "--final-recall-csv", tmp_path / "r.csv")
+    assert r.returncode == 0, r.stderr
+    assert "QPS:" in r.stdout and "QueryLatency(ms): avg=" in r.stdout and "Recall @ 10:" in r.stdout
+    ids = np.fromfile(tmp_path / "res_ids.bin", dtype="<i4")
+    n, k = ids[:2]
+    assert (n, k) == (200, 10)
+    ids = ids[2:].reshape(200, 10)
+    host = O.HostIndex.from_files(ix["dir"], "uint8")
+    oids, _, _, _ = O.search(host, q.astype(np.float32), 10, 64, early_exit=O.EXIT_NONE)
+    np.testing.assert_array_equal(ids[:100], oids)
+    np.testing.assert_array_equal(ids[100:], oids)   # --repeat 2 repeats the set
+    line = [s for s in r.stdout.splitlines() if s.startswith("Recall @ 10:")][0]
+    assert abs(float(line.split(":")[1]) - O.recall(oids, ix["gt"][:100], 10)) < 1e-6
+    assert (tmp_path / "r.csv").read_text().startswith("query_id,gt_query_id,hits,recall")
