@@ -121,6 +121,8 @@ typedef struct {
   int32_t max_inflight;
   int32_t early_stopped;     /* queries ended by gpruning */
   int32_t reserved;
+  double total_hops;         /* expanded nodes over all queries */
+  double total_evals;        /* neighbour ADC evaluations over all queries */
 } qv_search_report;
 
 void qv_search_opts_default(qv_search_opts* opts);
@@ -213,6 +215,30 @@ void qv_build_params_default(qv_build_params* p);
 
 int qv_build_index_cpu(const void* base, int32_t data_type, int64_t n, int32_t dim,
                        const qv_build_params* params, const char* out_prefix);
+
+/* GPU construction of the same index from a device array d_base [n][dim]
+ * (Vamana with batched insertion; PQ trained on the device).  Returns a handle
+ * whose graph, vectors and codes are already resident in HBM; qv_index_save
+ * writes the three files. */
+int qv_build_index_gpu(const void* d_base, int32_t data_type, int64_t n, int32_t dim,
+                       const qv_build_params* params, int device, qv_index** out);
+
+/* Writes <out_prefix>_disk.index, _pq_pivots.bin and _pq_compressed.bin of a
+ * handle (device data copied back to the host). */
+int qv_index_save(const qv_index* index, const char* out_prefix);
+
+/* Copies a handle's data to caller host buffers (any may be NULL): the page
+ * image [num_pages * 4096], codes [n][M], centroid [dim], pivots [256][dim],
+ * chunk offsets [M+1] -- the heap-backend view host-side tools read. */
+int qv_index_copy_out(const qv_index* index, uint8_t* pages, uint8_t* codes, float* centroid,
+                      float* pivots, int32_t* chunk_offsets);
+
+/* Brute-force exact top-k of each query over a device base array (fp32
+ * arithmetic, exact for 8-bit data; ties broken by the smaller id).  All
+ * pointers are device pointers; ids [nq][k] int32, dists [nq][k] f32. */
+int qv_ground_truth(const void* d_base, int32_t data_type, int64_t n, int32_t dim,
+                    const float* d_queries, int64_t nq, int32_t k, int32_t* d_ids,
+                    float* d_dists, int device);
 
 /* ---- Synthetic data: the seeded Gaussian mixture of the benchmark configs ----
  * Host generator (CPU) and device generator (HIP) produce identical values for

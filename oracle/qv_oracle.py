@@ -151,6 +151,23 @@ class HostIndex:
         return cls(dt, dim, n, R, medoid, node_len, npp, dim * esz, pages, codes, centroid,
                    pivots, np.ascontiguousarray(pivots.T), co.astype(np.int32), chunk_id)
 
+    @classmethod
+    def from_arrays(cls, dtype: int, dim: int, n: int, R: int, medoid: int, pages: np.ndarray,
+                    codes: np.ndarray, centroid: np.ndarray, pivots: np.ndarray,
+                    chunk_offsets: np.ndarray) -> "HostIndex":
+        """An index already in host memory (page image without the header page)."""
+        esz = 4 if dtype == FLOAT else 1
+        node_size = dim * esz + 4 + 4 * R
+        npp = PAGE // node_size
+        co = np.ascontiguousarray(chunk_offsets, np.int32)
+        chunk_id = np.full(dim, -1, dtype=np.int32)
+        for i in range(len(co) - 1):
+            chunk_id[co[i]:co[i + 1]] = i
+        piv = np.ascontiguousarray(pivots, np.float32)
+        return cls(dtype, dim, n, R, medoid, node_size, npp, dim * esz, np.ascontiguousarray(pages),
+                   np.ascontiguousarray(codes), np.ascontiguousarray(centroid, np.float32), piv,
+                   np.ascontiguousarray(piv.T), co, chunk_id)
+
     def node_record(self, v: int) -> np.ndarray:
         off = (v // self.npp) * PAGE + (v % self.npp) * self.node_size
         return self.pages[off:off + self.node_size]

@@ -70,6 +70,7 @@ void read_index_pages(const std::string& path, int64_t num_pages, uint8_t* dst);
 void write_diskann_index(const std::string& path, const Layout& lay,
                          const void* base, const std::vector<uint32_t>& adj,
                          const std::vector<uint32_t>& deg);
+void write_index_image(const std::string& path, const Layout& lay, const uint8_t* pages);
 void write_pq_tables(const std::string& pivots_file, const std::string& codes_file,
                      const PQTables& t);
 

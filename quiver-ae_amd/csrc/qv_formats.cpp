@@ -204,6 +204,22 @@ void write_diskann_index(const std::string& path, const Layout& lay, const void*
   if (!out) fail(QV_EIO, "Failed writing " + path);
 }
 
+// Header page followed by an existing page image (pages 1..num_pages).
+void write_index_image(const std::string& path, const Layout& lay, const uint8_t* pages) {
+  std::ofstream out(path, std::ios::binary | std::ios::trunc);
+  if (!out.is_open()) fail(QV_EIO, "Failed to open " + path + " for writing");
+  std::vector<uint8_t> page((size_t)kPageSize, 0);
+  uint32_t hdr[2] = {9, 1};
+  uint64_t meta[9] = {(uint64_t)lay.num_data, (uint64_t)lay.num_dims, (uint64_t)lay.enter_point,
+                      (uint64_t)lay.node_size, (uint64_t)lay.nodes_per_page, 0, 0, 0,
+                      (uint64_t)((lay.num_pages + 1) * kPageSize)};
+  std::memcpy(page.data(), hdr, sizeof(hdr));
+  std::memcpy(page.data() + sizeof(hdr), meta, sizeof(meta));
+  out.write(reinterpret_cast<const char*>(page.data()), kPageSize);
+  out.write(reinterpret_cast<const char*>(pages), (std::streamsize)(lay.num_pages * kPageSize));
+  if (!out) fail(QV_EIO, "Failed writing " + path);
+}
+
 // DiskANN pivot file: a 4 KB metadata block holding four u64 offsets
 // (pivots, centroid, chunk offsets, end), then the three bin sections.
 void write_pq_tables(const std::string& pivots_file, const std::string& codes_file,

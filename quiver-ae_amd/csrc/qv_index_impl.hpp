@@ -1,0 +1,74 @@
+// qv_index_impl.hpp -- the opaque qv_index handle shared by the library's
+// translation units (index open, search, GPU build).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "qv_common.hpp"
+
+struct qv_index {
+  int device = 0;
+  qv::Layout lay;
+  int M = 0;
+  uint8_t* d_pages = nullptr;
+  uint8_t* d_codes = nullptr;
+  float* d_centroid = nullptr;
+  float* d_pivots_t = nullptr;
+  int32_t* d_chunk_off = nullptr;
+  int64_t device_bytes = 0;
+  int num_cus = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  // search scratch (grown on demand, reused across calls)
+  int64_t cap_q = 0;
+  int cap_k = 0;
+  float* d_queries = nullptr;
+  int32_t* d_ids = nullptr;
+  float* d_dists = nullptr;
+  int32_t* d_found = nullptr;
+  int32_t* d_hops = nullptr;
+  int32_t* d_stopped = nullptr;
+  int32_t* d_evals = nullptr;
+  uint64_t* d_tstart = nullptr;
+  uint64_t* d_tend = nullptr;
+  int32_t* d_counters = nullptr;
+  int32_t* h_ctrl = nullptr;   // [0] feed_count, [1] terminate (host-coherent)
+  int32_t* h_ring = nullptr;   // [cap_q] completion ring (host-coherent)
+  std::vector<int32_t> last_hops;
+  // host copies of the PQ tables (for saving the index)
+  std::vector<float> h_centroid, h_pivots;
+  std::vector<int32_t> h_chunk_off;
+  std::mutex mu;
+};
+
+namespace qv {
+
+// Extra per-query outputs of a search: the expanded nodes in order with their
+// exact distances (used by the graph builder).
+struct SearchRecord {
+  int32_t* ids = nullptr;    // [nq][cap]
+  float* dists = nullptr;    // [nq][cap]
+  int32_t cap = 0;
+};
+
+// Creates a handle around device buffers the caller allocated with hipMalloc
+// (ownership moves to the handle) and host PQ tables; validates the graph.
+qv_index* make_index(int device, const Layout& lay, const PQTables& pq, uint8_t* d_pages,
+                     uint8_t* d_codes, bool validate);
+
+void release_index(qv_index* ix);
+
+// Checks degree <= R, neighbour ids < n and duplicate-free lists on the device;
+// throws QV_EINDEX on the first violation.
+void validate_graph(qv_index* ix);
+
+// Device-buffer search in whole-batch admission with optional record output.
+void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef,
+                   const SearchRecord& rec, int32_t* d_hops, int num_blocks);
+
+}  // namespace qv

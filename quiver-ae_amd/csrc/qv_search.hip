@@ -23,6 +23,7 @@
 #include "qv_common.hpp"
 #include "qv_device.hpp"
 #include "qv_hip_util.hpp"
+#include "qv_index_impl.hpp"
 
 using namespace qv;
 using namespace qv::dev;
@@ -59,6 +60,7 @@ struct SearchArgs {
   int32_t* out_found;
   int32_t* out_hops;
   int32_t* out_stopped;
+  int32_t* out_evals;              // neighbour distance evaluations per query
   uint64_t* t_start;
   uint64_t* t_end;
   // dispatch
@@ -67,6 +69,10 @@ struct SearchArgs {
   const int32_t* terminate;        // host-coherent, may be null
   int32_t* ring;                   // host-coherent completion ring, may be null
   uint64_t spin_limit_ticks;       // watchdog on feed waits (100 MHz ticks)
+  // optional record of expanded nodes (graph construction)
+  int32_t* rec_ids;
+  float* rec_dists;
+  int32_t rec_cap;
 };
 
 enum : int32_t { kErrSpinTimeout = 1 };
@@ -99,9 +105,11 @@ struct Query {
   float td;      // top-k entry of this lane
   int32_t ti;
   int fc;        // found count
+  int evals;     // ADC evaluations so far
+  float last_e;  // exact distance of the node expanded by the last hop
 
   __device__ Query(const SearchArgs& args, char* smem)
-      : a(args), sz(0), td(__int_as_float(0x7f800000)), ti(-1), fc(0) {
+      : a(args), sz(0), td(__int_as_float(0x7f800000)), ti(-1), fc(0), evals(0) {
     LdsPlan pl = lds_plan(a.num_chunks, a.dim, P);
     lut = reinterpret_cast<float*>(smem + pl.lut_off);
     qc = reinterpret_cast<float*>(smem + pl.qc_off);
@@ -123,6 +131,7 @@ struct Query {
     const uint8_t* rec = record(v);
     const uint32_t* rec32 = reinterpret_cast<const uint32_t*>(rec + a.data_size);
     const int deg = (int)rec32[0];
+    evals += deg;
     const bool has = lane < deg;
     const uint32_t nbr = has ? rec32[1 + lane] : 0u;
 
@@ -135,6 +144,7 @@ struct Query {
 
     // Exact distance of v and the top-k insert (the reference's second warp).
     const float e = exact_l2_ref<T>(rec, qu, a.dim);
+    last_e = e;
     const float dlast = __shfl(td, a.topk - 1);
     if (fc < a.topk || e < dlast) topk_insert(td, ti, fc, a.topk, e, v);
 
@@ -289,8 +299,16 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
       return gpr && step >= a.warmup && a.patience > 0 && g.no_improve >= a.patience;
     };
 
+    auto log_hop = [&](int32_t v) {
+      if (a.rec_ids && lane == 0 && step < a.rec_cap) {
+        a.rec_ids[(int64_t)qid * a.rec_cap + step] = v;
+        a.rec_dists[(int64_t)qid * a.rec_cap + step] = Q.last_e;
+      }
+    };
+
     // ---- boot (kernel_q1.cuh:199-397)
     int32_t first = Q.hop(a.medoid);
+    log_hop(a.medoid);
     step = 1;
     if (check()) {
       stop = true;
@@ -316,6 +334,7 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
         if (!(cur & (1u << w))) continue;
         const int32_t v = lane_node[w];
         int32_t nx = Q.hop(v);
+        log_hop(v);
         ++step;
         if (check()) {
           stop = true;
@@ -346,6 +365,7 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
       if (a.out_found) a.out_found[qid] = Q.fc;
       if (a.out_hops) a.out_hops[qid] = step;
       if (a.out_stopped) a.out_stopped[qid] = stop ? 1 : 0;
+      if (a.out_evals) a.out_evals[qid] = Q.evals;
       if (a.t_end) a.t_end[qid] = wall_ticks();
       atomicAdd(&a.counters[1], 1);
       if (a.ring) {
@@ -422,37 +442,6 @@ int merge_slots(int ef) { return ef <= 64 ? 2 : (ef <= 192 ? 4 : 8); }
 
 // ============================================================== host side ===
 
-struct qv_index {
-  int device = 0;
-  Layout lay;
-  int M = 0;
-  uint8_t* d_pages = nullptr;
-  uint8_t* d_codes = nullptr;
-  float* d_centroid = nullptr;
-  float* d_pivots_t = nullptr;
-  int32_t* d_chunk_off = nullptr;
-  int64_t device_bytes = 0;
-  int num_cus = 0;
-  hipStream_t stream = nullptr;
-  hipEvent_t ev0 = nullptr, ev1 = nullptr;
-  // search scratch (grown on demand, reused across calls)
-  int64_t cap_q = 0;
-  int cap_k = 0;
-  float* d_queries = nullptr;
-  int32_t* d_ids = nullptr;
-  float* d_dists = nullptr;
-  int32_t* d_found = nullptr;
-  int32_t* d_hops = nullptr;
-  int32_t* d_stopped = nullptr;
-  uint64_t* d_tstart = nullptr;
-  uint64_t* d_tend = nullptr;
-  int32_t* d_counters = nullptr;
-  int32_t* h_ctrl = nullptr;   // [0] feed_count, [1] terminate (host-coherent)
-  int32_t* h_ring = nullptr;   // [cap_q] completion ring (host-coherent)
-  std::vector<int32_t> last_hops;
-  std::mutex mu;
-};
-
 namespace qv {
 
 static void free_scratch(qv_index* ix) {
@@ -462,11 +451,12 @@ static void free_scratch(qv_index* ix) {
   hipFree(ix->d_found);
   hipFree(ix->d_hops);
   hipFree(ix->d_stopped);
+  hipFree(ix->d_evals);
   hipFree(ix->d_tstart);
   hipFree(ix->d_tend);
   hipHostFree(ix->h_ring);
   ix->d_queries = nullptr;
-  ix->d_ids = ix->d_found = ix->d_hops = ix->d_stopped = nullptr;
+  ix->d_ids = ix->d_found = ix->d_hops = ix->d_stopped = ix->d_evals = nullptr;
   ix->d_dists = nullptr;
   ix->d_tstart = ix->d_tend = nullptr;
   ix->h_ring = nullptr;
@@ -490,6 +480,7 @@ static void ensure_scratch(qv_index* ix, int64_t nq, int k) {
   HIP_OK(hipMalloc(&ix->d_found, sizeof(int32_t) * (size_t)cq));
   HIP_OK(hipMalloc(&ix->d_hops, sizeof(int32_t) * (size_t)cq));
   HIP_OK(hipMalloc(&ix->d_stopped, sizeof(int32_t) * (size_t)cq));
+  HIP_OK(hipMalloc(&ix->d_evals, sizeof(int32_t) * (size_t)cq));
   HIP_OK(hipMalloc(&ix->d_tstart, sizeof(uint64_t) * (size_t)cq));
   HIP_OK(hipMalloc(&ix->d_tend, sizeof(uint64_t) * (size_t)cq));
   HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_ring), sizeof(int32_t) * (size_t)cq,
@@ -498,7 +489,7 @@ static void ensure_scratch(qv_index* ix, int64_t nq, int k) {
   ix->cap_k = ck;
 }
 
-static void release_index(qv_index* ix) {
+void release_index(qv_index* ix) {
   if (!ix) return;
   hipSetDevice(ix->device);
   free_scratch(ix);
@@ -535,7 +526,7 @@ static void upload_index_pages(const std::string& path, int64_t num_pages, uint8
   }
 }
 
-static void validate_graph(qv_index* ix) {
+void validate_graph(qv_index* ix) {
   int32_t* d_err = nullptr;
   int64_t* d_bad = nullptr;
   HIP_OK(hipMalloc(&d_err, sizeof(int32_t)));
@@ -592,34 +583,51 @@ qv_index* open_index(const std::string& index_dir, const std::string& dtype_s,
   HIP_OK(hipGetDeviceCount(&ndev));
   if (device < 0 || device >= ndev) fail(QV_EINVAL, "device " + std::to_string(device) + " not present");
   HIP_OK(hipSetDevice(device));
+  const size_t page_bytes = (size_t)(lay.num_pages * kPageSize);
+  const size_t code_bytes = (size_t)lay.num_data * (size_t)pq.num_chunks;
+  uint8_t* d_pages = nullptr;
+  uint8_t* d_codes = nullptr;
+  HIP_OK(hipMalloc(&d_pages, page_bytes));
+  std::unique_ptr<uint8_t, void (*)(uint8_t*)> pg(d_pages, [](uint8_t* p) { (void)hipFree(p); });
+  HIP_OK(hipMalloc(&d_codes, std::max<size_t>(code_bytes, 64)));
+  std::unique_ptr<uint8_t, void (*)(uint8_t*)> cg(d_codes, [](uint8_t* p) { (void)hipFree(p); });
+  upload_index_pages(pages_file, lay.num_pages, d_pages);
+  HIP_OK(hipMemcpy(d_codes, pq.codes.data(), code_bytes, hipMemcpyHostToDevice));
+  pg.release();
+  cg.release();
+  return make_index(device, lay, pq, d_pages, d_codes, true);
+}
+
+qv_index* make_index(int device, const Layout& lay, const PQTables& pq, uint8_t* d_pages,
+                     uint8_t* d_codes, bool validate) {
   std::unique_ptr<qv_index, void (*)(qv_index*)> ix(new qv_index(), release_index);
   ix->device = device;
   ix->lay = lay;
   ix->M = pq.num_chunks;
+  ix->d_pages = d_pages;
+  ix->d_codes = d_codes;
+  HIP_OK(hipSetDevice(device));
   hipDeviceProp_t prop;
   HIP_OK(hipGetDeviceProperties(&prop, device));
   ix->num_cus = prop.multiProcessorCount;
   HIP_OK(hipStreamCreateWithFlags(&ix->stream, hipStreamNonBlocking));
   HIP_OK(hipEventCreate(&ix->ev0));
   HIP_OK(hipEventCreate(&ix->ev1));
-
-  const size_t page_bytes = (size_t)(lay.num_pages * kPageSize);
-  const size_t code_bytes = (size_t)lay.num_data * (size_t)ix->M;
-  HIP_OK(hipMalloc(&ix->d_pages, page_bytes));
-  HIP_OK(hipMalloc(&ix->d_codes, std::max<size_t>(code_bytes, 64)));
   HIP_OK(hipMalloc(&ix->d_centroid, sizeof(float) * pq.centroid.size()));
   HIP_OK(hipMalloc(&ix->d_pivots_t, sizeof(float) * pq.pivots_t.size()));
   HIP_OK(hipMalloc(&ix->d_chunk_off, sizeof(int32_t) * pq.chunk_offsets.size()));
-  ix->device_bytes = (int64_t)(page_bytes + code_bytes + 4 * (pq.centroid.size() + pq.pivots_t.size()));
-  upload_index_pages(pages_file, lay.num_pages, ix->d_pages);
-  HIP_OK(hipMemcpy(ix->d_codes, pq.codes.data(), code_bytes, hipMemcpyHostToDevice));
+  ix->device_bytes = (int64_t)(lay.num_pages * kPageSize + lay.num_data * pq.num_chunks +
+                               4 * (int64_t)(pq.centroid.size() + pq.pivots_t.size()));
   HIP_OK(hipMemcpy(ix->d_centroid, pq.centroid.data(), sizeof(float) * pq.centroid.size(),
                    hipMemcpyHostToDevice));
   HIP_OK(hipMemcpy(ix->d_pivots_t, pq.pivots_t.data(), sizeof(float) * pq.pivots_t.size(),
                    hipMemcpyHostToDevice));
   HIP_OK(hipMemcpy(ix->d_chunk_off, pq.chunk_offsets.data(),
                    sizeof(int32_t) * pq.chunk_offsets.size(), hipMemcpyHostToDevice));
-  validate_graph(ix.get());
+  ix->h_centroid = pq.centroid;
+  ix->h_pivots = pq.pivots;
+  ix->h_chunk_off = pq.chunk_offsets;
+  if (validate) validate_graph(ix.get());
   return ix.release();
 }
 
@@ -634,6 +642,75 @@ int slots_per_cu(qv_index* ix, int ef) {
   HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(k), 64,
                                                       (size_t)pl.total));
   return nb;
+}
+
+static SearchArgs base_args(qv_index* ix) {
+  const Layout& L = ix->lay;
+  SearchArgs a{};
+  a.pages = ix->d_pages;
+  a.codes = ix->d_codes;
+  a.centroid = ix->d_centroid;
+  a.pivots_t = ix->d_pivots_t;
+  a.chunk_off = ix->d_chunk_off;
+  a.num_points = L.num_data;
+  a.nodes_per_page = L.nodes_per_page;
+  a.node_size = L.node_size;
+  a.data_size = L.data_size;
+  a.dim = (int32_t)L.num_dims;
+  a.num_chunks = ix->M;
+  a.max_m = (int32_t)L.max_m0;
+  a.medoid = (int32_t)L.enter_point;
+  return a;
+}
+
+// Whole-batch search over device queries that records every expanded node and
+// its exact distance (the greedy-search step of graph construction).
+void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, const SearchRecord& rec,
+                   int32_t* d_hops, int num_blocks) {
+  std::lock_guard<std::mutex> lk(ix->mu);
+  if (nq <= 0 || nq > INT32_MAX - 1) fail(QV_EINVAL, "number of queries out of range");
+  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 448]");
+  HIP_OK(hipSetDevice(ix->device));
+  ensure_scratch(ix, nq, 1);
+  const int P = merge_slots(ef);
+  KernelFn kern = pick_kernel(ix->lay.data_type, P, ix->M);
+  const LdsPlan pl = lds_plan(ix->M, (int)ix->lay.num_dims, P);
+  const int spc = slots_per_cu(ix, ef);
+  int nb = num_blocks > 0 ? num_blocks : spc * ix->num_cus;
+  nb = (int)std::min<int64_t>(nb, nq);
+  SearchArgs a = base_args(ix);
+  a.queries = d_queries;
+  a.nq = (int32_t)nq;
+  a.topk = 1;
+  a.ef = ef;
+  a.pipe_w = 1;
+  a.early_exit = QV_EXIT_NONE;
+  a.warmup = 0;
+  a.patience = 0;
+  a.out_ids = ix->d_ids;
+  a.out_dists = ix->d_dists;
+  a.out_found = nullptr;
+  a.out_hops = d_hops;
+  a.out_stopped = nullptr;
+  a.out_evals = nullptr;
+  a.t_start = nullptr;
+  a.t_end = nullptr;
+  a.counters = ix->d_counters;
+  a.feed_count = nullptr;
+  a.terminate = nullptr;
+  a.ring = nullptr;
+  a.spin_limit_ticks = (uint64_t)(60.0 * 1e8);
+  a.rec_ids = rec.ids;
+  a.rec_dists = rec.dists;
+  a.rec_cap = rec.cap;
+  HIP_OK(hipMemsetAsync(ix->d_counters, 0, 64, ix->stream));
+  hipLaunchKernelGGL(kern, dim3(nb), dim3(64), (size_t)pl.total, ix->stream, a);
+  HIP_OK(hipGetLastError());
+  HIP_OK(hipStreamSynchronize(ix->stream));
+  int32_t counters[4] = {0, 0, 0, 0};
+  HIP_OK(hipMemcpy(counters, ix->d_counters, sizeof(counters), hipMemcpyDeviceToHost));
+  if (counters[1] != nq)
+    fail(QV_EHIP, "record search finished " + std::to_string(counters[1]) + " of " + std::to_string(nq) + " queries");
 }
 
 static double percentile_sorted(const std::vector<double>& v, double frac) {
@@ -696,20 +773,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   HIP_OK(hipHostGetDevicePointer(reinterpret_cast<void**>(&dev_ctrl), ix->h_ctrl, 0));
   HIP_OK(hipHostGetDevicePointer(reinterpret_cast<void**>(&dev_ring), ix->h_ring, 0));
 
-  SearchArgs a{};
-  a.pages = ix->d_pages;
-  a.codes = ix->d_codes;
-  a.centroid = ix->d_centroid;
-  a.pivots_t = ix->d_pivots_t;
-  a.chunk_off = ix->d_chunk_off;
-  a.num_points = L.num_data;
-  a.nodes_per_page = L.nodes_per_page;
-  a.node_size = L.node_size;
-  a.data_size = L.data_size;
-  a.dim = (int32_t)L.num_dims;
-  a.num_chunks = ix->M;
-  a.max_m = (int32_t)L.max_m0;
-  a.medoid = (int32_t)L.enter_point;
+  SearchArgs a = base_args(ix);
   a.queries = d_q;
   a.nq = (int32_t)nq;
   a.topk = topk;
@@ -723,6 +787,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   a.out_found = d_found;
   a.out_hops = ix->d_hops;
   a.out_stopped = ix->d_stopped;
+  a.out_evals = ix->d_evals;
   a.t_start = ix->d_tstart;
   a.t_end = ix->d_tend;
   a.counters = ix->d_counters;
@@ -733,6 +798,9 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   // admits more work, so a lost host thread cannot leave the kernel spinning.
   const double spin_s = o.timeout_s > 0 ? o.timeout_s + 5.0 : 60.0;
   a.spin_limit_ticks = (uint64_t)(spin_s * 1e8);
+  a.rec_ids = nullptr;
+  a.rec_dists = nullptr;
+  a.rec_cap = 0;
 
   using clock = std::chrono::steady_clock;
   HIP_OK(hipEventRecord(ix->ev0, ix->stream));
@@ -835,6 +903,12 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     double hop_sum = 0;
     for (int32_t h : ix->last_hops) hop_sum += h;
     rep->avg_hops = hop_sum / (double)nq;
+    rep->total_hops = hop_sum;
+    std::vector<int32_t> ev((size_t)nq);
+    HIP_OK(hipMemcpy(ev.data(), ix->d_evals, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost));
+    double ev_sum = 0;
+    for (int32_t e : ev) ev_sum += e;
+    rep->total_evals = ev_sum;
     std::sort(lat_ms.begin(), lat_ms.end());
     rep->lat_avg_ms = std::accumulate(lat_ms.begin(), lat_ms.end(), 0.0) / (double)nq;
     rep->lat_p50_ms = percentile_sorted(lat_ms, 0.50);
@@ -909,6 +983,43 @@ int qv_search(qv_index* ix, const float* queries, int64_t nq, int32_t dim, int32
     qv_search_opts_default(&o);
     if (opts) o = *opts;
     qv::search(ix, queries, nq, dim, topk, ef, o, ids, dists, found, rep);
+  });
+}
+
+int qv_index_save(const qv_index* ix, const char* out_prefix) {
+  return qv::guard([&] {
+    if (!ix || !out_prefix) qv::fail(QV_EINVAL, "null argument");
+    const Layout& L = ix->lay;
+    HIP_OK(hipSetDevice(ix->device));
+    std::vector<uint8_t> pages((size_t)(L.num_pages * kPageSize));
+    HIP_OK(hipMemcpy(pages.data(), ix->d_pages, pages.size(), hipMemcpyDeviceToHost));
+    const std::string pre = out_prefix;
+    qv::write_index_image(pre + "_disk.index", L, pages.data());
+    qv::PQTables t;
+    t.dim = (int)L.num_dims;
+    t.num_chunks = ix->M;
+    t.num_pts = L.num_data;
+    t.centroid = ix->h_centroid;
+    t.pivots = ix->h_pivots;
+    t.chunk_offsets = ix->h_chunk_off;
+    t.codes.resize((size_t)L.num_data * ix->M);
+    HIP_OK(hipMemcpy(t.codes.data(), ix->d_codes, t.codes.size(), hipMemcpyDeviceToHost));
+    qv::write_pq_tables(pre + "_pq_pivots.bin", pre + "_pq_compressed.bin", t);
+  });
+}
+
+int qv_index_copy_out(const qv_index* ix, uint8_t* pages, uint8_t* codes, float* centroid,
+                      float* pivots, int32_t* chunk_offsets) {
+  return qv::guard([&] {
+    if (!ix) qv::fail(QV_EINVAL, "null index");
+    const Layout& L = ix->lay;
+    HIP_OK(hipSetDevice(ix->device));
+    if (pages) HIP_OK(hipMemcpy(pages, ix->d_pages, (size_t)(L.num_pages * kPageSize), hipMemcpyDeviceToHost));
+    if (codes) HIP_OK(hipMemcpy(codes, ix->d_codes, (size_t)L.num_data * ix->M, hipMemcpyDeviceToHost));
+    if (centroid) std::memcpy(centroid, ix->h_centroid.data(), sizeof(float) * ix->h_centroid.size());
+    if (pivots) std::memcpy(pivots, ix->h_pivots.data(), sizeof(float) * ix->h_pivots.size());
+    if (chunk_offsets)
+      std::memcpy(chunk_offsets, ix->h_chunk_off.data(), sizeof(int32_t) * ix->h_chunk_off.size());
   });
 }
 

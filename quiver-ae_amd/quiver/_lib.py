@@ -86,6 +86,8 @@ class SearchReport(C.Structure):
         ("max_inflight", C.c_int32),
         ("early_stopped", C.c_int32),
         ("reserved", C.c_int32),
+        ("total_hops", C.c_double),
+        ("total_evals", C.c_double),
     ]
 
     def as_dict(self) -> dict:
@@ -145,6 +147,10 @@ SIGNATURES = {
     "qv_mixture_fill_host": (_I32, [C.POINTER(Mixture), _I64, _I64, _P]),
     "qv_mixture_fill_device": (_I32, [C.POINTER(Mixture), _I64, _I64, _P, C.c_int]),
     "qv_device_count": (_I32, [C.POINTER(_I32)]),
+    "qv_build_index_gpu": (_I32, [_P, _I32, _I64, _I32, C.POINTER(BuildParams), C.c_int, C.POINTER(_P)]),
+    "qv_index_save": (_I32, [_P, C.c_char_p]),
+    "qv_index_copy_out": (_I32, [_P, _P, _P, _P, _P, _P]),
+    "qv_ground_truth": (_I32, [_P, _I32, _I64, _I32, _P, _I64, _I32, _P, _P, C.c_int]),
     "qv_find_index_files": (_I32, [C.c_char_p, C.c_char_p, C.c_char_p, _I32]),
     "qv_read_layout": (_I32, [C.c_char_p, C.c_char_p, C.POINTER(IndexInfo)]),
     "qv_read_index_pages": (_I32, [C.c_char_p, _I64, _P]),
