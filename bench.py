@@ -54,6 +54,9 @@ def main() -> int:
     ap.add_argument("--no-adc", action="store_true", help="skip the ADC microbenchmark leg")
     ap.add_argument("--adc-codes", type=int, default=1_000_000_000)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--ef", type=int, default=0, help="time this ef_search and skip the sweep")
+    ap.add_argument("--policy", default="none", choices=("none", "gpruning"),
+                    help="early-exit policy used with --ef")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1",
@@ -132,7 +135,12 @@ def main() -> int:
     # ---- sweep (untimed): the fastest (ef, policy) with recall >= target ----
     sweep = []
     best = None
-    for policy, pname in ((_lib.QV_EXIT_GPRUNING, "gpruning"), (_lib.QV_EXIT_NONE, "none")):
+    plan = ((_lib.QV_EXIT_GPRUNING, "gpruning"), (_lib.QV_EXIT_NONE, "none"))
+    if args.ef:
+        pol = _lib.QV_EXIT_GPRUNING if args.policy == "gpruning" else _lib.QV_EXIT_NONE
+        best = (args.ef, pol, 0.0, args.policy)
+        plan = ()
+    for policy, pname in plan:
         for ef in w["efs"]:
             rep = run(ef, policy)
             r = recall_of()

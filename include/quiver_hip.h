@@ -150,7 +150,8 @@ int qv_device_info(int device, char* name, int32_t name_len, int32_t* num_cus,
 /* ---- Device-buffer plumbing (no reference counterpart) ---------------------
  * For callers that reach the library through a plain FFI (ctypes) and have no
  * HIP binding of their own: allocate, copy and clear device memory on the
- * library's HIP runtime.  kind: 0 host->device, 1 device->host, 2 device->device. */
+ * library's HIP runtime.  kind: 0 host->device, 1 device->host, 2 device->device
+ * (one GPU, 16-byte aligned: a grid-stride copy kernel, else hipMemcpy). */
 int qv_device_count(int32_t* count);
 int qv_dev_alloc(int device, int64_t bytes, void** out);
 int qv_dev_free(void* ptr);
@@ -176,7 +177,9 @@ int qv_lut_build_raw(const float* d_centroid, const float* d_pivots_t,
  * (sequential fp32 sum over m) with id = ids[q][s]; keeps the topk smallest
  * under (d, s), i.e. the reference's first-found-wins insert applied in s order.
  * All pointers are device pointers: luts [nq][M][256] f32, codes
- * [num_codes][M] u8, ids [nq][ids_per_query] int32 (each < num_codes),
+ * [num_codes][M] u8, ids [nq][ids_per_query] int32 (each in [0, num_codes);
+ * the base address 16-byte aligned, else QV_EINVAL; an id outside the range
+ * reads a row inside the table and its distance is unspecified),
  * out_ids [nq][topk] int32, out_dists [nq][topk] f32, dist_sums [nq] f64 (may
  * be NULL; the sum of all distances of a query).  elapsed_ms (may be NULL)
  * receives the kernel time from HIP events. */

@@ -39,6 +39,56 @@ __device__ __forceinline__ uint64_t sentinel_key(int lane) {
   return make_key(__int_as_float(0x7f800000), 0xffffffffu - (uint32_t)lane, false);
 }
 
+// ---- wave64 exchange primitives ------------------------------------------
+// DPP controls (GFX9): quad_perm [1,0,3,2] = 0xB1 (xor 1), [2,3,0,1] = 0x4E
+// (xor 2), row_ror:8 = 0x128 (xor 8 inside a 16-lane row), wave_shr:1 = 0x138.
+// ds_swizzle bit mode (and 0x1F, xor m) for xor 4 / 16 inside 32 lanes;
+// ds_bpermute for xor 32.  Uniform-lane reads use v_readlane.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane32(uint32_t v, int lane) {
+  if constexpr (M == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+  } else if constexpr (M == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+  } else if constexpr (M == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
+  } else if constexpr (M == 4 || M == 16) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (M << 10));
+  } else {
+    return (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ M) << 2, (int)v);
+  }
+}
+
+template <int M>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v, int lane) {
+  const uint32_t lo = xor_lane32<M>((uint32_t)v, lane);
+  const uint32_t hi = xor_lane32<M>((uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Value of lane i-1 (lane 0 keeps its own value).
+__device__ __forceinline__ uint32_t lane_up1_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x138, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float lane_up1_f32(float v) { return __uint_as_float(lane_up1_u32(__float_as_uint(v))); }
+
+// Value held by lane l (l wave-uniform).
+__device__ __forceinline__ uint32_t read_lane_u32(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+__device__ __forceinline__ int32_t read_lane_i32(int32_t v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ float read_lane_f32(float v, int l) {
+  return __uint_as_float(read_lane_u32(__float_as_uint(v), l));
+}
+__device__ __forceinline__ uint64_t read_lane_u64(uint64_t v, int l) {
+  return ((uint64_t)read_lane_u32((uint32_t)(v >> 32), l) << 32) | read_lane_u32((uint32_t)v, l);
+}
+
+// Number of set bits of mask below this lane.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
   uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
   lo = (uint32_t)__shfl_xor((int)lo, m);
@@ -49,19 +99,33 @@ __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
 __device__ __forceinline__ uint64_t umin64(uint64_t a, uint64_t b) { return a < b ? a : b; }
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a < b ? b : a; }
 
+// Lane id the compiler cannot treat as loop-invariant: comparisons derived
+// from it are recomputed where they are used instead of being hoisted into
+// dozens of live 64-bit lane masks (which spill scalar registers).
+__device__ __forceinline__ int opaque_lane() {
+  int lane = lane_id();
+  asm volatile("" : "+v"(lane));
+  return lane;
+}
+
+template <int J>
+__device__ __forceinline__ uint64_t cx_step(uint64_t key, int lane, bool up) {
+  const uint64_t other = xor_lane64<J>(key, lane);
+  const bool lower = (lane & J) == 0;
+  return (lower == up) ? umin64(key, other) : umax64(key, other);
+}
+
 // Bitonic sort of one key per lane, descending across the wave.
 __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int k = 2; k <= kWave; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      uint64_t other = shfl_xor64(key, j);
-      bool up = (lane & k) != 0;         // final pass (k = 64): descending
-      bool lower = (lane & j) == 0;
-      key = (lower == up) ? umin64(key, other) : umax64(key, other);
-    }
-  }
+  const int lane = opaque_lane();
+#define QV_STAGE(K, J) key = cx_step<J>(key, lane, (lane & (K)) != 0)
+  QV_STAGE(2, 1);
+  QV_STAGE(4, 2); QV_STAGE(4, 1);
+  QV_STAGE(8, 4); QV_STAGE(8, 2); QV_STAGE(8, 1);
+  QV_STAGE(16, 8); QV_STAGE(16, 4); QV_STAGE(16, 2); QV_STAGE(16, 1);
+  QV_STAGE(32, 16); QV_STAGE(32, 8); QV_STAGE(32, 4); QV_STAGE(32, 2); QV_STAGE(32, 1);
+  QV_STAGE(64, 32); QV_STAGE(64, 16); QV_STAGE(64, 8); QV_STAGE(64, 4); QV_STAGE(64, 2); QV_STAGE(64, 1);
+#undef QV_STAGE
   return key;
 }
 
@@ -69,7 +133,7 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key) {
 // Input: slots 0..P-2 ascending (padded with kPadKey), slot P-1 descending.
 template <int P>
 __device__ __forceinline__ void wave_merge_asc(uint64_t (&b)[P]) {
-  const int lane = lane_id();
+  const int lane = opaque_lane();
 #pragma unroll
   for (int half = P / 2; half >= 1; half >>= 1) {
 #pragma unroll
@@ -82,15 +146,10 @@ __device__ __forceinline__ void wave_merge_asc(uint64_t (&b)[P]) {
       }
     }
   }
-#pragma unroll
-  for (int j = kWave / 2; j > 0; j >>= 1) {
-#pragma unroll
-    for (int s = 0; s < P; s++) {
-      uint64_t other = shfl_xor64(b[s], j);
-      bool lower = (lane & j) == 0;
-      b[s] = lower ? umin64(b[s], other) : umax64(b[s], other);
-    }
-  }
+#define QV_MSTAGE(J)                                       \
+  _Pragma("unroll") for (int s = 0; s < P; s++) b[s] = cx_step<J>(b[s], lane, true)
+  QV_MSTAGE(32); QV_MSTAGE(16); QV_MSTAGE(8); QV_MSTAGE(4); QV_MSTAGE(2); QV_MSTAGE(1);
+#undef QV_MSTAGE
 }
 
 // Per-query LUT in LDS: PQSearchData::init_query (src/shared/index/
@@ -164,12 +223,12 @@ __device__ __forceinline__ float elem_to_float(const uint8_t* rec, int i) {
 
 // Exact squared L2 in the reference's order: square_sum_32
 // (src/shared/common/gpu_primitives.cuh:26-44).  Lanes 0..31 accumulate the
-// dimensions l, l+32, ... with a fused multiply-add, then a shuffle-down tree
-// over 32 lanes; every lane receives lane 0's value.
+// dimensions l, l+32, ... with a fused multiply-add, then the shuffle-down
+// tree over 32 lanes; every lane receives lane 0's value.
 template <class T>
 __device__ __forceinline__ float exact_l2_ref(const uint8_t* __restrict__ rec,
                                               const float* __restrict__ qu_lds, int dim) {
-  const int lane = lane_id();
+  const int lane = opaque_lane();
   float val = 0.f;
   if (lane < 32) {
     for (int i = lane; i < dim; i += 32) {
@@ -177,9 +236,16 @@ __device__ __forceinline__ float exact_l2_ref(const uint8_t* __restrict__ rec,
       val = __fmaf_rn(diff, diff, val);
     }
   }
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) val += __shfl_down(val, off, 32);
-  return __shfl(val, 0);
+  // Shuffle-down tree: lane l adds lane l+off for off = 16, 8, 4, 2, 1.  Only
+  // lane 0's sum is returned, and it depends only on lanes l < off at each
+  // step, whose partners l+off are reached by swizzle (xor 16) and by DPP
+  // row_shl inside the first 16-lane row.
+  val += __uint_as_float(xor_lane32<16>(__float_as_uint(val), lane));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x108, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x104, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x102, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x101, 0xF, 0xF, false));
+  return read_lane_f32(val, 0);
 }
 
 // Stable top-k insert (retset_push_topk_le32, kernel_helpers.cuh:65-104,
@@ -187,12 +253,12 @@ __device__ __forceinline__ float exact_l2_ref(const uint8_t* __restrict__ rec,
 // entry <= value; the caller applies the fc < k || value < D[k-1] guard.
 __device__ __forceinline__ void topk_insert(float& td, int32_t& ti, int& fc, int k,
                                             float value, int32_t id) {
-  const int lane = lane_id();
+  const int lane = opaque_lane();
   uint64_t le = __ballot(lane < fc && td <= value);
   int pos = __popcll(le);
   int ns = fc < k ? fc + 1 : k;
-  float pd = __shfl_up(td, 1);
-  int32_t pi = __shfl_up(ti, 1);
+  float pd = lane_up1_f32(td);
+  int32_t pi = (int32_t)lane_up1_u32((uint32_t)ti);
   if (lane < ns) {
     if (lane == pos) {
       td = value;

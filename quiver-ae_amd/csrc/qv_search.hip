@@ -127,7 +127,7 @@ struct Query {
   // followed by persistent_visit_select_dualwarp (kernel_helpers.cuh:422-489).
   // Returns the selected next node or -1.
   __device__ int32_t hop(int32_t v) {
-    const int lane = lane_id();
+    const int lane = opaque_lane();
     const uint8_t* rec = record(v);
     const uint32_t* rec32 = reinterpret_cast<const uint32_t*>(rec + a.data_size);
     const int deg = (int)rec32[0];
@@ -145,7 +145,7 @@ struct Query {
     // Exact distance of v and the top-k insert (the reference's second warp).
     const float e = exact_l2_ref<T>(rec, qu, a.dim);
     last_e = e;
-    const float dlast = __shfl(td, a.topk - 1);
+    const float dlast = read_lane_f32(td, a.topk - 1);
     if (fc < a.topk || e < dlast) topk_insert(td, ti, fc, a.topk, e, v);
 
     // Sort the new candidates (descending) and merge with the beam.
@@ -167,29 +167,27 @@ struct Query {
     uint32_t prev_id = 0xffffffffu;
     int sel_pos = -1;
     uint64_t sel_key = 0;
-    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
     for (int s = 0; s < P; s++) {
       const int i = s * kWave + lane;
       const uint32_t id = key_id(b[s]);
-      uint32_t pid = (uint32_t)__shfl_up((int)id, 1);
+      uint32_t pid = lane_up1_u32(id);
       if (lane == 0) pid = prev_id;
       const bool valid = i < keep_n;
       const bool keep = valid && !(i > 0 && id == pid);
       const uint64_t km = __ballot(keep);
-      const int pos = base + __popcll(km & lt_mask);
+      const int pos = base + lanes_below(km);
       if (keep && pos < a.ef) beam[pos] = b[s];
       if (sel_pos < 0) {
         const uint64_t cm = __ballot(keep && pos < a.ef && key_unvisited(b[s]));
         if (cm) {
           const int l = __ffsll((long long)cm) - 1;
-          sel_pos = __shfl(pos, l);
-          sel_key = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(b[s] >> 32), l) << 32) |
-                    (uint32_t)__shfl((int)(uint32_t)b[s], l);
+          sel_pos = read_lane_i32(pos, l);
+          sel_key = read_lane_u64(b[s], l);
         }
       }
       base += __popcll(km);
-      prev_id = (uint32_t)__shfl((int)id, kWave - 1);
+      prev_id = read_lane_u32(id, kWave - 1);
     }
     sz = min(base, a.ef);
     int32_t next = -1;
@@ -203,7 +201,7 @@ struct Query {
 
   // persistent_select_next_no_compact (kernel_helpers.cuh:491-518).
   __device__ int32_t select_next_no_compact() {
-    const int lane = lane_id();
+    const int lane = opaque_lane();
     const int n = min(sz, a.ef);
     sz = n;
     if (n == 0) return -1;
@@ -215,8 +213,7 @@ struct Query {
       if (cm) {
         const int l = __ffsll((long long)cm) - 1;
         const int pos = s * kWave + l;
-        const uint64_t sk = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(k >> 32), l) << 32) |
-                            (uint32_t)__shfl((int)(uint32_t)k, l);
+        const uint64_t sk = read_lane_u64(k, l);
         if (lane == 0) beam[pos] = sk & ~1ull;
         __syncthreads();
         return (int32_t)key_id(sk);
@@ -266,7 +263,7 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
         }
       }
     }
-    qid = __shfl(qid, 0);
+    qid = read_lane_i32(qid, 0);
     if (qid < 0) break;
     if (a.t_start && lane == 0) a.t_start[qid] = wall_ticks();
 
@@ -288,8 +285,8 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
     bool stop = false;
     const bool gpr = a.early_exit == QV_EXIT_GPRUNING;
     auto check = [&]() -> bool {
-      const float top1 = __shfl(Q.td, 0);
-      const float topk = __shfl(Q.td, a.topk - 1);
+      const float top1 = read_lane_f32(Q.td, 0);
+      const float topk = read_lane_f32(Q.td, a.topk - 1);
       const bool improved = Q.fc > g.last_fc || top1 < g.last_top1 || topk < g.last_topk;
       if (step < a.warmup) g.no_improve = 0;
       else g.no_improve = improved ? 0 : g.no_improve + 1;
@@ -400,7 +397,7 @@ __global__ __launch_bounds__(256) void validate_kernel(const uint8_t* pages, int
     if (has && (int64_t)nb >= n) bits |= 2;
     uint64_t key = has ? (uint64_t)nb : ((1ull << 32) + (uint64_t)lane);
     key = wave_sort_desc(key);
-    const uint64_t up = (uint64_t)__shfl_up((long long)key, 1);
+    const uint64_t up = ((uint64_t)lane_up1_u32((uint32_t)(key >> 32)) << 32) | lane_up1_u32((uint32_t)key);
     if (lane > 0 && up == key) bits |= 4;
     const uint64_t any = __ballot(bits != 0);
     if (any) {
