@@ -178,6 +178,33 @@ __device__ __forceinline__ void build_lut_lds(const float* __restrict__ qc_lds,
   }
 }
 
+// Code row of MC bytes (MC % 16 == 0) held as MC/4 words.
+template <int MC>
+struct CodeRow {
+  uint32_t w[MC / 4 > 0 ? MC / 4 : 1];
+};
+
+template <int MC>
+__device__ __forceinline__ void adc_load(CodeRow<MC>& cr, const uint8_t* __restrict__ row) {
+  const uint4* r4 = reinterpret_cast<const uint4*>(row);
+#pragma unroll
+  for (int t = 0; t < MC / 16; t++) {
+    const uint4 v = r4[t];
+    cr.w[4 * t + 0] = v.x;
+    cr.w[4 * t + 1] = v.y;
+    cr.w[4 * t + 2] = v.z;
+    cr.w[4 * t + 3] = v.w;
+  }
+}
+
+template <int MC>
+__device__ __forceinline__ float adc_sum(const CodeRow<MC>& cr, const float* __restrict__ lut) {
+  float dist = 0.f;
+#pragma unroll
+  for (int j = 0; j < MC; j++) dist += lut[j * kPivots + (int)((cr.w[j >> 2] >> ((j & 3) * 8)) & 0xffu)];
+  return dist;
+}
+
 // Sequential fp32 ADC of one code row against an LDS LUT
 // (kernel_helpers.cuh:280-285): dist = 0; dist += LUT[j][code_j] for j = 0..M-1.
 template <int MC>
@@ -219,6 +246,47 @@ __device__ __forceinline__ float adc_row(const uint8_t* __restrict__ row,
 template <class T>
 __device__ __forceinline__ float elem_to_float(const uint8_t* rec, int i) {
   return (float)reinterpret_cast<const T*>(rec)[i];
+}
+
+// Elements lane + 32k (k < kVecPre) of a node vector, loaded into registers by
+// lanes 0..31 so the loads are in flight together with the neighbour list.
+constexpr int kVecPre = 4;
+
+template <class T>
+__device__ __forceinline__ void load_vec_pre(const uint8_t* __restrict__ rec, int dim, int lane,
+                                             float (&x)[kVecPre]) {
+#pragma unroll
+  for (int k = 0; k < kVecPre; k++) {
+    const int i = lane + 32 * k;
+    x[k] = (lane < 32 && i < dim) ? elem_to_float<T>(rec, i) : 0.f;
+  }
+}
+
+// exact_l2_ref with the first kVecPre elements of each lane taken from x.
+template <class T>
+__device__ __forceinline__ float exact_l2_pre(const float (&x)[kVecPre], const uint8_t* __restrict__ rec,
+                                              const float* __restrict__ qu_lds, int dim, int lane) {
+  float val = 0.f;
+  if (lane < 32) {
+#pragma unroll
+    for (int k = 0; k < kVecPre; k++) {
+      const int i = lane + 32 * k;
+      if (i < dim) {
+        const float diff = qu_lds[i] - x[k];
+        val = __fmaf_rn(diff, diff, val);
+      }
+    }
+    for (int i = lane + 32 * kVecPre; i < dim; i += 32) {
+      const float diff = qu_lds[i] - elem_to_float<T>(rec, i);
+      val = __fmaf_rn(diff, diff, val);
+    }
+  }
+  val += __uint_as_float(xor_lane32<16>(__float_as_uint(val), lane));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x108, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x104, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x102, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x101, 0xF, 0xF, false));
+  return read_lane_f32(val, 0);
 }
 
 // Exact squared L2 in the reference's order: square_sum_32

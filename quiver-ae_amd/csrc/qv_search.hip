@@ -123,6 +123,15 @@ struct Query {
     return a.pages + page * 4096 + slot * a.node_size;
   }
 
+  // Exact distance of v and the top-k insert (the reference's second warp).
+  __device__ __forceinline__ void exact_and_topk(int32_t v, const float (&xv)[kVecPre], const uint8_t* rec,
+                                                 int lane) {
+    const float e = exact_l2_pre<T>(xv, rec, qu, a.dim, lane);
+    last_e = e;
+    const float dlast = read_lane_f32(td, a.topk - 1);
+    if (fc < a.topk || e < dlast) topk_insert(td, ti, fc, a.topk, e, v);
+  }
+
   // One expansion of node v: persistent_merge_data (kernel_helpers.cuh:232-357)
   // followed by persistent_visit_select_dualwarp (kernel_helpers.cuh:422-489).
   // Returns the selected next node or -1.
@@ -130,23 +139,30 @@ struct Query {
     const int lane = opaque_lane();
     const uint8_t* rec = record(v);
     const uint32_t* rec32 = reinterpret_cast<const uint32_t*>(rec + a.data_size);
+    // Degree, neighbour slots (all max_m of them: they lie inside the record)
+    // and the vector elements are requested together.
     const int deg = (int)rec32[0];
+    const uint32_t nbr_raw = lane < a.max_m ? rec32[1 + lane] : 0u;
+    float xv[kVecPre];
+    load_vec_pre<T>(rec, a.dim, lane, xv);
     evals += deg;
     const bool has = lane < deg;
-    const uint32_t nbr = has ? rec32[1 + lane] : 0u;
+    const uint32_t nbr = has ? nbr_raw : 0u;
 
-    // ADC gather-sum over the neighbour's code row (LUT in LDS).
+    // ADC gather-sum over the neighbour's code row (LUT in LDS); the code rows
+    // are in flight while the exact distance of v is computed.
     uint64_t nkey = sentinel_key(lane);
-    if (has) {
-      const float d = adc_row<MC>(a.codes + (int64_t)nbr * a.num_chunks, lut, a.num_chunks);
-      nkey = make_key(d, nbr, false);
+    float d = 0.f;
+    if constexpr (MC > 0 && MC % 16 == 0) {
+      CodeRow<MC> cr;
+      if (has) adc_load<MC>(cr, a.codes + (int64_t)nbr * MC);
+      exact_and_topk(v, xv, rec, lane);
+      if (has) d = adc_sum<MC>(cr, lut);
+    } else {
+      if (has) d = adc_row<MC>(a.codes + (int64_t)nbr * a.num_chunks, lut, a.num_chunks);
+      exact_and_topk(v, xv, rec, lane);
     }
-
-    // Exact distance of v and the top-k insert (the reference's second warp).
-    const float e = exact_l2_ref<T>(rec, qu, a.dim);
-    last_e = e;
-    const float dlast = read_lane_f32(td, a.topk - 1);
-    if (fc < a.topk || e < dlast) topk_insert(td, ti, fc, a.topk, e, v);
+    if (has) nkey = make_key(d, nbr, false);
 
     // Sort the new candidates (descending) and merge with the beam.
     nkey = wave_sort_desc(nkey);
