@@ -129,6 +129,86 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key) {
   return key;
 }
 
+// Compare-exchange of one bitonic stage (partner lane ^ J) for an ascending
+// block when `up`.  Partners 16 and 32 apart are exchanged with the CDNA4
+// permlane swaps, which hand both lanes of a pair the keys (A, B) of the lane
+// with bit J clear and the lane with bit J set; the other distances use DPP or
+// swizzle through xor_lane64.
+template <int J>
+__device__ __forceinline__ uint64_t cx_stage(uint64_t key, int lane, bool up) {
+  if constexpr (J == 16 || J == 32) {
+    const uint32_t lo = (uint32_t)key, hi = (uint32_t)(key >> 32);
+    uint32_t alo, blo, ahi, bhi;
+    if constexpr (J == 16) {
+      const auto pl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+      const auto ph = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+      alo = pl[0]; blo = pl[1]; ahi = ph[0]; bhi = ph[1];
+    } else {
+      const auto pl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+      const auto ph = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+      alo = pl[0]; blo = pl[1]; ahi = ph[0]; bhi = ph[1];
+    }
+    const uint64_t A = ((uint64_t)ahi << 32) | alo;
+    const uint64_t B = ((uint64_t)bhi << 32) | blo;
+    const bool want_min = ((lane & J) == 0) == up;
+    return ((A < B) == want_min) ? A : B;
+  } else {
+    const uint64_t other = xor_lane64<J>(key, lane);
+    const bool lower = (lane & J) == 0;
+    return (lower == up) ? umin64(key, other) : umax64(key, other);
+  }
+}
+
+// Bitonic sort of one key per lane, ascending across the wave (keys distinct).
+__device__ __forceinline__ uint64_t wave_sort_asc(uint64_t key) {
+  const int lane = opaque_lane();
+#define QV_STAGE(K, J) key = cx_stage<J>(key, lane, (lane & (K)) == 0)
+  QV_STAGE(2, 1);
+  QV_STAGE(4, 2); QV_STAGE(4, 1);
+  QV_STAGE(8, 4); QV_STAGE(8, 2); QV_STAGE(8, 1);
+  QV_STAGE(16, 8); QV_STAGE(16, 4); QV_STAGE(16, 2); QV_STAGE(16, 1);
+  QV_STAGE(32, 16); QV_STAGE(32, 8); QV_STAGE(32, 4); QV_STAGE(32, 2); QV_STAGE(32, 1);
+  QV_STAGE(64, 32); QV_STAGE(64, 16); QV_STAGE(64, 8); QV_STAGE(64, 4); QV_STAGE(64, 2); QV_STAGE(64, 1);
+#undef QV_STAGE
+  return key;
+}
+
+// Inclusive prefix sum over the 64 lanes (DPP row shifts, then row broadcasts).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);  // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true);  // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true);  // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true);  // row_shr:8
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false); // row_bcast:15
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false); // row_bcast:31
+  return v;
+}
+
+// Rank of a candidate key c1 (visited bit set) in an ascending key array of
+// CAP = 8^LEVELS entries (LEVELS <= 3) whose unused tail holds kPadKey: the
+// number of entries below c1 when the visited bit is ignored, for ranks up to
+// CAP - 1.  An 8-ary search on the distance word (the high 32 bits), seven
+// independent LDS reads per level, then a walk over entries of equal distance
+// on the full key.  Every index read is at most CAP - 1.
+template <int LEVELS>
+__device__ __forceinline__ int beam_rank(const uint64_t* __restrict__ a, uint64_t c1) {
+  constexpr int CAP = LEVELS == 2 ? 64 : 512;
+  const uint32_t* hi = reinterpret_cast<const uint32_t*>(a) + 1;  // hi[2 i] = a[i] >> 32
+  const uint32_t cd = (uint32_t)(c1 >> 32);
+  int pos = 0;
+#pragma unroll
+  for (int lev = 0; lev < LEVELS; lev++) {
+    const int e = LEVELS - 1 - lev;
+    const int S = e == 0 ? 1 : (e == 1 ? 8 : 64);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 1; j <= 7; j++) cnt += hi[2 * (pos + j * S - 1)] < cd ? 1 : 0;
+    pos += cnt * S;
+  }
+  while (pos < CAP - 1 && (uint32_t)(a[pos] >> 32) == cd && (a[pos] | 1ull) < c1) pos++;
+  return pos;
+}
+
 // Bitonic merge of P slots (element i = s*64 + lane) into ascending order.
 // Input: slots 0..P-2 ascending (padded with kPadKey), slot P-1 descending.
 template <int P>

@@ -79,8 +79,11 @@ enum : int32_t { kErrSpinTimeout = 1 };
 
 // Dynamic LDS carve-up shared by the kernel and its launcher.
 struct LdsPlan {
-  int lut_off, qc_off, qu_off, beam_off, lanes_off, total;
+  int lut_off, qc_off, qu_off, beam_off, hist_off, lanes_off, total;
 };
+
+// Beam capacity in LDS: the search of beam_rank probes up to 8^LEVELS entries.
+__host__ __device__ constexpr int beam_cap(int P) { return P <= 2 ? 64 : 512; }
 
 __host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int P) {
   LdsPlan p;
@@ -89,7 +92,8 @@ __host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int P) {
   int dpad = (dim + 3) & ~3;
   p.qu_off = p.qc_off + dpad * 4;
   p.beam_off = (p.qu_off + dpad * 4 + 7) & ~7;
-  p.lanes_off = p.beam_off + (P - 1) * kWave * 8;
+  p.hist_off = p.beam_off + beam_cap(P) * 8;
+  p.lanes_off = p.hist_off + (P - 1) * kWave * 4;
   p.total = p.lanes_off + 16 * 4;
   return p;
 }
@@ -101,6 +105,7 @@ struct Query {
   float* qc;
   float* qu;
   uint64_t* beam;
+  uint32_t* hist;  // insertion counts per beam position, zero between hops
   int sz;        // beam size (ctx.size)
   float td;      // top-k entry of this lane
   int32_t ti;
@@ -115,6 +120,7 @@ struct Query {
     qc = reinterpret_cast<float*>(smem + pl.qc_off);
     qu = reinterpret_cast<float*>(smem + pl.qu_off);
     beam = reinterpret_cast<uint64_t*>(smem + pl.beam_off);
+    hist = reinterpret_cast<uint32_t*>(smem + pl.hist_off);
   }
 
   __device__ __forceinline__ const uint8_t* record(int32_t v) const {
@@ -164,55 +170,108 @@ struct Query {
     }
     if (has) nkey = make_key(d, nbr, false);
 
-    // Sort the new candidates (descending) and merge with the beam.
-    nkey = wave_sort_desc(nkey);
-    uint64_t b[P];
-#pragma unroll
-    for (int s = 0; s < P - 1; s++) {
-      const int i = s * kWave + lane;
-      b[s] = i < sz ? beam[i] : kPadKey;
-    }
-    b[P - 1] = nkey;
-    wave_merge_asc<P>(b);
+    return merge_select(nkey, has, lane);
+  }
 
-    // Keep min(sz + deg, 2 ef) (kernel_helpers.cuh:350), drop entries equal to
-    // their predecessor (:440-455), truncate to ef and take the first unvisited
-    // entry (:456-472).
-    const int keep_n = min(sz + deg, 2 * a.ef);
-    int base = 0;
-    uint32_t prev_id = 0xffffffffu;
-    int sel_pos = -1;
-    uint64_t sel_key = 0;
+  // persistent_merge_data's result after persistent_visit_select_dualwarp's
+  // compaction and truncation (kernel_helpers.cuh:288-357, 440-472), built by
+  // rank.  The reference places a candidate equal to a beam entry (same id,
+  // hence same distance) right after it (lower_bound + 1, :300-329) and the
+  // adjacent-id compaction then drops it; the min(sz + deg, 2 ef) cap (:350)
+  // only removes entries that sit at or beyond ef after compaction, since at
+  // most sz <= ef entries are compacted away.  So the new beam is the first ef
+  // entries of  beam  U  {candidates whose id is not in the beam}, in key
+  // order, and its first unvisited entry is taken and marked visited.
+  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool has, int lane) {
+    constexpr int Q = P - 1;                      // beam positions per lane in the scan
+    constexpr int LEVELS = P <= 2 ? 2 : 3;        // 8^LEVELS = beam_cap(P) >= (P - 1) * 64
+    const int ef = a.ef;
+    // Candidates at or above the last entry of a full beam end beyond ef.
+    const uint64_t last = sz >= ef ? beam[ef - 1] : ~0ull;
+    const bool rel = has && nkey < last;
+    const uint64_t relm = __ballot(rel);
+    const int nrel = __popcll(relm);
+
+    // Rank of each relevant candidate in the beam; equal to a beam entry = dup.
+    int r = 0;
+    bool valid = false;
+    if (nrel > 0 && rel) {
+      const uint64_t c1 = nkey | 1ull;
+      r = beam_rank<LEVELS>(beam, c1);
+      valid = (beam[r] | 1ull) != c1;
+    }
+    const uint64_t vm = __ballot(valid);
+
+    // Old beam, chunk-major: lane l holds positions [l Q, l Q + Q).
+    uint64_t ck[Q];
 #pragma unroll
-    for (int s = 0; s < P; s++) {
-      const int i = s * kWave + lane;
-      const uint32_t id = key_id(b[s]);
-      uint32_t pid = lane_up1_u32(id);
-      if (lane == 0) pid = prev_id;
-      const bool valid = i < keep_n;
-      const bool keep = valid && !(i > 0 && id == pid);
-      const uint64_t km = __ballot(keep);
-      const int pos = base + lanes_below(km);
-      if (keep && pos < a.ef) beam[pos] = b[s];
-      if (sel_pos < 0) {
-        const uint64_t cm = __ballot(keep && pos < a.ef && key_unvisited(b[s]));
-        if (cm) {
-          const int l = __ffsll((long long)cm) - 1;
-          sel_pos = read_lane_i32(pos, l);
-          sel_key = read_lane_u64(b[s], l);
-        }
+    for (int k = 0; k < Q; k++) {
+      const int pos = lane * Q + k;
+      ck[k] = pos < sz ? beam[pos] : kPadKey;
+    }
+    // First unvisited entry of the old beam (all entries before it are visited).
+    int u = INT32_MAX;
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      const uint64_t m = __ballot(lane * Q + k < sz && key_unvisited(ck[k]));
+      if (m) u = min(u, (__ffsll((long long)m) - 1) * Q + k);
+    }
+    const uint64_t bu = u < sz ? beam[u] : ~0ull;
+
+    if (vm == 0) {
+      if (u >= sz) {
+        __syncthreads();
+        return -1;
       }
-      base += __popcll(km);
-      prev_id = read_lane_u32(id, kWave - 1);
+      if (lane == 0) beam[u] = bu & ~1ull;
+      __syncthreads();
+      return (int32_t)key_id(bu);
     }
-    sz = min(base, a.ef);
-    int32_t next = -1;
-    if (sel_pos >= 0) {
-      if (lane == 0) beam[sel_pos] = sel_key & ~1ull;
-      next = (int32_t)key_id(sel_key);
-    }
+
+    // Insertion points inside the beam -> shift of every old entry.
+    if (valid && r < sz) atomicAdd(&hist[r], 1u);
     __syncthreads();
-    return next;
+    uint32_t sh[Q];
+    uint32_t run = 0;
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      run += hist[lane * Q + k];
+      sh[k] = run;
+    }
+    const uint32_t excl = wave_incl_scan(run) - run;
+    if (valid && r < sz) hist[r] = 0u;
+
+    // Rank among the surviving candidates (few per hop: most relevant
+    // candidates are already in the beam).
+    int t = 0;
+    for (uint64_t rest = vm; rest; rest &= rest - 1) {
+      const uint64_t c = read_lane_u64(nkey, __ffsll((long long)rest) - 1);
+      t += c < nkey ? 1 : 0;
+    }
+    // The smallest new candidate lands at its rank r0; an old unvisited entry
+    // below it keeps its position u.
+    const int l0 = __ffsll((long long)__ballot(valid && t == 0)) - 1;
+    const uint64_t kv0 = read_lane_u64(nkey, l0);
+    int selpos;
+    uint64_t selkey;
+    if (bu < kv0) {
+      selpos = u;
+      selkey = bu;
+    } else {
+      selpos = read_lane_i32(r, l0);
+      selkey = kv0;
+    }
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      const int pos = lane * Q + k;
+      const int g = pos + (int)(excl + sh[k]);
+      if (pos < sz && g < ef) beam[g] = g == selpos ? (ck[k] & ~1ull) : ck[k];
+    }
+    const int f = r + t;
+    if (valid && f < ef) beam[f] = f == selpos ? (nkey & ~1ull) : nkey;
+    sz = min(sz + __popcll(vm), ef);
+    __syncthreads();
+    return (int32_t)key_id(selkey);
   }
 
   // persistent_select_next_no_compact (kernel_helpers.cuh:491-518).
@@ -294,6 +353,8 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
     }
     __syncthreads();
     build_lut_lds(Q.qc, a.pivots_t, a.chunk_off, a.num_chunks, Q.lut);
+    for (int i = lane; i < (P - 1) * kWave; i += kWave) Q.hist[i] = 0u;
+    for (int i = lane; i < beam_cap(P); i += kWave) Q.beam[i] = kPadKey;
     __syncthreads();
 
     GPrune g;
