@@ -328,23 +328,34 @@ __device__ __forceinline__ float elem_to_float(const uint8_t* rec, int i) {
   return (float)reinterpret_cast<const T*>(rec)[i];
 }
 
-// Elements lane + 32k (k < kVecPre) of a node vector, loaded into registers by
-// lanes 0..31 so the loads are in flight together with the neighbour list.
+// Elements lane + 32k (k < kVecPre) of a node vector, requested into registers
+// by every lane with the index clamped into the vector (values of lanes >= 32
+// and of indexes >= dim are never used), so that no load sits behind a branch
+// and the loads stay in flight together with the neighbour list.
 constexpr int kVecPre = 4;
 
 template <class T>
+__device__ __forceinline__ uint32_t elem_raw(const uint8_t* rec, int i) {
+  if constexpr (sizeof(T) == 4) return reinterpret_cast<const uint32_t*>(rec)[i];
+  else return (uint32_t)rec[i];
+}
+
+template <class T>
+__device__ __forceinline__ float raw_to_float(uint32_t r) {
+  if constexpr (sizeof(T) == 4) return __uint_as_float(r);
+  else return (float)(T)(uint8_t)r;
+}
+
+template <class T>
 __device__ __forceinline__ void load_vec_pre(const uint8_t* __restrict__ rec, int dim, int lane,
-                                             float (&x)[kVecPre]) {
+                                             uint32_t (&x)[kVecPre]) {
 #pragma unroll
-  for (int k = 0; k < kVecPre; k++) {
-    const int i = lane + 32 * k;
-    x[k] = (lane < 32 && i < dim) ? elem_to_float<T>(rec, i) : 0.f;
-  }
+  for (int k = 0; k < kVecPre; k++) x[k] = elem_raw<T>(rec, min((lane & 31) + 32 * k, dim - 1));
 }
 
 // exact_l2_ref with the first kVecPre elements of each lane taken from x.
 template <class T>
-__device__ __forceinline__ float exact_l2_pre(const float (&x)[kVecPre], const uint8_t* __restrict__ rec,
+__device__ __forceinline__ float exact_l2_pre(const uint32_t (&x)[kVecPre], const uint8_t* __restrict__ rec,
                                               const float* __restrict__ qu_lds, int dim, int lane) {
   float val = 0.f;
   if (lane < 32) {
@@ -352,7 +363,7 @@ __device__ __forceinline__ float exact_l2_pre(const float (&x)[kVecPre], const u
     for (int k = 0; k < kVecPre; k++) {
       const int i = lane + 32 * k;
       if (i < dim) {
-        const float diff = qu_lds[i] - x[k];
+        const float diff = qu_lds[i] - raw_to_float<T>(x[k]);
         val = __fmaf_rn(diff, diff, val);
       }
     }

@@ -39,6 +39,8 @@ struct SearchArgs {
   const int32_t* chunk_off;
   int64_t num_points;
   int64_t nodes_per_page;
+  uint64_t npp_magic;              // page = (v * npp_magic) >> npp_shift, exact for 0 <= v < 2^31
+  int32_t npp_shift;
   int64_t node_size;
   int64_t data_size;
   int32_t dim;
@@ -98,6 +100,13 @@ __host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int P) {
   return p;
 }
 
+// Registers holding the start of a node record (see Query::fetch).
+struct NodeRec {
+  int deg;
+  uint32_t nbr;
+  uint32_t xv[kVecPre];  // raw vector elements (load_vec_pre)
+};
+
 template <class T, int P, int MC>
 struct Query {
   const SearchArgs& a;
@@ -124,13 +133,26 @@ struct Query {
   }
 
   __device__ __forceinline__ const uint8_t* record(int32_t v) const {
-    const int64_t page = (int64_t)v / a.nodes_per_page;
+    const int64_t page = (int64_t)(((uint64_t)(uint32_t)v * a.npp_magic) >> a.npp_shift);
     const int64_t slot = (int64_t)v - page * a.nodes_per_page;
     return a.pages + page * 4096 + slot * a.node_size;
   }
 
+  // Requests the parts of v's record a hop reads: degree, the max_m neighbour
+  // slots (inside the record) and the first vector elements.  Only vector
+  // loads are used, so waits on LDS traffic never wait for these.
+  __device__ __forceinline__ void fetch(int32_t v, int lane, NodeRec& nr) const {
+    const uint8_t* rec = record(v);
+    const uint32_t* rec32 = reinterpret_cast<const uint32_t*>(rec + a.data_size);
+    int z = 0;
+    asm volatile("" : "+v"(z));  // per-lane address: a vector load of the degree
+    nr.deg = (int)rec32[z];
+    nr.nbr = rec32[1 + min(lane, a.max_m - 1)];  // lanes >= max_m are masked by the degree
+    load_vec_pre<T>(rec, a.dim, lane, nr.xv);
+  }
+
   // Exact distance of v and the top-k insert (the reference's second warp).
-  __device__ __forceinline__ void exact_and_topk(int32_t v, const float (&xv)[kVecPre], const uint8_t* rec,
+  __device__ __forceinline__ void exact_and_topk(int32_t v, const uint32_t (&xv)[kVecPre], const uint8_t* rec,
                                                  int lane) {
     const float e = exact_l2_pre<T>(xv, rec, qu, a.dim, lane);
     last_e = e;
@@ -140,37 +162,35 @@ struct Query {
 
   // One expansion of node v: persistent_merge_data (kernel_helpers.cuh:232-357)
   // followed by persistent_visit_select_dualwarp (kernel_helpers.cuh:422-489).
-  // Returns the selected next node or -1.
-  __device__ int32_t hop(int32_t v) {
+  // nr holds v's record (fetch); with pf the selected next node's record is
+  // requested into nr as soon as it is known.  Returns the next node or -1.
+  __device__ int32_t hop(int32_t v, NodeRec& nr, bool pf) {
     const int lane = opaque_lane();
-    const uint8_t* rec = record(v);
-    const uint32_t* rec32 = reinterpret_cast<const uint32_t*>(rec + a.data_size);
-    // Degree, neighbour slots (all max_m of them: they lie inside the record)
-    // and the vector elements are requested together.
-    const int deg = (int)rec32[0];
-    const uint32_t nbr_raw = lane < a.max_m ? rec32[1 + lane] : 0u;
-    float xv[kVecPre];
-    load_vec_pre<T>(rec, a.dim, lane, xv);
+    const int deg = read_lane_i32(nr.deg, 0);
     evals += deg;
     const bool has = lane < deg;
-    const uint32_t nbr = has ? nbr_raw : 0u;
+    const uint32_t nbr = has ? nr.nbr : 0u;
+    uint32_t xv[kVecPre];
+#pragma unroll
+    for (int k = 0; k < kVecPre; k++) xv[k] = nr.xv[k];
+    const uint8_t* rec = a.dim > 32 * kVecPre ? record(v) : nullptr;
 
     // ADC gather-sum over the neighbour's code row (LUT in LDS); the code rows
     // are in flight while the exact distance of v is computed.
-    uint64_t nkey = sentinel_key(lane);
-    float d = 0.f;
+    // Lanes without a neighbour read code row 0 and discard the sum.
+    float d;
     if constexpr (MC > 0 && MC % 16 == 0) {
       CodeRow<MC> cr;
-      if (has) adc_load<MC>(cr, a.codes + (int64_t)nbr * MC);
+      adc_load<MC>(cr, a.codes + (int64_t)nbr * MC);
       exact_and_topk(v, xv, rec, lane);
-      if (has) d = adc_sum<MC>(cr, lut);
+      d = adc_sum<MC>(cr, lut);
     } else {
-      if (has) d = adc_row<MC>(a.codes + (int64_t)nbr * a.num_chunks, lut, a.num_chunks);
+      d = adc_row<MC>(a.codes + (int64_t)nbr * a.num_chunks, lut, a.num_chunks);
       exact_and_topk(v, xv, rec, lane);
     }
-    if (has) nkey = make_key(d, nbr, false);
+    const uint64_t nkey = has ? make_key(d, nbr, false) : sentinel_key(lane);
 
-    return merge_select(nkey, has, lane);
+    return merge_select(nkey, has, lane, nr, pf);
   }
 
   // persistent_merge_data's result after persistent_visit_select_dualwarp's
@@ -182,7 +202,7 @@ struct Query {
   // most sz <= ef entries are compacted away.  So the new beam is the first ef
   // entries of  beam  U  {candidates whose id is not in the beam}, in key
   // order, and its first unvisited entry is taken and marked visited.
-  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool has, int lane) {
+  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool has, int lane, NodeRec& nr, bool pf) {
     constexpr int Q = P - 1;                      // beam positions per lane in the scan
     constexpr int LEVELS = P <= 2 ? 2 : 3;        // 8^LEVELS = beam_cap(P) >= (P - 1) * 64
     const int ef = a.ef;
@@ -223,23 +243,11 @@ struct Query {
         __syncthreads();
         return -1;
       }
+      if (pf) fetch((int32_t)key_id(bu), lane, nr);
       if (lane == 0) beam[u] = bu & ~1ull;
       __syncthreads();
       return (int32_t)key_id(bu);
     }
-
-    // Insertion points inside the beam -> shift of every old entry.
-    if (valid && r < sz) atomicAdd(&hist[r], 1u);
-    __syncthreads();
-    uint32_t sh[Q];
-    uint32_t run = 0;
-#pragma unroll
-    for (int k = 0; k < Q; k++) {
-      run += hist[lane * Q + k];
-      sh[k] = run;
-    }
-    const uint32_t excl = wave_incl_scan(run) - run;
-    if (valid && r < sz) hist[r] = 0u;
 
     // Rank among the surviving candidates (few per hop: most relevant
     // candidates are already in the beam).
@@ -261,6 +269,21 @@ struct Query {
       selpos = read_lane_i32(r, l0);
       selkey = kv0;
     }
+    if (pf) fetch((int32_t)key_id(selkey), lane, nr);
+
+    // Insertion points inside the beam -> shift of every old entry.
+    if (valid && r < sz) atomicAdd(&hist[r], 1u);
+    __syncthreads();
+    uint32_t sh[Q];
+    uint32_t run = 0;
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      run += hist[lane * Q + k];
+      sh[k] = run;
+    }
+    const uint32_t excl = wave_incl_scan(run) - run;
+    if (valid && r < sz) hist[r] = 0u;
+
 #pragma unroll
     for (int k = 0; k < Q; k++) {
       const int pos = lane * Q + k;
@@ -269,7 +292,7 @@ struct Query {
     }
     const int f = r + t;
     if (valid && f < ef) beam[f] = f == selpos ? (nkey & ~1ull) : nkey;
-    sz = min(sz + __popcll(vm), ef);
+    sz = min(sz + (int)__popcll(vm), ef);
     __syncthreads();
     return (int32_t)key_id(selkey);
   }
@@ -380,8 +403,20 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
       }
     };
 
+    // With one pipe lane the node selected by a hop is the next one expanded,
+    // so its record is requested while the hop finishes.
+    const bool pf = a.pipe_w == 1;
+    NodeRec nr;
+    int32_t nr_node = -1;
+    auto expand = [&](int32_t v) -> int32_t {
+      if (v != nr_node) Q.fetch(v, lane, nr);
+      const int32_t nx = Q.hop(v, nr, pf);
+      nr_node = pf ? nx : -1;
+      return nx;
+    };
+
     // ---- boot (kernel_q1.cuh:199-397)
-    int32_t first = Q.hop(a.medoid);
+    int32_t first = expand(a.medoid);
     log_hop(a.medoid);
     step = 1;
     if (check()) {
@@ -407,7 +442,7 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
       for (int w = 0; w < W; w++) {
         if (!(cur & (1u << w))) continue;
         const int32_t v = lane_node[w];
-        int32_t nx = Q.hop(v);
+        int32_t nx = expand(v);
         log_hop(v);
         ++step;
         if (check()) {
@@ -718,6 +753,20 @@ int slots_per_cu(qv_index* ix, int ef) {
   return nb;
 }
 
+// page = floor(v / npp) as (v * m) >> k with k = 32 + ceil(log2 npp) and
+// m = ceil(2^k / npp): the error term v (m npp - 2^k) / (npp 2^k) stays below
+// 1 / (2 npp) for v < 2^31, so the quotient is exact for every node id.
+static void set_page_divisor(SearchArgs& a, int64_t npp) {
+  if (npp < 1 || npp > 4096) fail(QV_EINDEX, "nodes per page out of range");
+  int l = 0;
+  while ((int64_t(1) << l) < npp) ++l;
+  const int k = 32 + l;
+  a.npp_magic = ((uint64_t(1) << k) + (uint64_t)npp - 1) / (uint64_t)npp;
+  a.npp_shift = k;
+  for (uint64_t v : {uint64_t(0), uint64_t(npp - 1), uint64_t(npp), uint64_t(INT32_MAX - 1), uint64_t(INT32_MAX)})
+    if (((v * a.npp_magic) >> k) != v / (uint64_t)npp) fail(QV_EINDEX, "page divisor check failed");
+}
+
 static SearchArgs base_args(qv_index* ix) {
   const Layout& L = ix->lay;
   SearchArgs a{};
@@ -728,6 +777,7 @@ static SearchArgs base_args(qv_index* ix) {
   a.chunk_off = ix->d_chunk_off;
   a.num_points = L.num_data;
   a.nodes_per_page = L.nodes_per_page;
+  set_page_divisor(a, L.nodes_per_page);
   a.node_size = L.node_size;
   a.data_size = L.data_size;
   a.dim = (int32_t)L.num_dims;
