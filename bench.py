@@ -250,11 +250,23 @@ def adc_leg(_lib, L, ncodes: int, log) -> dict:
     alg = evals * (M + 4) + nq * M * 256 * 4
     gbs = alg / (ms * 1e-3) / 1e9
     log(f"adc: {ms:.3f} ms, {gbs:.0f} GB/s algorithmic, {evals / ms / 1e6:.1f} G evals/s")
+    # the same rows fetched with nothing else: the device's random 32-byte row rate
+    fold = _lib.DeviceBuffer((2 * evals + 255) // 256 * 4)
+    gt = []
+    for _ in range(4):
+        gms = C.c_float()
+        _lib.check(L.qv_gather_bench(codes.ptr, ncodes, ids.ptr, evals, fold.ptr, 0, C.byref(gms)))
+        gt.append(gms.value)
+    gms = float(np.median(gt[1:]))
+    fold.close()
+    log(f"gather alone: {gms:.3f} ms, {evals / gms / 1e6:.1f} G rows/s; ADC at {gms / ms:.1%} of that rate")
     codes.close()
     ids.close()
     return {"kernel": "adc_bench_kernel", "codes": ncodes, "M": M, "queries": nq, "ids_per_query": per_q,
             "kernel_ms": round(ms, 4), "bytes_per_launch": int(alg), "achieved_gbs": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "evals_per_s": round(evals / (ms * 1e-3), 1)}
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "evals_per_s": round(evals / (ms * 1e-3), 1),
+            "gather_alone_ms": round(gms, 4), "gather_alone_rows_per_s": round(evals / (gms * 1e-3), 1),
+            "frac_of_gather_alone": round(gms / ms, 4)}
 
 
 def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, d_ids, nq, seconds: float) -> dict:

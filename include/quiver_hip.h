@@ -189,6 +189,15 @@ int qv_adc_bench(const float* d_luts, int32_t num_chunks, const uint8_t* d_codes
                  float* d_out_dists, double* d_dist_sums, int device,
                  float* elapsed_ms);
 
+/* Random row gather alone (no reference counterpart; a measurement aid): reads
+ * the 32-byte rows d_rows[d_ids[i]] for i < n exactly as qv_adc_bench fetches
+ * code rows (lane pairs, one 32-byte access per row) and XOR-folds them into
+ * d_fold[ceil(2 n / 256)] (one word per 256-thread workgroup).  Ids are clamped
+ * into [0, num_rows).  Its rows per second bound the ADC gather from above on
+ * the device at hand.  elapsed_ms (may be NULL) receives the kernel time. */
+int qv_gather_bench(const uint8_t* d_rows, int64_t num_rows, const int32_t* d_ids,
+                    int64_t n, uint32_t* d_fold, int device, float* elapsed_ms);
+
 /* Counter-based fills for synthetic tables: 8-byte word w of the buffer is a
  * function of (seed, w) only; id i is uniform in [0, num_codes) and a function
  * of (seed, i) only. */

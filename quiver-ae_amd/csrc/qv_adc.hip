@@ -102,16 +102,42 @@ struct Rows {
   u32x4 v[PER][MC / 16];
 };
 
+// Code rows of one step.  32-byte rows are fetched by lane pairs: in each load
+// instruction the even lane reads the first and the odd lane the second half of
+// the same row, so every row is one 32-byte access of one instruction (random
+// rows cost one cache-line access each instead of two); a DPP swap inside the
+// pair then gives each lane its own full row.  Other widths load whole rows per
+// lane.  Rows outside [0, last_row] are never read: padding lanes load row 0.
 template <int MC, int PER>
 __device__ __forceinline__ void load_rows(Rows<MC, PER>& rw, const uint8_t* __restrict__ codes, const i32x4& id,
                                           int64_t last_row) {
+  if constexpr (MC == 32) {
+    const bool odd = lane_id() & 1;
 #pragma unroll
-  for (int u = 0; u < PER; u++) {
-    // rows outside [0, last_row] are never read: padding lanes load row 0
-    const int64_t row = min((int64_t)(id[u] < 0 ? 0 : id[u]), last_row);
-    const u32x4* r = reinterpret_cast<const u32x4*>(codes + row * MC);
+    for (int u = 0; u < PER; u++) {
+      const int32_t row = (int32_t)min((int64_t)(id[u] < 0 ? 0 : id[u]), last_row);
+      const int32_t prow = __builtin_amdgcn_update_dpp(0, row, 0xB1, 0xF, 0xF, false);  // partner lane's row
+      const int64_t re = odd ? prow : row;  // the even lane's row
+      const int64_t ro = odd ? row : prow;  // the odd lane's row
+      const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(codes + re * 32) + (odd ? 1 : 0));
+      const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(codes + ro * 32) + (odd ? 1 : 0));
+      u32x4 sa, sb;
 #pragma unroll
-    for (int t = 0; t < MC / 16; t++) rw.v[u][t] = __builtin_nontemporal_load(r + t);
+      for (int c = 0; c < 4; c++) {
+        sa[c] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a[c], 0xB1, 0xF, 0xF, false);
+        sb[c] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)b[c], 0xB1, 0xF, 0xF, false);
+      }
+      rw.v[u][0] = odd ? sb : a;
+      rw.v[u][1] = odd ? b : sa;
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+      const int64_t row = min((int64_t)(id[u] < 0 ? 0 : id[u]), last_row);
+      const u32x4* r = reinterpret_cast<const u32x4*>(codes + row * MC);
+#pragma unroll
+      for (int t = 0; t < MC / 16; t++) rw.v[u][t] = __builtin_nontemporal_load(r + t);
+    }
   }
 }
 
@@ -128,7 +154,7 @@ __device__ __forceinline__ float adc_regs(const u32x4 (&w)[MC / 16], const float
 }
 
 // One workgroup per query.  Code rows of the next step are requested before the
-// current step is summed, so every wave keeps two steps of 16-byte loads in flight.
+// current step is summed, so every wave keeps two steps of row loads in flight.
 template <int MC, int PER>
 __global__ __launch_bounds__(kAdcWaves * 64) void adc_bench_kernel(
     const float* __restrict__ luts, int M, const uint8_t* __restrict__ codes,
@@ -213,6 +239,27 @@ __global__ __launch_bounds__(kAdcWaves * 64) void adc_bench_kernel(
       dist_sums[q] = t;
     }
   }
+}
+
+// Random 32-byte row gather with nothing else: lane pairs read the two halves
+// of row ids[i] in one instruction, as the ADC kernel does, and XOR-fold them
+// into one word per workgroup.  Its row rate is the ceiling of the ADC gather.
+__global__ __launch_bounds__(256) void gather_kernel(const uint8_t* __restrict__ rows, int64_t last_row,
+                                                     const int32_t* __restrict__ ids, int64_t n,
+                                                     uint32_t* __restrict__ fold) {
+  __shared__ uint32_t part[4];
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t i = t >> 1;
+  uint32_t x = 0;
+  if (i < n) {
+    const int64_t row = min((int64_t)max(ids[i], 0), last_row);
+    const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rows + row * 32) + (t & 1));
+    x = a[0] ^ a[1] ^ a[2] ^ a[3];
+  }
+  for (int off = 32; off > 0; off >>= 1) x ^= (uint32_t)__shfl_xor((int)x, off);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) fold[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
 }
 
 // Device-to-device copy of 16-byte words (grid-stride); also the reference
@@ -326,6 +373,31 @@ int qv_adc_bench(const float* d_luts, int32_t M, const uint8_t* d_codes, int64_t
     HIP_OK(hipEventRecord(e0, 0));
     hipLaunchKernelGGL(k, dim3((unsigned)nq), dim3(kAdcWaves * 64), lds, 0, d_luts, M, d_codes, num_codes, d_ids,
                        ids_per_query, topk, d_out_ids, d_out_dists, d_dist_sums);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipEventRecord(e1, 0));
+    HIP_OK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (elapsed_ms) *elapsed_ms = ms;
+  });
+}
+
+int qv_gather_bench(const uint8_t* d_rows, int64_t num_rows, const int32_t* d_ids, int64_t n, uint32_t* d_fold,
+                    int device, float* elapsed_ms) {
+  return qv::guard([&] {
+    if (!d_rows || !d_ids || !d_fold || num_rows <= 0 || n <= 0 || n > ((int64_t)1 << 36))
+      qv::fail(QV_EINVAL, "bad argument");
+    if ((reinterpret_cast<uintptr_t>(d_rows) & 15) != 0) qv::fail(QV_EINVAL, "rows must be 16-byte aligned");
+    HIP_OK(hipSetDevice(device));
+    const int64_t blocks = (2 * n + 255) / 256;
+    if (blocks > INT32_MAX) qv::fail(QV_EINVAL, "too many rows");
+    hipEvent_t e0, e1;
+    HIP_OK(hipEventCreate(&e0));
+    HIP_OK(hipEventCreate(&e1));
+    HIP_OK(hipEventRecord(e0, 0));
+    hipLaunchKernelGGL(gather_kernel, dim3((unsigned)blocks), dim3(256), 0, 0, d_rows, num_rows - 1, d_ids, n, d_fold);
     HIP_OK(hipGetLastError());
     HIP_OK(hipEventRecord(e1, 0));
     HIP_OK(hipEventSynchronize(e1));

@@ -264,9 +264,12 @@ struct CodeRow {
   uint32_t w[MC / 4 > 0 ? MC / 4 : 1];
 };
 
+// Code row `row` (of MC bytes, MC % 16 == 0) of the table `codes` into this
+// lane's registers.  Each lane loads its own row: in the latency-bound search a
+// row waits for one load of its own only.
 template <int MC>
-__device__ __forceinline__ void adc_load(CodeRow<MC>& cr, const uint8_t* __restrict__ row) {
-  const uint4* r4 = reinterpret_cast<const uint4*>(row);
+__device__ __forceinline__ void adc_load(CodeRow<MC>& cr, const uint8_t* __restrict__ codes, uint32_t row) {
+  const uint4* r4 = reinterpret_cast<const uint4*>(codes + (int64_t)row * MC);
 #pragma unroll
   for (int t = 0; t < MC / 16; t++) {
     const uint4 v = r4[t];

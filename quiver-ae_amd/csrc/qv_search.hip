@@ -181,7 +181,7 @@ struct Query {
     float d;
     if constexpr (MC > 0 && MC % 16 == 0) {
       CodeRow<MC> cr;
-      adc_load<MC>(cr, a.codes + (int64_t)nbr * MC);
+      adc_load<MC>(cr, a.codes, nbr);
       exact_and_topk(v, xv, rec, lane);
       d = adc_sum<MC>(cr, lut);
     } else {

@@ -140,6 +140,7 @@ SIGNATURES = {
     "qv_lut_build_raw": (_I32, [_P, _P, _P, _I32, _I32, _P, _I64, _P, _P, C.c_int]),
     "qv_adc_bench": (_I32, [_P, _I32, _P, _I64, _P, _I64, _I64, _I32, _P, _P, _P, C.c_int,
                             C.POINTER(C.c_float)]),
+    "qv_gather_bench": (_I32, [_P, _I64, _P, _I64, _P, C.c_int, C.POINTER(C.c_float)]),
     "qv_fill_uniform_bytes": (_I32, [_P, _I64, C.c_uint64, C.c_int]),
     "qv_fill_uniform_ids": (_I32, [_P, _I64, _I64, C.c_uint64, C.c_int]),
     "qv_build_params_default": (None, [C.POINTER(BuildParams)]),

@@ -154,6 +154,29 @@ def test_adc_bench_matches_oracle(lib, M):
         assert abs(gs[i] - osum) <= 1e-9 * abs(osum)
 
 
+def test_gather_bench_fold(lib):
+    from quiver import _lib
+
+    _say("[gpu] gather bench fold")
+    rng = np.random.default_rng(9)
+    nrows, n = 5000, 64 * 300 + 37
+    rows = rng.integers(0, 2**32, (nrows, 8), dtype=np.uint32)
+    ids = rng.integers(0, nrows, n, dtype=np.int32)
+    nblk = (2 * n + 255) // 256
+    dr = _lib.DeviceBuffer(rows.nbytes).upload(rows)
+    di = _lib.DeviceBuffer(ids.nbytes).upload(ids)
+    df = _lib.DeviceBuffer(nblk * 4)
+    ms = C.c_float(0)
+    _lib.check(_lib.load().qv_gather_bench(dr.ptr, nrows, di.ptr, n, df.ptr, 0, C.byref(ms)))
+    got = df.download(np.uint32, (nblk,))
+    # workgroup b covers ids [128 b, 128 b + 128): the XOR of all words of those rows
+    want = np.zeros(nblk, np.uint32)
+    for b in range(nblk):
+        sel = rows[ids[128 * b: 128 * b + 128]]
+        want[b] = np.bitwise_xor.reduce(sel.reshape(-1)) if sel.size else 0
+    np.testing.assert_array_equal(got, want)
+
+
 def test_mixture_device_matches_host(lib):
     import quiver
     from quiver import _lib
