@@ -173,6 +173,23 @@ __device__ __forceinline__ uint64_t wave_sort_asc(uint64_t key) {
   return key;
 }
 
+// Minimum of one 64-bit value per lane, returned to every lane.
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t x) {
+  const int lane = opaque_lane();
+  x = umin64(x, xor_lane64<1>(x, lane));
+  x = umin64(x, xor_lane64<2>(x, lane));
+  x = umin64(x, xor_lane64<4>(x, lane));
+  x = umin64(x, xor_lane64<8>(x, lane));
+  const uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
+  const auto pl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+  const auto ph = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+  x = umin64(((uint64_t)ph[0] << 32) | pl[0], ((uint64_t)ph[1] << 32) | pl[1]);
+  const uint32_t lo2 = (uint32_t)x, hi2 = (uint32_t)(x >> 32);
+  const auto ql = __builtin_amdgcn_permlane32_swap(lo2, lo2, false, false);
+  const auto qh = __builtin_amdgcn_permlane32_swap(hi2, hi2, false, false);
+  return umin64(((uint64_t)qh[0] << 32) | ql[0], ((uint64_t)qh[1] << 32) | ql[1]);
+}
+
 // Inclusive prefix sum over the 64 lanes (DPP row shifts, then row broadcasts).
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);  // row_shr:1

@@ -71,6 +71,10 @@ struct SearchArgs {
   const int32_t* terminate;        // host-coherent, may be null
   int32_t* ring;                   // host-coherent completion ring, may be null
   uint64_t spin_limit_ticks;       // watchdog on feed waits (100 MHz ticks)
+  // per-workgroup membership bitmaps of the beam (bit v set <=> v in the beam),
+  // bits_words 32-bit words per workgroup, all zero between queries
+  uint32_t* bits;
+  int64_t bits_words;
   // optional record of expanded nodes (graph construction)
   int32_t* rec_ids;
   float* rec_dists;
@@ -81,22 +85,18 @@ enum : int32_t { kErrSpinTimeout = 1 };
 
 // Dynamic LDS carve-up shared by the kernel and its launcher.
 struct LdsPlan {
-  int lut_off, qc_off, qu_off, beam_off, hist_off, lanes_off, total;
+  int lut_off, qc_off, qu_off, beam_off, total;
 };
 
-// Beam capacity in LDS: the search of beam_rank probes up to 8^LEVELS entries.
-__host__ __device__ constexpr int beam_cap(int P) { return P <= 2 ? 64 : 512; }
-
-__host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int P) {
+// Q = beam positions per lane: the beam holds up to Q * 64 >= ef entries.
+__host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q) {
   LdsPlan p;
   p.lut_off = 0;
   p.qc_off = p.lut_off + num_chunks * kPivots * 4;
   int dpad = (dim + 3) & ~3;
   p.qu_off = p.qc_off + dpad * 4;
   p.beam_off = (p.qu_off + dpad * 4 + 7) & ~7;
-  p.hist_off = p.beam_off + beam_cap(P) * 8;
-  p.lanes_off = p.hist_off + (P - 1) * kWave * 4;
-  p.total = p.lanes_off + 16 * 4;
+  p.total = p.beam_off + Q * kWave * 8;
   return p;
 }
 
@@ -107,15 +107,22 @@ struct NodeRec {
   uint32_t xv[kVecPre];  // raw vector elements (load_vec_pre)
 };
 
-template <class T, int P, int MC>
+template <class T, int Q, int MC>
 struct Query {
   const SearchArgs& a;
   float* lut;
   float* qc;
   float* qu;
   uint64_t* beam;
-  uint32_t* hist;  // insertion counts per beam position, zero between hops
+  uint32_t* bits;  // this workgroup's beam membership bitmap
   int sz;        // beam size (ctx.size)
+  // The beam in registers, chunk-major (lane l holds positions [l Q, l Q + Q),
+  // kPadKey at and beyond sz), and its first unvisited entry u with key bu
+  // (INT32_MAX and ~0 when every entry is visited).  LDS holds the same beam
+  // for the scatter of each merge.
+  uint64_t ck[Q];
+  int u;
+  uint64_t bu;
   float td;      // top-k entry of this lane
   int32_t ti;
   int fc;        // found count
@@ -123,13 +130,15 @@ struct Query {
   float last_e;  // exact distance of the node expanded by the last hop
 
   __device__ Query(const SearchArgs& args, char* smem)
-      : a(args), sz(0), td(__int_as_float(0x7f800000)), ti(-1), fc(0), evals(0) {
-    LdsPlan pl = lds_plan(a.num_chunks, a.dim, P);
+      : a(args), sz(0), u(INT32_MAX), bu(~0ull), td(__int_as_float(0x7f800000)), ti(-1), fc(0), evals(0) {
+#pragma unroll
+    for (int k = 0; k < Q; k++) ck[k] = kPadKey;
+    LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q);
     lut = reinterpret_cast<float*>(smem + pl.lut_off);
     qc = reinterpret_cast<float*>(smem + pl.qc_off);
     qu = reinterpret_cast<float*>(smem + pl.qu_off);
     beam = reinterpret_cast<uint64_t*>(smem + pl.beam_off);
-    hist = reinterpret_cast<uint32_t*>(smem + pl.hist_off);
+    bits = a.bits + (int64_t)blockIdx.x * a.bits_words;
   }
 
   __device__ __forceinline__ const uint8_t* record(int32_t v) const {
@@ -162,9 +171,10 @@ struct Query {
 
   // One expansion of node v: persistent_merge_data (kernel_helpers.cuh:232-357)
   // followed by persistent_visit_select_dualwarp (kernel_helpers.cuh:422-489).
-  // nr holds v's record (fetch); with pf the selected next node's record is
+  // nr holds v's record (fetch); with PF the selected next node's record is
   // requested into nr as soon as it is known.  Returns the next node or -1.
-  __device__ int32_t hop(int32_t v, NodeRec& nr, bool pf) {
+  template <bool PF>
+  __device__ __forceinline__ int32_t hop(int32_t v, NodeRec& nr) {
     const int lane = opaque_lane();
     const int deg = read_lane_i32(nr.deg, 0);
     evals += deg;
@@ -177,6 +187,12 @@ struct Query {
 
     // ADC gather-sum over the neighbour's code row (LUT in LDS); the code rows
     // are in flight while the exact distance of v is computed.
+    // Beam membership of each neighbour.  The bitmap updates of the previous
+    // hop were issued before this hop's record arrived; waiting for every
+    // outstanding vector memory operation here (the record is complete by
+    // now) orders them before these reads, which bypass the vector L1.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint32_t bword = __hip_atomic_load(bits + (nbr >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // Lanes without a neighbour read code row 0 and discard the sum.
     float d;
     if constexpr (MC > 0 && MC % 16 == 0) {
@@ -190,7 +206,41 @@ struct Query {
     }
     const uint64_t nkey = has ? make_key(d, nbr, false) : sentinel_key(lane);
 
-    return merge_select(nkey, has, lane, nr, pf);
+    const bool in_beam = (bword >> (nbr & 31)) & 1u;
+    return merge_select<PF>(nkey, has && !in_beam, lane, nr);
+  }
+
+  // Key at beam position pos (uniform) from the register copy.  Every chunk
+  // is read out and selected by value, so the copy is never indexed
+  // dynamically (which would move it to scratch memory).
+  __device__ __forceinline__ uint64_t beam_at(int pos) const {
+    const int kk = pos % Q, l = pos / Q;
+    uint64_t x = read_lane_u64(ck[0], l);
+#pragma unroll
+    for (int k = 1; k < Q; k++) {
+      const uint64_t v = read_lane_u64(ck[k], l);
+      x = kk == k ? v : x;
+    }
+    return x;
+  }
+
+  // First unvisited entry of the beam from the register copy.
+  __device__ __forceinline__ void find_unvisited(int lane) {
+    int first = INT32_MAX;
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      const uint64_t m = __ballot(lane * Q + k < sz && key_unvisited(ck[k]));
+      if (m) first = min(first, (__ffsll((long long)m) - 1) * Q + k);
+    }
+    u = first;
+    bu = first < sz ? beam_at(first) : ~0ull;
+  }
+
+  // Marks the entry at position pos visited (LDS and registers).
+  __device__ __forceinline__ void mark_visited(int pos, uint64_t key, int lane) {
+    if (lane == 0) beam[pos] = key & ~1ull;
+#pragma unroll
+    for (int k = 0; k < Q; k++) ck[k] &= lane * Q + k == pos ? ~1ull : ~0ull;
   }
 
   // persistent_merge_data's result after persistent_visit_select_dualwarp's
@@ -202,122 +252,116 @@ struct Query {
   // most sz <= ef entries are compacted away.  So the new beam is the first ef
   // entries of  beam  U  {candidates whose id is not in the beam}, in key
   // order, and its first unvisited entry is taken and marked visited.
-  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool has, int lane, NodeRec& nr, bool pf) {
-    constexpr int Q = P - 1;                      // beam positions per lane in the scan
-    constexpr int LEVELS = P <= 2 ? 2 : 3;        // 8^LEVELS = beam_cap(P) >= (P - 1) * 64
+  // fresh: lane holds a neighbour whose id is not in the beam (bitmap).
+  //
+  // The selected node only depends on the smallest surviving candidate and
+  // the old first unvisited entry, so it is found first and its record is
+  // requested (PF) before the rest of the merge, which then overlaps that load.
+  // There is one request site, so the loaded registers carry straight into
+  // the next hop (no copies that would wait for the load).
+  template <bool PF>
+  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool fresh, int lane, NodeRec& nr) {
     const int ef = a.ef;
     // Candidates at or above the last entry of a full beam end beyond ef.
-    const uint64_t last = sz >= ef ? beam[ef - 1] : ~0ull;
-    const bool rel = has && nkey < last;
-    const uint64_t relm = __ballot(rel);
-    const int nrel = __popcll(relm);
-
-    // Rank of each relevant candidate in the beam; equal to a beam entry = dup.
-    int r = 0;
-    bool valid = false;
-    if (nrel > 0 && rel) {
-      const uint64_t c1 = nkey | 1ull;
-      r = beam_rank<LEVELS>(beam, c1);
-      valid = (beam[r] | 1ull) != c1;
-    }
+    const uint64_t last = sz >= ef ? beam_at(ef - 1) : ~0ull;
+    const bool valid = fresh && nkey < last;
     const uint64_t vm = __ballot(valid);
 
-    // Old beam, chunk-major: lane l holds positions [l Q, l Q + Q).
-    uint64_t ck[Q];
+    if (vm == 0 && u >= sz) return -1;
+    // Smallest surviving candidate and its rank in the beam (entries below it
+    // with the visited bit ignored: e < c iff e < (c & ~1)).
+    int selpos = u;
+    uint64_t selkey = bu;
+    if (vm != 0) {
+      const uint64_t kv0 = wave_min_u64(valid ? nkey : ~0ull);
+      int r0 = 0;
+#pragma unroll
+      for (int k = 0; k < Q; k++) r0 += __popcll(__ballot(ck[k] < (kv0 & ~1ull)));
+      if (kv0 < bu) {
+        selpos = r0;
+        selkey = kv0;
+      }
+    }
+    if constexpr (PF) fetch((int32_t)key_id(selkey), lane, nr);
+    if (vm == 0) {
+      mark_visited(selpos, selkey, lane);
+      find_unvisited(lane);
+      return (int32_t)key_id(selkey);
+    }
+
+    // For each surviving candidate c (few per hop: most neighbours below the
+    // beam's end are already in it): its rank r in the beam, its rank t among
+    // the candidates, and the shift of every old entry at or above r.
+    int t = 0, r = 0;
+    uint32_t sh[Q];
+#pragma unroll
+    for (int k = 0; k < Q; k++) sh[k] = 0u;
+    for (uint64_t rest = vm; rest; rest &= rest - 1) {
+      const int l = __ffsll((long long)rest) - 1;
+      const uint64_t c = read_lane_u64(nkey, l);
+      const uint64_t c0 = c & ~1ull;
+      int rc = 0;
+#pragma unroll
+      for (int k = 0; k < Q; k++) rc += __popcll(__ballot(ck[k] < c0));
+      t += c < nkey ? 1 : 0;
+      if (lane == l) r = rc;
+#pragma unroll
+      for (int k = 0; k < Q; k++) sh[k] += lane * Q + k >= rc ? 1u : 0u;
+    }
+
+    // Scatter in place and keep the membership bitmap in step: entries pushed
+    // beyond ef leave it, inserted candidates join it.
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      const int pos = lane * Q + k;
+      const int g = pos + (int)sh[k];
+      if (pos < sz) {
+        if (g < ef) {
+          beam[g] = g == selpos ? (ck[k] & ~1ull) : ck[k];
+        } else {
+          const uint32_t id = key_id(ck[k]);
+          atomicAnd(bits + (id >> 5), ~(1u << (id & 31)));
+        }
+      }
+    }
+    const int f = r + t;
+    if (valid && f < ef) {
+      beam[f] = f == selpos ? (nkey & ~1ull) : nkey;
+      const uint32_t id = key_id(nkey);
+      atomicOr(bits + (id >> 5), 1u << (id & 31));
+    }
+    sz = min(sz + (int)__popcll(vm), ef);
+    // Register copy of the new beam (the wave's LDS accesses complete in order).
 #pragma unroll
     for (int k = 0; k < Q; k++) {
       const int pos = lane * Q + k;
       ck[k] = pos < sz ? beam[pos] : kPadKey;
     }
-    // First unvisited entry of the old beam (all entries before it are visited).
-    int u = INT32_MAX;
-#pragma unroll
-    for (int k = 0; k < Q; k++) {
-      const uint64_t m = __ballot(lane * Q + k < sz && key_unvisited(ck[k]));
-      if (m) u = min(u, (__ffsll((long long)m) - 1) * Q + k);
-    }
-    const uint64_t bu = u < sz ? beam[u] : ~0ull;
-
-    if (vm == 0) {
-      if (u >= sz) {
-        __syncthreads();
-        return -1;
-      }
-      if (pf) fetch((int32_t)key_id(bu), lane, nr);
-      if (lane == 0) beam[u] = bu & ~1ull;
-      __syncthreads();
-      return (int32_t)key_id(bu);
-    }
-
-    // Rank among the surviving candidates (few per hop: most relevant
-    // candidates are already in the beam).
-    int t = 0;
-    for (uint64_t rest = vm; rest; rest &= rest - 1) {
-      const uint64_t c = read_lane_u64(nkey, __ffsll((long long)rest) - 1);
-      t += c < nkey ? 1 : 0;
-    }
-    // The smallest new candidate lands at its rank r0; an old unvisited entry
-    // below it keeps its position u.
-    const int l0 = __ffsll((long long)__ballot(valid && t == 0)) - 1;
-    const uint64_t kv0 = read_lane_u64(nkey, l0);
-    int selpos;
-    uint64_t selkey;
-    if (bu < kv0) {
-      selpos = u;
-      selkey = bu;
-    } else {
-      selpos = read_lane_i32(r, l0);
-      selkey = kv0;
-    }
-    if (pf) fetch((int32_t)key_id(selkey), lane, nr);
-
-    // Insertion points inside the beam -> shift of every old entry.
-    if (valid && r < sz) atomicAdd(&hist[r], 1u);
-    __syncthreads();
-    uint32_t sh[Q];
-    uint32_t run = 0;
-#pragma unroll
-    for (int k = 0; k < Q; k++) {
-      run += hist[lane * Q + k];
-      sh[k] = run;
-    }
-    const uint32_t excl = wave_incl_scan(run) - run;
-    if (valid && r < sz) hist[r] = 0u;
-
-#pragma unroll
-    for (int k = 0; k < Q; k++) {
-      const int pos = lane * Q + k;
-      const int g = pos + (int)(excl + sh[k]);
-      if (pos < sz && g < ef) beam[g] = g == selpos ? (ck[k] & ~1ull) : ck[k];
-    }
-    const int f = r + t;
-    if (valid && f < ef) beam[f] = f == selpos ? (nkey & ~1ull) : nkey;
-    sz = min(sz + (int)__popcll(vm), ef);
-    __syncthreads();
+    find_unvisited(lane);
     return (int32_t)key_id(selkey);
   }
 
-  // persistent_select_next_no_compact (kernel_helpers.cuh:491-518).
-  __device__ int32_t select_next_no_compact() {
-    const int lane = opaque_lane();
-    const int n = min(sz, a.ef);
-    sz = n;
-    if (n == 0) return -1;
+  // Clears the bitmap bits of the final beam (bitmaps are zero between queries).
+  __device__ __forceinline__ void clear_bits(int lane) {
 #pragma unroll
-    for (int s = 0; s < P - 1; s++) {
-      const int i = s * kWave + lane;
-      const uint64_t k = i < n ? beam[i] : 0ull;
-      const uint64_t cm = __ballot(i < n && key_unvisited(k));
-      if (cm) {
-        const int l = __ffsll((long long)cm) - 1;
-        const int pos = s * kWave + l;
-        const uint64_t sk = read_lane_u64(k, l);
-        if (lane == 0) beam[pos] = sk & ~1ull;
-        __syncthreads();
-        return (int32_t)key_id(sk);
+    for (int k = 0; k < Q; k++) {
+      const int pos = lane * Q + k;
+      if (pos < sz) {
+        const uint32_t id = key_id(ck[k]);
+        atomicAnd(bits + (id >> 5), ~(1u << (id & 31)));
       }
     }
-    return -1;
+  }
+
+  // persistent_select_next_no_compact (kernel_helpers.cuh:491-518): the first
+  // unvisited entry (the beam never exceeds ef here) is taken and marked.
+  __device__ __forceinline__ int32_t select_next_no_compact() {
+    const int lane = opaque_lane();
+    if (u >= sz) return -1;
+    const uint64_t sel = bu;
+    mark_visited(u, sel, lane);
+    find_unvisited(lane);
+    return (int32_t)key_id(sel);
   }
 };
 
@@ -327,12 +371,11 @@ struct GPrune {
   float last_top1 = __int_as_float(0x7f800000), last_topk = __int_as_float(0x7f800000);
 };
 
-template <class T, int P, int MC>
+template <class T, int Q, int MC>
 __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
   extern __shared__ __align__(16) char smem[];
   const int lane = lane_id();
-  LdsPlan pl = lds_plan(a.num_chunks, a.dim, P);
-  int32_t* lane_node = reinterpret_cast<int32_t*>(smem + pl.lanes_off);
+  LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q);
 
   while (true) {
     // ---- acquire (StreamingDispatch, src/quiver/kernel_core/policies/dispatch.cuh:39-79)
@@ -365,19 +408,17 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
     if (qid < 0) break;
     if (a.t_start && lane == 0) a.t_start[qid] = wall_ticks();
 
-    Query<T, P, MC> Q(a, smem);
+    Query<T, Q, MC> Qy(a, smem);
     // ---- query into LDS: q - mu for the LUT, fl(fl(q - mu) + mu) for the exact
     // distance (pq_device.cuh:18-20, 33-35).
     const float* q = a.queries + (int64_t)qid * a.dim;
     for (int i = lane; i < a.dim; i += kWave) {
       const float c = q[i] - a.centroid[i];
-      Q.qc[i] = c;
-      Q.qu[i] = c + a.centroid[i];
+      Qy.qc[i] = c;
+      Qy.qu[i] = c + a.centroid[i];
     }
     __syncthreads();
-    build_lut_lds(Q.qc, a.pivots_t, a.chunk_off, a.num_chunks, Q.lut);
-    for (int i = lane; i < (P - 1) * kWave; i += kWave) Q.hist[i] = 0u;
-    for (int i = lane; i < beam_cap(P); i += kWave) Q.beam[i] = kPadKey;
+    build_lut_lds(Qy.qc, a.pivots_t, a.chunk_off, a.num_chunks, Qy.lut);
     __syncthreads();
 
     GPrune g;
@@ -385,12 +426,12 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
     bool stop = false;
     const bool gpr = a.early_exit == QV_EXIT_GPRUNING;
     auto check = [&]() -> bool {
-      const float top1 = read_lane_f32(Q.td, 0);
-      const float topk = read_lane_f32(Q.td, a.topk - 1);
-      const bool improved = Q.fc > g.last_fc || top1 < g.last_top1 || topk < g.last_topk;
+      const float top1 = read_lane_f32(Qy.td, 0);
+      const float topk = read_lane_f32(Qy.td, a.topk - 1);
+      const bool improved = Qy.fc > g.last_fc || top1 < g.last_top1 || topk < g.last_topk;
       if (step < a.warmup) g.no_improve = 0;
       else g.no_improve = improved ? 0 : g.no_improve + 1;
-      g.last_fc = Q.fc;
+      g.last_fc = Qy.fc;
       g.last_top1 = top1;
       g.last_topk = topk;
       return gpr && step >= a.warmup && a.patience > 0 && g.no_improve >= a.patience;
@@ -399,22 +440,36 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
     auto log_hop = [&](int32_t v) {
       if (a.rec_ids && lane == 0 && step < a.rec_cap) {
         a.rec_ids[(int64_t)qid * a.rec_cap + step] = v;
-        a.rec_dists[(int64_t)qid * a.rec_cap + step] = Q.last_e;
+        a.rec_dists[(int64_t)qid * a.rec_cap + step] = Qy.last_e;
       }
     };
 
-    // With one pipe lane the node selected by a hop is the next one expanded,
-    // so its record is requested while the hop finishes.
-    const bool pf = a.pipe_w == 1;
     NodeRec nr;
-    int32_t nr_node = -1;
     auto expand = [&](int32_t v) -> int32_t {
-      if (v != nr_node) Q.fetch(v, lane, nr);
-      const int32_t nx = Q.hop(v, nr, pf);
-      nr_node = pf ? nx : -1;
-      return nx;
+      Qy.fetch(v, lane, nr);
+      return Qy.template hop<false>(v, nr);
     };
 
+    if (a.pipe_w == 1) {
+      // One pipe lane (kernel_q1.cuh:199-397 boot, then 407-670): the node a
+      // hop selects is the next one expanded, so its record is requested while
+      // the hop finishes.
+      Qy.fetch(a.medoid, lane, nr);
+      int32_t v = a.medoid;
+      while (true) {
+        const int32_t nx = Qy.template hop<true>(v, nr);
+        log_hop(v);
+        ++step;
+        if (check()) {
+          stop = true;
+          break;
+        }
+        if (nx < 0) break;
+        v = nx;
+      }
+      goto finish;
+    }
+    {
     // ---- boot (kernel_q1.cuh:199-397)
     int32_t first = expand(a.medoid);
     log_hop(a.medoid);
@@ -423,25 +478,23 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
       stop = true;
       first = -1;
     }
+    // Lane w < W of pipe_node holds the node of pipe lane w (-1: idle).  The
+    // pipe state stays in registers: no LDS round trip and no barrier, whose
+    // memory fence would also wait for the record requested by the last hop.
     const int W = a.pipe_w;
-    uint32_t ready = 0;
-    if (lane == 0) lane_node[0] = first;
+    int32_t pipe_node = lane == 0 ? first : -1;
     for (int w = 1; w < W; w++) {
-      const int32_t nx = Q.select_next_no_compact();
-      if (lane == 0) lane_node[w] = nx;
+      const int32_t nx = Qy.select_next_no_compact();
+      pipe_node = lane == w ? nx : pipe_node;
     }
-    __syncthreads();
-    if (!stop) {
-      for (int w = 0; w < W; w++)
-        if (lane_node[w] != -1) ready |= 1u << w;
-    }
+    uint32_t ready = stop ? 0u : (uint32_t)__ballot(lane < W && pipe_node != -1);
 
     // ---- pipe loop, every issued lane served at once (kernel_q1.cuh:407-670)
     while (!stop && ready) {
       const uint32_t cur = ready;
       for (int w = 0; w < W; w++) {
         if (!(cur & (1u << w))) continue;
-        const int32_t v = lane_node[w];
+        const int32_t v = read_lane_i32(pipe_node, w);
         int32_t nx = expand(v);
         log_hop(v);
         ++step;
@@ -449,32 +502,30 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
           stop = true;
           nx = -1;
         }
-        __syncthreads();
-        if (lane == 0) lane_node[w] = nx;
-        __syncthreads();
+        pipe_node = lane == w ? nx : pipe_node;
       }
       if (stop) break;
       for (int w = 0; w < W; w++) {
         if (cur & (1u << w)) continue;
-        const int32_t nx = Q.select_next_no_compact();
-        if (lane == 0) lane_node[w] = nx;
+        const int32_t nx = Qy.select_next_no_compact();
+        pipe_node = lane == w ? nx : pipe_node;
       }
-      __syncthreads();
-      ready = 0;
-      for (int w = 0; w < W; w++)
-        if (lane_node[w] != -1) ready |= 1u << w;
+      ready = (uint32_t)__ballot(lane < W && pipe_node != -1);
+    }
     }
 
+  finish:
     // ---- finish (kernel_q1.cuh:684-704)
+    Qy.clear_bits(lane);
     if (lane < a.topk) {
-      a.out_ids[(int64_t)qid * a.topk + lane] = Q.ti;
-      a.out_dists[(int64_t)qid * a.topk + lane] = Q.td;
+      a.out_ids[(int64_t)qid * a.topk + lane] = Qy.ti;
+      a.out_dists[(int64_t)qid * a.topk + lane] = Qy.td;
     }
     if (lane == 0) {
-      if (a.out_found) a.out_found[qid] = Q.fc;
+      if (a.out_found) a.out_found[qid] = Qy.fc;
       if (a.out_hops) a.out_hops[qid] = step;
       if (a.out_stopped) a.out_stopped[qid] = stop ? 1 : 0;
-      if (a.out_evals) a.out_evals[qid] = Q.evals;
+      if (a.out_evals) a.out_evals[qid] = Qy.evals;
       if (a.t_end) a.t_end[qid] = wall_ticks();
       atomicAdd(&a.counters[1], 1);
       if (a.ring) {
@@ -525,27 +576,29 @@ __global__ __launch_bounds__(256) void validate_kernel(const uint8_t* pages, int
 
 using KernelFn = void (*)(SearchArgs);
 
-template <class T, int P>
+template <class T, int Q>
 KernelFn pick_mc(int M) {
-  if (M == 32) return search_kernel<T, P, 32>;
-  if (M == 48) return search_kernel<T, P, 48>;
-  return search_kernel<T, P, 0>;
+  if (M == 32) return search_kernel<T, Q, 32>;
+  if (M == 48) return search_kernel<T, Q, 48>;
+  return search_kernel<T, Q, 0>;
 }
 
 template <class T>
-KernelFn pick_p(int P, int M) {
-  if (P == 2) return pick_mc<T, 2>(M);
-  if (P == 4) return pick_mc<T, 4>(M);
-  return pick_mc<T, 8>(M);
+KernelFn pick_q(int Q, int M) {
+  if (Q == 1) return pick_mc<T, 1>(M);
+  if (Q == 2) return pick_mc<T, 2>(M);
+  if (Q == 4) return pick_mc<T, 4>(M);
+  return pick_mc<T, 7>(M);
 }
 
-KernelFn pick_kernel(int dtype, int P, int M) {
-  if (dtype == QV_UINT8) return pick_p<uint8_t>(P, M);
-  if (dtype == QV_INT8) return pick_p<int8_t>(P, M);
-  return pick_p<float>(P, M);
+KernelFn pick_kernel(int dtype, int Q, int M) {
+  if (dtype == QV_UINT8) return pick_q<uint8_t>(Q, M);
+  if (dtype == QV_INT8) return pick_q<int8_t>(Q, M);
+  return pick_q<float>(Q, M);
 }
 
-int merge_slots(int ef) { return ef <= 64 ? 2 : (ef <= 192 ? 4 : 8); }
+// Beam positions per lane for ef (beam capacity 64 Q >= ef; kMaxEf = 448 = 64 * 7).
+int beam_chunks(int ef) { return ef <= 64 ? 1 : (ef <= 128 ? 2 : (ef <= 256 ? 4 : 7)); }
 
 }  // namespace
 
@@ -571,6 +624,26 @@ static void free_scratch(qv_index* ix) {
   ix->h_ring = nullptr;
   ix->cap_q = 0;
   ix->cap_k = 0;
+}
+
+// Beam membership bitmaps, one per workgroup of the grid, zero between
+// queries (each query clears the bits of its final beam).  Reallocated when a
+// larger grid is launched and zeroed again after a search that did not finish.
+static void ensure_bits(qv_index* ix, int64_t slots) {
+  const int64_t words = ((ix->lay.num_data + 31) / 32 + 15) / 16 * 16;
+  if (slots > ix->bits_slots || words != ix->bits_words) {
+    hipFree(ix->d_bits);
+    ix->d_bits = nullptr;
+    ix->bits_slots = 0;
+    HIP_OK(hipMalloc(&ix->d_bits, sizeof(uint32_t) * (size_t)(slots * words)));
+    ix->bits_slots = slots;
+    ix->bits_words = words;
+    ix->bits_dirty = true;
+  }
+  if (ix->bits_dirty) {
+    HIP_OK(hipMemset(ix->d_bits, 0, sizeof(uint32_t) * (size_t)(ix->bits_slots * ix->bits_words)));
+    ix->bits_dirty = false;
+  }
 }
 
 static void ensure_scratch(qv_index* ix, int64_t nq, int k) {
@@ -604,6 +677,7 @@ void release_index(qv_index* ix) {
   free_scratch(ix);
   hipFree(ix->d_counters);
   hipHostFree(ix->h_ctrl);
+  hipFree(ix->d_bits);
   hipFree(ix->d_pages);
   hipFree(ix->d_codes);
   hipFree(ix->d_centroid);
@@ -741,7 +815,7 @@ qv_index* make_index(int device, const Layout& lay, const PQTables& pq, uint8_t*
 }
 
 int slots_per_cu(qv_index* ix, int ef) {
-  const int P = merge_slots(ef);
+  const int P = beam_chunks(ef);
   KernelFn k = pick_kernel(ix->lay.data_type, P, ix->M);
   const LdsPlan pl = lds_plan(ix->M, (int)ix->lay.num_dims, P);
   if (pl.total > 65536)
@@ -784,6 +858,8 @@ static SearchArgs base_args(qv_index* ix) {
   a.num_chunks = ix->M;
   a.max_m = (int32_t)L.max_m0;
   a.medoid = (int32_t)L.enter_point;
+  a.bits = ix->d_bits;
+  a.bits_words = ix->bits_words;
   return a;
 }
 
@@ -796,12 +872,13 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
   if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 448]");
   HIP_OK(hipSetDevice(ix->device));
   ensure_scratch(ix, nq, 1);
-  const int P = merge_slots(ef);
+  const int P = beam_chunks(ef);
   KernelFn kern = pick_kernel(ix->lay.data_type, P, ix->M);
   const LdsPlan pl = lds_plan(ix->M, (int)ix->lay.num_dims, P);
   const int spc = slots_per_cu(ix, ef);
   int nb = num_blocks > 0 ? num_blocks : spc * ix->num_cus;
   nb = (int)std::min<int64_t>(nb, nq);
+  ensure_bits(ix, nb);
   SearchArgs a = base_args(ix);
   a.queries = d_queries;
   a.nq = (int32_t)nq;
@@ -828,11 +905,13 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
   a.rec_dists = rec.dists;
   a.rec_cap = rec.cap;
   HIP_OK(hipMemsetAsync(ix->d_counters, 0, 64, ix->stream));
+  ix->bits_dirty = true;
   hipLaunchKernelGGL(kern, dim3(nb), dim3(64), (size_t)pl.total, ix->stream, a);
   HIP_OK(hipGetLastError());
   HIP_OK(hipStreamSynchronize(ix->stream));
   int32_t counters[4] = {0, 0, 0, 0};
   HIP_OK(hipMemcpy(counters, ix->d_counters, sizeof(counters), hipMemcpyDeviceToHost));
+  ix->bits_dirty = counters[1] < nq;  // conservative: zeroed again before the next launch
   if (counters[1] != nq)
     fail(QV_EHIP, "record search finished " + std::to_string(counters[1]) + " of " + std::to_string(nq) + " queries");
 }
@@ -864,13 +943,14 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
 
   HIP_OK(hipSetDevice(ix->device));
   ensure_scratch(ix, nq, topk);
-  const int P = merge_slots(ef);
+  const int P = beam_chunks(ef);
   KernelFn kern = pick_kernel(L.data_type, P, ix->M);
   const LdsPlan pl = lds_plan(ix->M, (int)L.num_dims, P);
   const int spc = slots_per_cu(ix, ef);
   if (spc <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
   const int num_blocks = o.num_blocks > 0 ? o.num_blocks : spc * ix->num_cus;
   const int max_inflight = (int)std::min<int64_t>(nq, (int64_t)num_blocks + std::max(0, o.prefeed));
+  ensure_bits(ix, num_blocks);
 
   const float* d_q = queries;
   if (!o.device_buffers) {
@@ -927,6 +1007,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   a.rec_cap = 0;
 
   using clock = std::chrono::steady_clock;
+  ix->bits_dirty = true;  // until every admitted query is seen to finish
   HIP_OK(hipEventRecord(ix->ev0, ix->stream));
   hipLaunchKernelGGL(kern, dim3(num_blocks), dim3(64), (size_t)pl.total, ix->stream, a);
   HIP_OK(hipGetLastError());
@@ -994,6 +1075,8 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
 
   int32_t counters[4] = {0, 0, 0, 0};
   HIP_OK(hipMemcpy(counters, ix->d_counters, sizeof(counters), hipMemcpyDeviceToHost));
+  // every query that took a ticket below nq ran to its end and cleared its bits
+  ix->bits_dirty = counters[1] < std::min<int64_t>(counters[0], nq);
   if (counters[2] & kErrSpinTimeout) fail(QV_ETIMEDOUT, "search kernel watchdog: feed wait exceeded its limit");
   if (timed_out || counters[1] < nq) {
     char buf[96];
