@@ -173,7 +173,7 @@ __device__ __forceinline__ uint64_t wave_sort_asc(uint64_t key) {
   return key;
 }
 
-// Minimum of one 64-bit value per lane, returned to every lane.
+// Minimum of one 64-bit value per lane, returned to every lane (uniform).
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t x) {
   const int lane = opaque_lane();
   x = umin64(x, xor_lane64<1>(x, lane));
@@ -187,7 +187,8 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t x) {
   const uint32_t lo2 = (uint32_t)x, hi2 = (uint32_t)(x >> 32);
   const auto ql = __builtin_amdgcn_permlane32_swap(lo2, lo2, false, false);
   const auto qh = __builtin_amdgcn_permlane32_swap(hi2, hi2, false, false);
-  return umin64(((uint64_t)qh[0] << 32) | ql[0], ((uint64_t)qh[1] << 32) | ql[1]);
+  // read back from lane 0 so the compiler sees a wave-uniform value
+  return read_lane_u64(umin64(((uint64_t)qh[0] << 32) | ql[0], ((uint64_t)qh[1] << 32) | ql[1]), 0);
 }
 
 // Inclusive prefix sum over the 64 lanes (DPP row shifts, then row broadcasts).

@@ -184,30 +184,37 @@ struct Query {
 #pragma unroll
     for (int k = 0; k < kVecPre; k++) xv[k] = nr.xv[k];
     const uint8_t* rec = a.dim > 32 * kVecPre ? record(v) : nullptr;
+    // With PF, the next node is most often the beam's first unvisited entry
+    // (whenever no new candidate beats it), so its record is requested right
+    // after this hop's code rows, and the merge only requests another record
+    // when a candidate wins.
+    const bool spec = PF && u < sz;
 
-    // ADC gather-sum over the neighbour's code row (LUT in LDS); the code rows
-    // are in flight while the exact distance of v is computed.
     // Beam membership of each neighbour.  The bitmap updates of the previous
     // hop were issued before this hop's record arrived; waiting for every
     // outstanding vector memory operation here (the record is complete by
     // now) orders them before these reads, which bypass the vector L1.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const uint32_t bword = __hip_atomic_load(bits + (nbr >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // Lanes without a neighbour read code row 0 and discard the sum.
+    // ADC gather-sum over the neighbour's code row (LUT in LDS); the code rows
+    // are in flight while the exact distance of v is computed.  Lanes without
+    // a neighbour read code row 0 and discard the sum.
     float d;
     if constexpr (MC > 0 && MC % 16 == 0) {
       CodeRow<MC> cr;
       adc_load<MC>(cr, a.codes, nbr);
+      if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
       exact_and_topk(v, xv, rec, lane);
       d = adc_sum<MC>(cr, lut);
     } else {
+      if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
       d = adc_row<MC>(a.codes + (int64_t)nbr * a.num_chunks, lut, a.num_chunks);
       exact_and_topk(v, xv, rec, lane);
     }
     const uint64_t nkey = has ? make_key(d, nbr, false) : sentinel_key(lane);
 
     const bool in_beam = (bword >> (nbr & 31)) & 1u;
-    return merge_select<PF>(nkey, has && !in_beam, lane, nr);
+    return merge_select<PF>(nkey, has && !in_beam, lane, nr, spec);
   }
 
   // Key at beam position pos (uniform) from the register copy.  Every chunk
@@ -256,11 +263,11 @@ struct Query {
   //
   // The selected node only depends on the smallest surviving candidate and
   // the old first unvisited entry, so it is found first and its record is
-  // requested (PF) before the rest of the merge, which then overlaps that load.
-  // There is one request site, so the loaded registers carry straight into
-  // the next hop (no copies that would wait for the load).
+  // requested (PF) before the rest of the merge, which then overlaps that load,
+  // unless it is the first unvisited entry whose record the hop requested at
+  // its start (spec).
   template <bool PF>
-  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool fresh, int lane, NodeRec& nr) {
+  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool fresh, int lane, NodeRec& nr, bool spec) {
     const int ef = a.ef;
     // Candidates at or above the last entry of a full beam end beyond ef.
     const uint64_t last = sz >= ef ? beam_at(ef - 1) : ~0ull;
@@ -282,7 +289,10 @@ struct Query {
         selkey = kv0;
       }
     }
-    if constexpr (PF) fetch((int32_t)key_id(selkey), lane, nr);
+    if constexpr (PF) {
+      // (the key test, not the position: a winning candidate lands at u too)
+      if (!(spec && selkey == bu)) fetch((int32_t)key_id(selkey), lane, nr);
+    }
     if (vm == 0) {
       mark_visited(selpos, selkey, lane);
       find_unvisited(lane);
@@ -428,10 +438,11 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
     auto check = [&]() -> bool {
       const float top1 = read_lane_f32(Qy.td, 0);
       const float topk = read_lane_f32(Qy.td, a.topk - 1);
-      const bool improved = Qy.fc > g.last_fc || top1 < g.last_top1 || topk < g.last_topk;
+      const int fc = read_lane_i32(Qy.fc, 0);  // equal in every lane; read as uniform
+      const bool improved = fc > g.last_fc || top1 < g.last_top1 || topk < g.last_topk;
       if (step < a.warmup) g.no_improve = 0;
       else g.no_improve = improved ? 0 : g.no_improve + 1;
-      g.last_fc = Qy.fc;
+      g.last_fc = fc;
       g.last_top1 = top1;
       g.last_topk = topk;
       return gpr && step >= a.warmup && a.patience > 0 && g.no_improve >= a.patience;
