@@ -57,6 +57,10 @@ def main() -> int:
     ap.add_argument("--ef", type=int, default=0, help="time this ef_search and skip the sweep")
     ap.add_argument("--policy", default="none", choices=("none", "gpruning"),
                     help="early-exit policy used with --ef")
+    ap.add_argument("--adc-only", action="store_true",
+                    help="run only the ADC microbenchmark leg (prints its JSON object)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="run one device-to-device copy of this size first (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1",
@@ -73,6 +77,17 @@ def main() -> int:
     mem = C.c_int64()
     _lib.check(L.qv_device_info(0, name, 64, C.byref(ncu), C.byref(mem)))
     log(f"device {name.value.decode()} CUs={ncu.value} mem={mem.value / 2**30:.0f} GiB")
+
+    if args.adc_only:
+        if args.copy_mib > 0:
+            nb = args.copy_mib << 20
+            src, dst = _lib.DeviceBuffer(nb), _lib.DeviceBuffer(nb)
+            _lib.check(L.qv_fill_uniform_bytes(src.ptr, nb, 7, 0))
+            _lib.check(L.qv_dev_copy(dst.ptr, src.ptr, nb, 2))
+            src.close()
+            dst.close()
+        print(json.dumps({"adc": adc_leg(_lib, L, args.adc_codes, log)}), flush=True)
+        return 0
 
     w = dict(WORKLOADS[args.workload])
     if args.n:
@@ -158,6 +173,16 @@ def main() -> int:
     else:
         ef, policy, _, pname = best
 
+    # ---- optional calibration copy: a kernel of known traffic for the counters
+    if args.copy_mib > 0:
+        nb = args.copy_mib << 20
+        src, dst = _lib.DeviceBuffer(nb), _lib.DeviceBuffer(nb)
+        _lib.check(L.qv_fill_uniform_bytes(src.ptr, nb, 7, 0))
+        _lib.check(L.qv_dev_copy(dst.ptr, src.ptr, nb, 2))
+        src.close()
+        dst.close()
+        log(f"calibration copy: {args.copy_mib} MiB read + {args.copy_mib} MiB written")
+
     # ---- warmup + timed steps ------------------------------------------------
     for _ in range(args.warmup):
         run(ef, policy)
@@ -178,11 +203,12 @@ def main() -> int:
     # records of the expanded nodes + one PQ code row per neighbour
     # evaluation + queries in + top-k out; time from HIP events on its stream.
     kernel_ms = float(np.median([r.kernel_ms for r in reps]))
-    alg_bytes = (last.total_hops * info.node_size + last.total_evals * info.num_chunks
-                 + nq * (dim * 4 + 10 * 8))
+    alg_bytes = (last.total_hops * info.node_size + last.total_evals * (info.num_chunks + 4)
+                 + nq * (info.num_chunks * 256 * 4 + dim * 4 + 10 * 8))
     achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(args.workload, ef, pname, log),
                 "kernel": "search_kernel", "kernel_ms": round(kernel_ms, 3),
                 "bytes_per_launch": int(alg_bytes), "hops_per_launch": int(last.total_hops),
                 "evals_per_launch": int(last.total_evals)}
@@ -214,6 +240,21 @@ def main() -> int:
     L.qv_index_close(h)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def measured_traffic(workload: str, ef: int, policy: str, log):
+    """HBM bytes per search-kernel launch for this configuration, as measured by
+    the FETCH_SIZE and WRITE_SIZE counter runs summarised under profiles/
+    (scaled by a copy kernel of known size); None when not measured."""
+    key = f"traffic_bytes_per_launch[{workload} ef={ef} {policy}]"
+    for f in sorted((Path(__file__).resolve().parent / "profiles").glob("*.md")):
+        for line in f.read_text().splitlines():
+            if line.strip().startswith(key):
+                try:
+                    return int(line.split("=")[-1].strip().replace(",", ""))
+                except ValueError:
+                    log(f"unreadable traffic line in {f.name}: {line}")
+    return None
 
 
 def adc_leg(_lib, L, ncodes: int, log) -> dict:

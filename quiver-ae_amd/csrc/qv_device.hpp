@@ -1,9 +1,9 @@
 // qv_device.hpp -- wave64 building blocks of the CDNA4 search path.
 //
 // One query is served by one 64-lane wavefront.  Lane l owns neighbour l of the
-// node being expanded (R <= 64), so the ADC gather, the candidate sort and the
-// beam merge are register-resident wave operations; the beam lives in LDS
-// between hops and the per-query LUT lives in LDS for the whole query.
+// node being expanded (R <= 64): its ADC gather-sum, its beam-membership test and
+// its key.  The per-query LUT lives in LDS for the whole query; the beam lives in
+// LDS and, chunk-major, in registers.
 //
 // Candidate keys are 64-bit: (fp32 bits of the PQ distance) << 32 |
 // (id & 0x7fffffff) << 1 | (unvisited ? 1 : 0).  Distances are sums of squares,
@@ -84,11 +84,6 @@ __device__ __forceinline__ uint64_t read_lane_u64(uint64_t v, int l) {
   return ((uint64_t)read_lane_u32((uint32_t)(v >> 32), l) << 32) | read_lane_u32((uint32_t)v, l);
 }
 
-// Number of set bits of mask below this lane.
-__device__ __forceinline__ int lanes_below(uint64_t mask) {
-  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-}
-
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
   uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
   lo = (uint32_t)__shfl_xor((int)lo, m);
@@ -106,27 +101,6 @@ __device__ __forceinline__ int opaque_lane() {
   int lane = lane_id();
   asm volatile("" : "+v"(lane));
   return lane;
-}
-
-template <int J>
-__device__ __forceinline__ uint64_t cx_step(uint64_t key, int lane, bool up) {
-  const uint64_t other = xor_lane64<J>(key, lane);
-  const bool lower = (lane & J) == 0;
-  return (lower == up) ? umin64(key, other) : umax64(key, other);
-}
-
-// Bitonic sort of one key per lane, descending across the wave.
-__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key) {
-  const int lane = opaque_lane();
-#define QV_STAGE(K, J) key = cx_step<J>(key, lane, (lane & (K)) != 0)
-  QV_STAGE(2, 1);
-  QV_STAGE(4, 2); QV_STAGE(4, 1);
-  QV_STAGE(8, 4); QV_STAGE(8, 2); QV_STAGE(8, 1);
-  QV_STAGE(16, 8); QV_STAGE(16, 4); QV_STAGE(16, 2); QV_STAGE(16, 1);
-  QV_STAGE(32, 16); QV_STAGE(32, 8); QV_STAGE(32, 4); QV_STAGE(32, 2); QV_STAGE(32, 1);
-  QV_STAGE(64, 32); QV_STAGE(64, 16); QV_STAGE(64, 8); QV_STAGE(64, 4); QV_STAGE(64, 2); QV_STAGE(64, 1);
-#undef QV_STAGE
-  return key;
 }
 
 // Compare-exchange of one bitonic stage (partner lane ^ J) for an ascending
@@ -159,10 +133,10 @@ __device__ __forceinline__ uint64_t cx_stage(uint64_t key, int lane, bool up) {
   }
 }
 
-// Bitonic sort of one key per lane, ascending across the wave (keys distinct).
-__device__ __forceinline__ uint64_t wave_sort_asc(uint64_t key) {
+// Bitonic sort of one key per lane, descending across the wave (keys distinct).
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key) {
   const int lane = opaque_lane();
-#define QV_STAGE(K, J) key = cx_stage<J>(key, lane, (lane & (K)) == 0)
+#define QV_STAGE(K, J) key = cx_stage<J>(key, lane, (lane & (K)) != 0)
   QV_STAGE(2, 1);
   QV_STAGE(4, 2); QV_STAGE(4, 1);
   QV_STAGE(8, 4); QV_STAGE(8, 2); QV_STAGE(8, 1);
@@ -189,65 +163,6 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t x) {
   const auto qh = __builtin_amdgcn_permlane32_swap(hi2, hi2, false, false);
   // read back from lane 0 so the compiler sees a wave-uniform value
   return read_lane_u64(umin64(((uint64_t)qh[0] << 32) | ql[0], ((uint64_t)qh[1] << 32) | ql[1]), 0);
-}
-
-// Inclusive prefix sum over the 64 lanes (DPP row shifts, then row broadcasts).
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);  // row_shr:1
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true);  // row_shr:2
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true);  // row_shr:4
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true);  // row_shr:8
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false); // row_bcast:15
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false); // row_bcast:31
-  return v;
-}
-
-// Rank of a candidate key c1 (visited bit set) in an ascending key array of
-// CAP = 8^LEVELS entries (LEVELS <= 3) whose unused tail holds kPadKey: the
-// number of entries below c1 when the visited bit is ignored, for ranks up to
-// CAP - 1.  An 8-ary search on the distance word (the high 32 bits), seven
-// independent LDS reads per level, then a walk over entries of equal distance
-// on the full key.  Every index read is at most CAP - 1.
-template <int LEVELS>
-__device__ __forceinline__ int beam_rank(const uint64_t* __restrict__ a, uint64_t c1) {
-  constexpr int CAP = LEVELS == 2 ? 64 : 512;
-  const uint32_t* hi = reinterpret_cast<const uint32_t*>(a) + 1;  // hi[2 i] = a[i] >> 32
-  const uint32_t cd = (uint32_t)(c1 >> 32);
-  int pos = 0;
-#pragma unroll
-  for (int lev = 0; lev < LEVELS; lev++) {
-    const int e = LEVELS - 1 - lev;
-    const int S = e == 0 ? 1 : (e == 1 ? 8 : 64);
-    int cnt = 0;
-#pragma unroll
-    for (int j = 1; j <= 7; j++) cnt += hi[2 * (pos + j * S - 1)] < cd ? 1 : 0;
-    pos += cnt * S;
-  }
-  while (pos < CAP - 1 && (uint32_t)(a[pos] >> 32) == cd && (a[pos] | 1ull) < c1) pos++;
-  return pos;
-}
-
-// Bitonic merge of P slots (element i = s*64 + lane) into ascending order.
-// Input: slots 0..P-2 ascending (padded with kPadKey), slot P-1 descending.
-template <int P>
-__device__ __forceinline__ void wave_merge_asc(uint64_t (&b)[P]) {
-  const int lane = opaque_lane();
-#pragma unroll
-  for (int half = P / 2; half >= 1; half >>= 1) {
-#pragma unroll
-    for (int s = 0; s < P; s++) {
-      if ((s & half) == 0) {
-        uint64_t lo = umin64(b[s], b[s + half]);
-        uint64_t hi = umax64(b[s], b[s + half]);
-        b[s] = lo;
-        b[s + half] = hi;
-      }
-    }
-  }
-#define QV_MSTAGE(J)                                       \
-  _Pragma("unroll") for (int s = 0; s < P; s++) b[s] = cx_step<J>(b[s], lane, true)
-  QV_MSTAGE(32); QV_MSTAGE(16); QV_MSTAGE(8); QV_MSTAGE(4); QV_MSTAGE(2); QV_MSTAGE(1);
-#undef QV_MSTAGE
 }
 
 // Per-query LUT in LDS: PQSearchData::init_query (src/shared/index/
@@ -393,33 +308,6 @@ __device__ __forceinline__ float exact_l2_pre(const uint32_t (&x)[kVecPre], cons
       val = __fmaf_rn(diff, diff, val);
     }
   }
-  val += __uint_as_float(xor_lane32<16>(__float_as_uint(val), lane));
-  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x108, 0xF, 0xF, false));
-  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x104, 0xF, 0xF, false));
-  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x102, 0xF, 0xF, false));
-  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x101, 0xF, 0xF, false));
-  return read_lane_f32(val, 0);
-}
-
-// Exact squared L2 in the reference's order: square_sum_32
-// (src/shared/common/gpu_primitives.cuh:26-44).  Lanes 0..31 accumulate the
-// dimensions l, l+32, ... with a fused multiply-add, then the shuffle-down
-// tree over 32 lanes; every lane receives lane 0's value.
-template <class T>
-__device__ __forceinline__ float exact_l2_ref(const uint8_t* __restrict__ rec,
-                                              const float* __restrict__ qu_lds, int dim) {
-  const int lane = opaque_lane();
-  float val = 0.f;
-  if (lane < 32) {
-    for (int i = lane; i < dim; i += 32) {
-      float diff = qu_lds[i] - elem_to_float<T>(rec, i);
-      val = __fmaf_rn(diff, diff, val);
-    }
-  }
-  // Shuffle-down tree: lane l adds lane l+off for off = 16, 8, 4, 2, 1.  Only
-  // lane 0's sum is returned, and it depends only on lanes l < off at each
-  // step, whose partners l+off are reached by swizzle (xor 16) and by DPP
-  // row_shl inside the first 16-lane row.
   val += __uint_as_float(xor_lane32<16>(__float_as_uint(val), lane));
   val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x108, 0xF, 0xF, false));
   val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x104, 0xF, 0xF, false));

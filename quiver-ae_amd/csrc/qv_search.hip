@@ -5,9 +5,12 @@
 // (src/quiver/search.cu:357-1361).  Differences by design:
 //   * one 64-lane wavefront per query; workgroups of one wave; the LUT, the
 //     query and the beam live in LDS; neighbour lists, vectors and PQ codes are
-//     read straight from HBM (no CPU poll threads, no 4 KB page copies);
-//   * candidate sort + beam merge are register bitonic networks over 64-bit
-//     keys instead of merge-path rounds with block barriers;
+//     read straight from HBM (no CPU poll threads, no 4 KB page copies), and the
+//     next node's record is requested while the current hop finishes;
+//   * the merge is built by rank: a per-workgroup bitmap answers "is this
+//     neighbour already in the beam", the few new candidates are ranked with
+//     ballots against a register copy of the beam and scattered into LDS,
+//     instead of merge-path rounds with block barriers;
 //   * a device work queue (atomic ticket) gated by a host-written feed count,
 //     completion published to a host ring so per-query latency is exact.
 #include <algorithm>
@@ -385,7 +388,6 @@ template <class T, int Q, int MC>
 __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
   extern __shared__ __align__(16) char smem[];
   const int lane = lane_id();
-  LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q);
 
   while (true) {
     // ---- acquire (StreamingDispatch, src/quiver/kernel_core/policies/dispatch.cuh:39-79)
