@@ -140,6 +140,13 @@ int qv_search(qv_index* index, const float* queries, int64_t nq, int32_t dim,
 /* Per-query hop counts of the last qv_search on this handle, [nq] int32. */
 int qv_last_hops(const qv_index* index, int32_t* hops, int64_t nq);
 
+/* Per-query latencies (ms) of the last qv_search on this handle, [nq] double,
+ * in query order: completion observed by the host minus admission (streaming
+ * admission), or completion minus the first query's start on the device clock
+ * (batch admission) -- the figures qv_search_report's percentiles summarise
+ * (src/quiver/search.cu:1006-1024). */
+int qv_last_latencies(const qv_index* index, double* ms, int64_t nq);
+
 /* Thread-local message of the last failing call on this thread. */
 const char* qv_last_error(void);
 

@@ -43,6 +43,7 @@ struct qv_index {
   int32_t* h_ctrl = nullptr;   // [0] feed_count, [1] terminate (host-coherent)
   int32_t* h_ring = nullptr;   // [cap_q] completion ring (host-coherent)
   std::vector<int32_t> last_hops;
+  std::vector<double> last_lat_ms;  // per-query latency of the last search, query order
   // host copies of the PQ tables (for saving the index)
   std::vector<float> h_centroid, h_pivots;
   std::vector<int32_t> h_chunk_off;

@@ -1098,6 +1098,16 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   }
   ix->last_hops.resize((size_t)nq);
   HIP_OK(hipMemcpy(ix->last_hops.data(), ix->d_hops, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost));
+  if (!streaming) {
+    // every query admitted at launch: latency = its completion tick - the first start tick
+    std::vector<uint64_t> ts((size_t)nq), te((size_t)nq);
+    HIP_OK(hipMemcpy(ts.data(), ix->d_tstart, sizeof(uint64_t) * (size_t)nq, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(te.data(), ix->d_tend, sizeof(uint64_t) * (size_t)nq, hipMemcpyDeviceToHost));
+    const uint64_t t_first = *std::min_element(ts.begin(), ts.end());
+    lat_ms.resize((size_t)nq);
+    for (int64_t i = 0; i < nq; i++) lat_ms[(size_t)i] = (double)(te[(size_t)i] - t_first) * 1e-5;
+  }
+  ix->last_lat_ms = lat_ms;
 
   if (rep) {
     std::memset(rep, 0, sizeof(*rep));
@@ -1109,14 +1119,6 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     rep->kernel_ms = kms;
     rep->num_blocks = num_blocks;
     rep->max_inflight = max_inflight;
-    if (!streaming) {
-      std::vector<uint64_t> ts((size_t)nq), te((size_t)nq);
-      HIP_OK(hipMemcpy(ts.data(), ix->d_tstart, sizeof(uint64_t) * (size_t)nq, hipMemcpyDeviceToHost));
-      HIP_OK(hipMemcpy(te.data(), ix->d_tend, sizeof(uint64_t) * (size_t)nq, hipMemcpyDeviceToHost));
-      const uint64_t t_first = *std::min_element(ts.begin(), ts.end());
-      lat_ms.resize((size_t)nq);
-      for (int64_t i = 0; i < nq; i++) lat_ms[(size_t)i] = (double)(te[(size_t)i] - t_first) * 1e-5;
-    }
     std::vector<int32_t> stopped((size_t)nq);
     HIP_OK(hipMemcpy(stopped.data(), ix->d_stopped, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost));
     rep->early_stopped = (int32_t)std::accumulate(stopped.begin(), stopped.end(), 0);
@@ -1248,6 +1250,14 @@ int qv_last_hops(const qv_index* ix, int32_t* hops, int64_t nq) {
     if (!ix || !hops) qv::fail(QV_EINVAL, "null argument");
     if ((size_t)nq > ix->last_hops.size()) qv::fail(QV_EINVAL, "nq exceeds the last search");
     std::memcpy(hops, ix->last_hops.data(), sizeof(int32_t) * (size_t)nq);
+  });
+}
+
+int qv_last_latencies(const qv_index* ix, double* ms, int64_t nq) {
+  return qv::guard([&] {
+    if (!ix || !ms) qv::fail(QV_EINVAL, "null argument");
+    if (nq < 0 || (size_t)nq > ix->last_lat_ms.size()) qv::fail(QV_EINVAL, "nq exceeds the last search");
+    std::memcpy(ms, ix->last_lat_ms.data(), sizeof(double) * (size_t)nq);
   });
 }
 

@@ -134,6 +134,7 @@ SIGNATURES = {
     "qv_search": (_I32, [_P, _P, _I64, _I32, _I32, _I32, C.POINTER(SearchOpts), _P, _P, _P,
                          C.POINTER(SearchReport)]),
     "qv_last_hops": (_I32, [_P, _P, _I64]),
+    "qv_last_latencies": (_I32, [_P, _P, _I64]),
     "qv_last_error": (C.c_char_p, []),
     "qv_device_info": (_I32, [C.c_int, C.c_char_p, _I32, C.POINTER(_I32), C.POINTER(_I64)]),
     "qv_lut_build": (_I32, [_P, _P, _I64, _P, _P]),
