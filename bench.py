@@ -115,6 +115,7 @@ def main() -> int:
 
     # ---- index build on the GPU (untimed setup) ------------------------------
     t = time.time()
+    os.environ.setdefault("QV_BUILD_PROGRESS", "1")  # the builder notes its progress on stderr
     p = _lib.default_build_params()
     p.R, p.L, p.num_chunks, p.alpha, p.kmeans_iters, p.passes = w["R"], w["L"], w["M"], 1.2, 15, 2
     h = C.c_void_p()

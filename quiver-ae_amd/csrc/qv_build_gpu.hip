@@ -760,6 +760,9 @@ qv_index* build_gpu_t(const T* d_base, int dtype, int64_t n, int dim, const qv_b
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)prune_lds));
 
   const int passes = std::max(1, std::min(2, prm.passes));
+  // QV_BUILD_PROGRESS=1: a progress line on stderr at most every 10 s (long builds)
+  const bool progress = std::getenv("QV_BUILD_PROGRESS") != nullptr;
+  auto last_note = std::chrono::steady_clock::now();
   for (int pass = 0; pass < passes; pass++) {
     const float alpha = (passes == 2 && pass == 0) ? 1.0f : prm.alpha;
     int64_t done = 0, bsz = 1;
@@ -823,6 +826,12 @@ qv_index* build_gpu_t(const T* d_base, int dtype, int64_t n, int dim, const qv_b
       }
       done += nb;
       bsz *= 2;
+      if (progress && std::chrono::steady_clock::now() - last_note > std::chrono::seconds(10)) {
+        last_note = std::chrono::steady_clock::now();
+        std::fprintf(stderr, "[qv build] pass %d/%d: %lld of %lld points inserted\n", pass + 1, passes,
+                     (long long)done, (long long)n);
+        std::fflush(stderr);
+      }
     }
   }
   (void)t_start;
