@@ -825,7 +825,7 @@ qv_index* build_gpu_t(const T* d_base, int dtype, int64_t n, int dim, const qv_b
         HIP_OK(hipStreamSynchronize(st));
       }
       done += nb;
-      bsz *= 2;
+      bsz = std::min<int64_t>(bsz * 2, max_batch);  // capped: no overflow on long builds
       if (progress && std::chrono::steady_clock::now() - last_note > std::chrono::seconds(10)) {
         last_note = std::chrono::steady_clock::now();
         std::fprintf(stderr, "[qv build] pass %d/%d: %lld of %lld points inserted\n", pass + 1, passes,

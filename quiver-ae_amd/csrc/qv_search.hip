@@ -881,7 +881,7 @@ static SearchArgs base_args(qv_index* ix) {
 void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, const SearchRecord& rec,
                    int32_t* d_hops, int num_blocks) {
   std::lock_guard<std::mutex> lk(ix->mu);
-  if (nq <= 0 || nq > INT32_MAX - 1) fail(QV_EINVAL, "number of queries out of range");
+  if (nq <= 0 || nq > INT32_MAX - 1) fail(QV_EINVAL, "number of queries out of range: " + std::to_string(nq));
   if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 448]");
   HIP_OK(hipSetDevice(ix->device));
   ensure_scratch(ix, nq, 1);
