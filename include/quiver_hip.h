@@ -61,6 +61,9 @@ typedef struct {
   int32_t device;
   int32_t slots_per_cu;   /* resident search workgroups per CU for this index */
   int64_t device_bytes;   /* HBM held by the index */
+  int64_t nav_nodes;      /* nodes of the loaded nav graph (0: none, entry = medoid) */
+  int32_t nav_max_m;      /* its max degree */
+  int32_t reserved;
 } qv_index_info;
 
 /* Replaces bin_common::prepare_search_setup (bin/common/search_setup.hpp:73-119):
@@ -77,6 +80,15 @@ int qv_index_open(const char* index_dir, const char* data_type,
                   int device, qv_index** out);
 
 int qv_index_get_info(const qv_index* index, qv_index_info* out);
+
+/* Loads (or replaces) the navigation graph of a handle from nav_dir
+ * (nav_index, nav_index.data, map.txt; NavGraph::init, src/shared/index/
+ * nav_graph.cu:12-73).  qv_index_open loads one by itself when index_dir holds
+ * nav_index or nav/nav_index (find_nav_dir, bin/common/index_discovery.hpp:
+ * 105-115).  With a nav graph every query starts from the node the in-kernel
+ * nav search returns (inkernel_nav_entry, src/quiver/kernel_core/
+ * inkernel_nav.cuh:61-200) instead of the medoid. */
+int qv_index_load_nav(qv_index* index, const char* nav_dir);
 
 /* ---- Host-only pieces of the setup path (no GPU needed) ---------------------
  * qv_find_index_files: find_index_file + find_pq_prefix
@@ -108,6 +120,8 @@ typedef struct {
   int32_t admission;         /* QV_ADMIT_STREAMING / QV_ADMIT_BATCH */
   int32_t device_buffers;    /* 1: queries and outputs are device pointers */
   double timeout_s;          /* 0: no limit */
+  int32_t skip_nav;          /* --skip-nav: medoid entry even with a nav graph loaded */
+  int32_t reserved0;
 } qv_search_opts;
 
 /* shared::RunReport (src/shared/common/run_report.hpp:32-56) for one search. */
@@ -234,6 +248,15 @@ void qv_build_params_default(qv_build_params* p);
 
 int qv_build_index_cpu(const void* base, int32_t data_type, int64_t n, int32_t dim,
                        const qv_build_params* params, const char* out_prefix);
+
+/* Navigation graph for the per-query entry search (the files NavGraph::init
+ * reads, src/shared/index/nav_graph.cu:12-73; the reference ships no builder
+ * for them): a Vamana graph of degree params->R <= 32 (default 28, the number
+ * of neighbours the nav search reads per node) over host rows [num_rows][dim]
+ * whose base ids are ids[num_rows]; start = the rows' medoid.  Writes
+ * out_dir/nav_index, nav_index.data and map.txt. */
+int qv_build_nav(const void* rows, const int32_t* ids, int64_t num_rows, int32_t dim,
+                 int32_t data_type, const qv_build_params* params, const char* out_dir);
 
 /* GPU construction of the same index from a device array d_base [n][dim]
  * (Vamana with batched insertion; PQ trained on the device).  Returns a handle

@@ -331,6 +331,110 @@ static int gpruning_step(const qvo_search_params* p, const qstate* s, gprune* g,
 }
 
 /* ------------------------------------------------------------------------ */
+/* Nav entry: inkernel_nav_entry, src/quiver/kernel_core/inkernel_nav.cuh:    */
+/* 61-200, as the persistent kernel launches it (128 threads = 4 warps,       */
+/* search.cu:903).  A 32-slot queue: [0, 4) the best four, [4, 32) the        */
+/* neighbours of the last expanded node.  Warp-wide steps are emulated on     */
+/* snapshots so every lane reads the values of before the step.               */
+/* ------------------------------------------------------------------------ */
+int64_t qvo_nav_entry(const qvo_nav* nav, const float* q, int64_t fallback) {
+  enum { L = 4, R = 28, S = 32, WARPS = 4, CHUNK = (R + WARPS - 1) / WARPS };
+  const size_t esz = nav->dtype == QVO_FLOAT ? 4 : 1;
+  const size_t row = (size_t)nav->dim * esz;
+  const uint8_t* data = (const uint8_t*)nav->data;
+  const int64_t glen = nav->num_node * (int64_t)nav->max_m;
+  uint32_t id[S];
+  float dist[S];
+  /* init (:82-93): slot 0 = root, the rest empty (id with the visited bit) */
+  id[0] = (uint32_t)nav->start;
+  dist[0] = qvo_exact_l2(q, data + (size_t)nav->start * row, nav->dtype, nav->dim);
+  for (int s = 1; s < S; s++) {
+    id[s] = 0xffffffffu;
+    dist[s] = INFINITY;
+  }
+  int idx = 0;
+  while (idx != -1) {
+    /* expand (:101-104) */
+    const uint32_t u = id[idx] & ID_MASK;
+    id[idx] |= VISITED;
+    /* distance phase (:113-135): warp w takes neighbours [7w, 7w+7) and stops
+     * at its first -1; slots past the break keep their values.  The row is
+     * read with stride max_m but always 28 wide; past the table's end (where
+     * the reference reads outside its array) the slot reads as -1. */
+    const int64_t e0 = (int64_t)nav->max_m * (int64_t)u;
+    for (int w = 0; w < WARPS; w++) {
+      for (int i = w * CHUNK; i < (w + 1) * CHUNK && i < R; i++) {
+        const int32_t v = e0 + i < glen ? nav->graph[e0 + i] : -1;
+        if (v == -1) break;
+        id[i + L] = (uint32_t)v;
+        dist[i + L] = qvo_exact_l2(q, data + (size_t)v * row, nav->dtype, nav->dim);
+      }
+    }
+    /* selection phase (:142-182): promote four minima into [0, 4) */
+    for (int i = 0; i < L; i++) {
+      float cd[S];
+      int pos[S];
+      const uint32_t prev = i != 0 ? id[i - 1] : 0;
+      uint32_t dup_or = 0;
+      for (int lane = 0; lane < S; lane++) {
+        cd[lane] = dist[lane];
+        pos[lane] = lane;
+        if (lane < i) {
+          cd[lane] = INFINITY;
+        } else if (i != 0 && ((id[lane] ^ prev) & ID_MASK) == 0) {
+          /* duplicate of the last promoted id: its visited bit joins slot i-1 */
+          dup_or |= id[lane];
+          dist[lane] = INFINITY;
+          cd[lane] = INFINITY;
+        }
+      }
+      if (i != 0) id[i - 1] |= dup_or;
+      /* shuffle-down argmin with strict <, offsets 16..1 (:159-167); a lane
+       * whose source is past lane 31 reads its own value */
+      for (int off = S / 2; off > 0; off /= 2) {
+        float od[S];
+        int op[S];
+        for (int lane = 0; lane < S; lane++) {
+          const int src = lane + off < S ? lane + off : lane;
+          od[lane] = cd[src];
+          op[lane] = pos[src];
+        }
+        for (int lane = 0; lane < S; lane++) {
+          if (od[lane] < cd[lane]) {
+            cd[lane] = od[lane];
+            pos[lane] = op[lane];
+          }
+        }
+      }
+      /* lane 0 swaps slot i with the winner unless their distances are equal
+       * (:170-180) */
+      const int p = pos[0];
+      if (i != p) {
+        const float t = dist[i], y = dist[p];
+        if (t != y) {
+          dist[i] = y;
+          dist[p] = t;
+          const uint32_t m = id[i];
+          id[i] = id[p];
+          id[p] = m;
+        }
+      }
+    }
+    /* next: first unvisited slot among all 32, kept only below L (:186-191) */
+    int x = S;
+    for (int s = 0; s < S; s++) {
+      if (!(id[s] & VISITED)) {
+        x = s;
+        break;
+      }
+    }
+    idx = x < L ? x : -1;
+  }
+  const uint32_t best = id[0] & ID_MASK;
+  return best < (uint64_t)nav->num_node ? nav->mapping[best] : fallback;
+}
+
+/* ------------------------------------------------------------------------ */
 /* One query: persistent_search_kernel body, kernel_q1.cuh:126-704, with the */
 /* node fetch served instantly (graph resident in memory), so every issued   */
 /* lane is ready on the next pipe iteration.                                  */
@@ -376,7 +480,9 @@ int qvo_search_one(const qvo_index* ix, const float* q, const qvo_search_params*
   int32_t lane_req[16];
   int32_t lane_node[16];
   int lane_ready[16];
-  int64_t entry = ix->medoid;
+  /* entry: the nav search on the raw query, else the medoid
+   * (kernel_q1.cuh:152-174, 198-205) */
+  int64_t entry = p->nav ? qvo_nav_entry(p->nav, q, ix->medoid) : ix->medoid;
 
   /* boot: kernel_q1.cuh:199-397 */
   rc = merge_data(ix, &s, lut, entry);

@@ -22,6 +22,15 @@
  *                      (bin/common/search_setup_test.cpp:67-81) and the reference
  *                      header compiled into oracle/_ref when it is present
  *   qvo_adc_topk       brute force sort by (dist, sequence) (tests/test_oracle.py)
+ *   qvo_nav_entry      complete nav graph known answer (exact nearest nav node),
+ *                      chain graphs (greedy descent stops at the reachable local
+ *                      minimum), a hand-traced 2- and 3-node graph where the
+ *                      empty-slot swap fires, the per-chunk break traced on a
+ *                      graph with a short row (tests/test_oracle_nav.py).  One case
+ *                      stays unpinned: three or more copies of one id in the
+ *                      queue with differing visited bits, where the reference's
+ *                      same-address shared-memory stores race; this restatement
+ *                      ORs all of them.
  */
 #ifndef QV_ORACLE_H
 #define QV_ORACLE_H
@@ -57,6 +66,20 @@ typedef struct {
   const int32_t* chunk_id; /* [d] chunk of each dimension */
 } qvo_index;
 
+/* Navigation graph (the reference's NavGraph, src/shared/index/nav_graph.cu):
+ * a small graph over sampled base vectors whose greedy search picks each
+ * query's entry node. */
+typedef struct {
+  int dtype;               /* same element type as the base index */
+  int dim;
+  int64_t num_node;
+  int max_m;               /* row stride of graph, 1..32 */
+  int start;               /* root of the nav search */
+  const void* data;        /* [num_node][dim] elements */
+  const int32_t* graph;    /* [num_node][max_m], -1 after each node's degree */
+  const int32_t* mapping;  /* [num_node] nav id -> base id */
+} qvo_nav;
+
 typedef struct {
   int topk;
   int ef_search;
@@ -64,7 +87,13 @@ typedef struct {
   int early_exit;          /* QVO_EXIT_NONE or QVO_EXIT_GPRUNING */
   int gpruning_warmup;     /* reference CLI default 10 */
   int gpruning_patience;   /* reference CLI default 8 */
+  const qvo_nav* nav;      /* entry from the nav search when not NULL, else the medoid */
 } qvo_search_params;
+
+/* Entry node of raw query q from the nav graph (base id).  `fallback` is
+ * returned when the queue's slot 0 ends empty (the reference reads past
+ * nav_mapping there). */
+int64_t qvo_nav_entry(const qvo_nav* nav, const float* q, int64_t fallback);
 
 /* LUT build.  lut is [M][256]; q_used receives fl(fl(q-mu)+mu), the query the
  * reference's exact-distance stage sees after init_query restores it. */

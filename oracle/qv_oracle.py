@@ -51,6 +51,20 @@ class SearchParams(C.Structure):
         ("early_exit", C.c_int),
         ("gpruning_warmup", C.c_int),
         ("gpruning_patience", C.c_int),
+        ("nav", C.c_void_p),
+    ]
+
+
+class OracleNav(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int),
+        ("dim", C.c_int),
+        ("num_node", C.c_int64),
+        ("max_m", C.c_int),
+        ("start", C.c_int),
+        ("data", C.c_void_p),
+        ("graph", C.c_void_p),
+        ("mapping", C.c_void_p),
     ]
 
 
@@ -83,6 +97,8 @@ def load() -> C.CDLL:
     lib.qvo_adc_topk.restype = None
     lib.qvo_ground_truth.argtypes = [P, C.c_int, C.c_int64, C.c_int, P, C.c_int64, C.c_int, C.c_int, P, P]
     lib.qvo_ground_truth.restype = None
+    lib.qvo_nav_entry.argtypes = [C.POINTER(OracleNav), P, C.c_int64]
+    lib.qvo_nav_entry.restype = C.c_int64
     _lib = lib
     return lib
 
@@ -189,9 +205,65 @@ class HostIndex:
                            _ptr(self.centroid), _ptr(self.pivots_t), _ptr(self.chunk_id))
 
 
+@dataclass
+class HostNav:
+    """A navigation graph (nav_index, nav_index.data, map.txt) in host memory."""
+
+    dtype: int
+    dim: int
+    num_node: int
+    max_m: int
+    start: int
+    data: np.ndarray      # [num_node, dim] of the base element type
+    graph: np.ndarray     # int32 [num_node, max_m], -1 after each degree
+    mapping: np.ndarray   # int32 [num_node]
+
+    @classmethod
+    def from_dir(cls, nav_dir: str | Path, data_type: str) -> "HostNav":
+        """Reads the three files the reference's NavGraph::init reads
+        (src/shared/index/nav_graph.cu:12-71)."""
+        d = Path(nav_dir)
+        dt = {"uint8": UINT8, "float": FLOAT, "float32": FLOAT, "int8": INT8}[data_type]
+        np_dt = {UINT8: np.uint8, INT8: np.int8, FLOAT: np.float32}[dt]
+        raw = np.fromfile(d / "nav_index.data", dtype=np.uint8)
+        num_node, dim = (int(x) for x in np.frombuffer(raw[:8].tobytes(), dtype="<i4"))
+        data = np.frombuffer(raw[8:].tobytes(), dtype=np_dt)[: num_node * dim].reshape(num_node, dim)
+        mapping = np.array([int(x) for x in (d / "map.txt").read_text().split()[:num_node]], np.int32)
+        g = np.fromfile(d / "nav_index", dtype="<u4")
+        max_m, start = int(g[2]), int(g[3])
+        graph = np.full((num_node, max_m), -1, np.int32)
+        pos = 6
+        for i in range(num_node):
+            deg = int(g[pos])
+            graph[i, :deg] = g[pos + 1:pos + 1 + deg].astype(np.int32)
+            pos += 1 + deg
+        return cls(dt, dim, num_node, max_m, start, np.ascontiguousarray(data), graph, mapping)
+
+    @classmethod
+    def from_arrays(cls, data: np.ndarray, graph: np.ndarray, mapping: np.ndarray,
+                    start: int = 0) -> "HostNav":
+        dt = {np.dtype("u1"): UINT8, np.dtype("i1"): INT8, np.dtype("<f4"): FLOAT}[data.dtype]
+        g = np.ascontiguousarray(graph, np.int32)
+        return cls(dt, int(data.shape[1]), int(data.shape[0]), int(g.shape[1]), int(start),
+                   np.ascontiguousarray(data), g, np.ascontiguousarray(mapping, np.int32))
+
+    def c_struct(self) -> OracleNav:
+        return OracleNav(self.dtype, self.dim, self.num_node, self.max_m, self.start, _ptr(self.data),
+                         _ptr(self.graph), _ptr(self.mapping))
+
+
+def nav_entry(nav: HostNav, q: np.ndarray, fallback: int = -1) -> int:
+    """Entry node (base id) that the nav search picks for the raw query q."""
+    cs = nav.c_struct()
+    qq = np.ascontiguousarray(q, np.float32)
+    return int(load().qvo_nav_entry(C.byref(cs), _ptr(qq), fallback))
+
+
 def search(ix: HostIndex, queries: np.ndarray, topk: int, ef: int, *, pipe_width: int = 1,
-           early_exit: int = EXIT_GPRUNING, warmup: int = 10, patience: int = 8, threads: int = 0):
-    """Oracle search: returns (ids int32 [n,k], dists float32 [n,k], found, hops)."""
+           early_exit: int = EXIT_GPRUNING, warmup: int = 10, patience: int = 8, threads: int = 0,
+           nav: HostNav | None = None):
+    """Oracle search: returns (ids int32 [n,k], dists float32 [n,k], found, hops).
+    With `nav`, each query starts from its nav-graph entry instead of the medoid."""
     lib = load()
     q = np.ascontiguousarray(queries, dtype=np.float32)
     n = q.shape[0]
@@ -199,7 +271,9 @@ def search(ix: HostIndex, queries: np.ndarray, topk: int, ef: int, *, pipe_width
     dists = np.empty((n, topk), np.float32)
     found = np.empty(n, np.int32)
     hops = np.empty(n, np.int32)
-    p = SearchParams(topk, ef, pipe_width, early_exit, warmup, patience)
+    ns = nav.c_struct() if nav is not None else None
+    p = SearchParams(topk, ef, pipe_width, early_exit, warmup, patience,
+                     C.cast(C.pointer(ns), C.c_void_p) if ns is not None else None)
     cs = ix.c_struct()
     rc = lib.qvo_search(C.byref(cs), _ptr(q), n, C.byref(p), threads, _ptr(ids), _ptr(dists),
                         _ptr(found), _ptr(hops))

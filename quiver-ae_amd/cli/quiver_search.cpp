@@ -254,6 +254,7 @@ int main(int argc, char** argv) {
     o.early_exit = policy == "gpruning" ? QV_EXIT_GPRUNING : QV_EXIT_NONE;
     o.gpruning_warmup = 10;
     o.gpruning_patience = 8;
+    o.skip_nav = f["--skip-nav"].used ? 1 : 0;
     if (const char* e = std::getenv("QUIVER_PREFEED")) o.prefeed = std::atoi(e);
     if (const char* e = std::getenv("QUIVER_ADMIT_MIN_BATCH")) o.admit_min_batch = std::max(1, std::atoi(e));
     qv_search_report rep;

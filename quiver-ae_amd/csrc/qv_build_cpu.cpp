@@ -367,4 +367,56 @@ void build_index_cpu(const void* base, int dtype, int64_t n, int dim,
   write_pq_tables(prefix + "_pq_pivots.bin", prefix + "_pq_compressed.bin", pq);
 }
 
+// Navigation graph over sample rows (their base ids in ids): a Vamana graph
+// of degree R <= 32 over the sample, start = the sample's medoid, written in
+// the format NavGraph::init reads (nav_graph.cu:12-73).
+void build_nav_cpu(const void* rows, const int32_t* ids, int64_t s, int dim, int dtype,
+                   const qv_build_params& prm_in, const std::string& dir) {
+  qv_build_params prm = prm_in;
+  if (prm.threads <= 0) prm.threads = omp_get_num_procs();
+  if (s <= 1 || s > (int64_t)INT32_MAX) fail(QV_EINVAL, "sample size must be in [2, 2^31)");
+  if (prm.R <= 0 || prm.R > 32) fail(QV_EINVAL, "nav graph degree must be in [1, 32]");
+  if (prm.L < prm.R) fail(QV_EINVAL, "L must be >= R");
+  Base B{static_cast<const uint8_t*>(rows), dtype, s, dim};
+  std::vector<double> mean((size_t)dim, 0.0);
+  for (int64_t i = 0; i < s; i++)
+    for (int j = 0; j < dim; j++) mean[(size_t)j] += B.at(i, j);
+  std::vector<float> meanf((size_t)dim);
+  for (int j = 0; j < dim; j++) meanf[(size_t)j] = (float)(mean[(size_t)j] / (double)s);
+  int64_t medoid = 0;
+  float best = INFINITY;
+  for (int64_t i = 0; i < s; i++) {
+    const float dd = B.dist_to(meanf.data(), i);
+    if (dd < best) {
+      best = dd;
+      medoid = i;
+    }
+  }
+  Graph G(s, prm.R);
+  std::vector<int64_t> order((size_t)s);
+  std::iota(order.begin(), order.end(), 0);
+  for (int64_t i = s - 1; i > 0; i--) {
+    const int64_t j = (int64_t)(rng_u64(prm.seed, 23, (uint64_t)i) % (uint64_t)(i + 1));
+    std::swap(order[(size_t)i], order[(size_t)j]);
+  }
+  if (prm.passes >= 2) vamana_pass(B, G, (uint32_t)medoid, prm, 1.0f, order);
+  vamana_pass(B, G, (uint32_t)medoid, prm, prm.alpha, order);
+
+  NavGraphHost nav;
+  nav.num_node = (int32_t)s;
+  nav.dims = dim;
+  nav.max_m = prm.R;
+  nav.start = (int32_t)medoid;
+  const size_t bytes = (size_t)s * (size_t)dim * (size_t)elem_size(dtype);
+  nav.data.assign(static_cast<const uint8_t*>(rows), static_cast<const uint8_t*>(rows) + bytes);
+  nav.graph.assign((size_t)s * prm.R, -1);
+  for (int64_t v = 0; v < s; v++) {
+    if (G.deg[(size_t)v] == 0) fail(QV_EINDEX, "nav graph node without neighbours (duplicate sample rows?)");
+    for (uint32_t k = 0; k < G.deg[(size_t)v]; k++)
+      nav.graph[(size_t)v * prm.R + k] = (int32_t)G.adj[(size_t)v * prm.R + k];
+  }
+  nav.mapping.assign(ids, ids + s);
+  write_nav(dir, dtype, nav);
+}
+
 }  // namespace qv

@@ -38,6 +38,8 @@ void set_last_error(const std::string& msg) { g_last_error = msg; }
 
 void build_index_cpu(const void* base, int dtype, int64_t n, int dim, const qv_build_params& prm,
                      const std::string& prefix);
+void build_nav_cpu(const void* rows, const int32_t* ids, int64_t s, int dim, int dtype, const qv_build_params& prm,
+                   const std::string& dir);
 
 }  // namespace qv
 
@@ -69,6 +71,21 @@ int qv_build_index_cpu(const void* base, int32_t data_type, int64_t n, int32_t d
     qv_build_params_default(&p);
     if (params) p = *params;
     qv::build_index_cpu(base, data_type, n, dim, p, out_prefix);
+  });
+}
+
+int qv_build_nav(const void* rows, const int32_t* ids, int64_t num_rows, int32_t dim, int32_t data_type,
+                 const qv_build_params* params, const char* out_dir) {
+  return qv::host_guard([&] {
+    if (!rows || !ids || !out_dir || dim <= 0) qv::fail(QV_EINVAL, "bad argument");
+    if (data_type != QV_UINT8 && data_type != QV_FLOAT && data_type != QV_INT8)
+      qv::fail(QV_EINVAL, "bad data type");
+    qv_build_params p;
+    qv_build_params_default(&p);
+    p.R = 28;
+    p.L = 64;
+    if (params) p = *params;
+    qv::build_nav_cpu(rows, ids, num_rows, dim, data_type, p, out_dir);
   });
 }
 

@@ -74,6 +74,27 @@ void write_index_image(const std::string& path, const Layout& lay, const uint8_t
 void write_pq_tables(const std::string& pivots_file, const std::string& codes_file,
                      const PQTables& t);
 
+// Navigation graph (shared::NavGraph, src/shared/index/nav_graph.hpp): a small
+// in-memory graph over a sample of the base points, searched per query for the
+// entry node.  graph is [num_node][max_m] with -1 after each node's degree;
+// mapping[i] is the base id of nav node i.
+struct NavGraphHost {
+  int32_t num_node = 0;
+  int32_t dims = 0;
+  int32_t max_m = 0;
+  int32_t start = 0;
+  std::vector<uint8_t> data;     // [num_node][dims] elements of the base type
+  std::vector<int32_t> graph;    // [num_node][max_m]
+  std::vector<int32_t> mapping;  // [num_node]
+};
+// find_nav_dir (bin/common/index_discovery.hpp:105-115): index_dir itself when
+// it holds nav_index, else index_dir/nav when that does, else "".
+std::string find_nav_dir(const std::string& index_dir);
+// NavGraph::init (src/shared/index/nav_graph.cu:12-73): nav_index,
+// nav_index.data and map.txt of dir; validated against the base (ids, dims).
+void read_nav(const std::string& dir, int data_type, int64_t base_n, int64_t dims, NavGraphHost& nav);
+void write_nav(const std::string& dir, int data_type, const NavGraphHost& nav);
+
 // typed .bin with int32 (n, d) header (bin/common/data_io.hpp:29-51, 116-140)
 template <class T>
 std::vector<T> read_typed_bin(const std::string& path, int64_t& n, int64_t& d);

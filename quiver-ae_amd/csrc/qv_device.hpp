@@ -339,6 +339,145 @@ __device__ __forceinline__ void topk_insert(float& td, int32_t& ti, int& fc, int
   fc = ns;
 }
 
+// ---- navigation-graph entry: inkernel_nav_entry (src/quiver/kernel_core/inkernel_nav.cuh:61-200)
+// A greedy search over the small nav graph with a 32-slot queue: slots [0, 4)
+// hold the best four, slots [4, 32) the neighbours of the last expanded node.
+// The reference runs it with one 32-lane warp for the queue and four warps for
+// the distances; here lanes 0..31 hold the slots and the two wave halves
+// compute two neighbour distances at a time.
+constexpr int kNavL = 4;
+constexpr int kNavR = 28;
+constexpr int kNavChunk = 7;  // neighbours per warp in the reference (28 over 4 warps)
+
+// square_sum_32 (src/shared/common/gpu_primitives.cuh:26-44) of the float query
+// q against vector x, per wave half: sub-lane s accumulates dimensions s, s+32,
+// ... with a fused multiply-add, then the shuffle-down tree; the sum is valid
+// at sub-lane 0 of each half.
+template <class T>
+__device__ __forceinline__ float nav_dist32(const float* __restrict__ q, const uint8_t* __restrict__ x, int dims,
+                                            int lane) {
+  float val = 0.f;
+  for (int i = lane & 31; i < dims; i += 32) {
+    const float diff = q[i] - elem_to_float<T>(x, i);
+    val = __fmaf_rn(diff, diff, val);
+  }
+  val += __uint_as_float(xor_lane32<16>(__float_as_uint(val), lane));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x108, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x104, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x102, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x101, 0xF, 0xF, false));
+  return val;
+}
+
+// Returns the mapped base id of the best nav node for query q (raw, before the
+// LUT's centring).  graph is [num_node][max_m] with -1 after the degree;
+// indexes past the end of graph read as -1.  With fewer than four distinct
+// nodes in the queue, the last selection round swaps an empty slot into slot 0
+// (all candidates +inf, the argmin stays at lane 0, and +inf != d); the
+// reference then reads nav_mapping[0x7fffffff].  Here that case returns
+// `fallback` (the medoid).
+template <class T>
+__device__ int32_t nav_entry(const float* __restrict__ q, const uint8_t* __restrict__ data,
+                             const int32_t* __restrict__ graph, const int32_t* __restrict__ mapping,
+                             int64_t num_node, int dims, int max_m, int start, int32_t fallback) {
+  const int lane = opaque_lane();
+  const int half = lane >> 5;
+  const int64_t row = (int64_t)dims * (int64_t)sizeof(T);
+  const int64_t glen = num_node * (int64_t)max_m;
+  // slot registers (lanes 0..31); unused slots carry id 0xffffffff (visited) and +inf
+  uint32_t pid = 0xffffffffu;
+  float pdist = __int_as_float(0x7f800000);
+  {
+    const float d0 = read_lane_f32(nav_dist32<T>(q, data + (int64_t)start * row, dims, lane), 0);
+    if (lane == 0) {
+      pid = (uint32_t)start;
+      pdist = d0;
+    }
+  }
+  int idx = 0;
+  while (idx != -1) {
+    const int u = (int)(read_lane_u32(pid, idx) & 0x7fffffffu);
+    if (lane == idx) pid |= 0x80000000u;
+    // Distance phase: neighbour i fills slot kNavL + i; in each 7-neighbour
+    // chunk (one warp of the reference) the first -1 ends the chunk, and the
+    // slots it leaves keep their values.
+    const int64_t e0 = (int64_t)max_m * u;
+    uint32_t broken = 0;  // chunks that met a -1
+    for (int j = 0; j < kNavR / 2; j++) {
+      const int i0 = 2 * j, i1 = 2 * j + 1;
+      const int32_t v0 = e0 + i0 < glen ? graph[e0 + i0] : -1;
+      const int32_t v1 = e0 + i1 < glen ? graph[e0 + i1] : -1;
+      bool ok0 = false, ok1 = false;
+      if (!(broken >> (i0 / kNavChunk) & 1u)) {
+        if (v0 == -1) broken |= 1u << (i0 / kNavChunk);
+        else ok0 = true;
+      }
+      if (!(broken >> (i1 / kNavChunk) & 1u)) {
+        if (v1 == -1) broken |= 1u << (i1 / kNavChunk);
+        else ok1 = true;
+      }
+      if (!ok0 && !ok1) continue;
+      const int32_t vh = half ? (ok1 ? v1 : 0) : (ok0 ? v0 : 0);
+      const float dh = nav_dist32<T>(q, data + (int64_t)vh * row, dims, lane);
+      const float d0 = read_lane_f32(dh, 0), d1 = read_lane_f32(dh, 32);
+      if (ok0 && lane == kNavL + i0) {
+        pid = (uint32_t)v0;
+        pdist = d0;
+      }
+      if (ok1 && lane == kNavL + i1) {
+        pid = (uint32_t)v1;
+        pdist = d1;
+      }
+    }
+    // Selection phase: promote the four smallest to slots 0..3.
+#pragma unroll
+    for (int i = 0; i < kNavL; i++) {
+      // Slots below i are final.  A slot at or above i holding the id selected
+      // last round is a duplicate: its visited bit joins that slot
+      // (pq_id[i-1] |= pq_id[lane]) and it drops out with +inf.
+      bool dup = false;
+      if (i != 0) {
+        const uint32_t prev = read_lane_u32(pid, i - 1);
+        dup = lane >= i && lane < 32 && ((pid ^ prev) & 0x7fffffffu) == 0;
+        const uint64_t visited_dups = __ballot(dup && (pid & 0x80000000u));
+        if (lane == i - 1 && visited_dups) pid |= 0x80000000u;
+        if (dup) pdist = __int_as_float(0x7f800000);
+      }
+      float dist = (lane < 32 && lane >= i && !dup) ? pdist : __int_as_float(0x7f800000);
+      int pos = lane;
+      // 32-lane shuffle-down argmin, strict <, result at lane 0
+      {
+        float od = __uint_as_float(xor_lane32<16>(__float_as_uint(dist), lane));
+        int op = (int)xor_lane32<16>((uint32_t)pos, lane);
+        if (od < dist) { dist = od; pos = op; }
+#define QV_NAV_STEP(CTRL)                                                                               \
+  od = __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(dist), CTRL, 0xF, 0xF, false)); \
+  op = __builtin_amdgcn_update_dpp(0, pos, CTRL, 0xF, 0xF, false);                                      \
+  if (od < dist) { dist = od; pos = op; }
+        QV_NAV_STEP(0x108)
+        QV_NAV_STEP(0x104)
+        QV_NAV_STEP(0x102)
+        QV_NAV_STEP(0x101)
+#undef QV_NAV_STEP
+      }
+      const int p0 = read_lane_i32(pos, 0);
+      if (i != p0) {
+        const float t = read_lane_f32(pdist, i), y = read_lane_f32(pdist, p0);
+        if (t != y) {
+          const uint32_t mi = read_lane_u32(pid, i), mp = read_lane_u32(pid, p0);
+          if (lane == i) { pdist = y; pid = mp; }
+          if (lane == p0) { pdist = t; pid = mi; }
+        }
+      }
+    }
+    const uint64_t unv = __ballot(lane < 32 && !(pid & 0x80000000u));
+    const int x = unv ? __ffsll((long long)unv) - 1 : 32;
+    idx = x < kNavL ? x : -1;
+  }
+  const uint32_t best = read_lane_u32(pid, 0) & 0x7fffffffu;
+  return best < (uint64_t)num_node ? mapping[best] : fallback;
+}
+
 // Wall clock at 100 MHz (s_memrealtime).
 __device__ __forceinline__ uint64_t wall_ticks() { return wall_clock64(); }
 

@@ -251,6 +251,106 @@ void write_pq_tables(const std::string& pivots_file, const std::string& codes_fi
   write_typed_bin<uint8_t>(codes_file, t.codes.data(), t.num_pts, t.num_chunks);
 }
 
+// ---- navigation graph ------------------------------------------------------
+
+std::string find_nav_dir(const std::string& index_dir) {
+  if (fs::exists(fs::path(index_dir) / "nav_index")) return index_dir;
+  if (fs::exists(fs::path(index_dir) / "nav" / "nav_index")) return (fs::path(index_dir) / "nav").string();
+  return "";
+}
+
+// nav_index: the DiskANN in-memory graph file -- u64 file size, u32 max
+// degree, u32 start, u64 frozen-point count, then per node u32 degree and the
+// neighbour ids (NavGraph::init reads the header as six ints, nav_graph.cu:47-53).
+// nav_index.data: i32 num_node, i32 dims, then the vectors.  map.txt: num_node
+// whitespace-separated base ids.
+void read_nav(const std::string& dir, int data_type, int64_t base_n, int64_t dims, NavGraphHost& nav) {
+  const std::string data_file = dir + "/nav_index.data", index_file = dir + "/nav_index",
+                    map_file = dir + "/map.txt";
+  std::ifstream fd(data_file, std::ios::binary);
+  if (!fd) fail(QV_EIO, "Failed to open data file: " + data_file);
+  int32_t hdr[2] = {0, 0};
+  fd.read(reinterpret_cast<char*>(hdr), sizeof(hdr));
+  if (!fd || hdr[0] <= 0 || hdr[1] <= 0) fail(QV_EIO, "bad nav data header: " + data_file);
+  nav.num_node = hdr[0];
+  nav.dims = hdr[1];
+  if (nav.dims != dims)
+    fail(QV_EINDEX, "nav graph has " + std::to_string(nav.dims) + " dims, the index " + std::to_string(dims));
+  const size_t bytes = (size_t)nav.num_node * (size_t)nav.dims * (size_t)elem_size(data_type);
+  nav.data.resize(bytes);
+  fd.read(reinterpret_cast<char*>(nav.data.data()), (std::streamsize)bytes);
+  if (!fd) fail(QV_EIO, "short nav data file: " + data_file);
+
+  std::ifstream fm(map_file);
+  if (!fm) fail(QV_EIO, "Failed to open map file: " + map_file);
+  nav.mapping.resize((size_t)nav.num_node);
+  for (int32_t i = 0; i < nav.num_node; i++) {
+    long long x = -1;
+    if (!(fm >> x)) fail(QV_EIO, "Failed to read map entry " + std::to_string(i) + " from " + map_file);
+    if (x < 0 || x >= base_n) fail(QV_EINDEX, "nav map entry out of range: " + std::to_string(x));
+    nav.mapping[(size_t)i] = (int32_t)x;
+  }
+
+  std::ifstream fi(index_file, std::ios::binary);
+  if (!fi) fail(QV_EIO, "Failed to open index file: " + index_file);
+  uint64_t fsize = 0, frozen = 0;
+  uint32_t max_m = 0, start = 0;
+  fi.read(reinterpret_cast<char*>(&fsize), 8);
+  fi.read(reinterpret_cast<char*>(&max_m), 4);
+  fi.read(reinterpret_cast<char*>(&start), 4);
+  fi.read(reinterpret_cast<char*>(&frozen), 8);
+  if (!fi) fail(QV_EIO, "short nav index header: " + index_file);
+  if (max_m == 0 || max_m > 32) fail(QV_EINDEX, "nav graph max degree must be in [1, 32]");  // nav_graph.cu:58
+  if (start >= (uint32_t)nav.num_node) fail(QV_EINDEX, "nav start out of range");
+  nav.max_m = (int32_t)max_m;
+  nav.start = (int32_t)start;
+  nav.graph.assign((size_t)nav.num_node * max_m, -1);
+  for (int32_t i = 0; i < nav.num_node; i++) {
+    uint32_t d = 0;
+    fi.read(reinterpret_cast<char*>(&d), 4);
+    if (!fi || d == 0 || d > max_m) fail(QV_EINDEX, "nav node " + std::to_string(i) + " has a bad degree");
+    fi.read(reinterpret_cast<char*>(&nav.graph[(size_t)i * max_m]), 4 * (std::streamsize)d);
+    if (!fi) fail(QV_EIO, "short nav index file: " + index_file);
+    for (uint32_t j = 0; j < d; j++) {
+      const int32_t v = nav.graph[(size_t)i * max_m + j];
+      if (v < 0 || v >= nav.num_node) fail(QV_EINDEX, "nav neighbour id out of range");
+    }
+  }
+}
+
+void write_nav(const std::string& dir, int data_type, const NavGraphHost& nav) {
+  fs::create_directories(dir);
+  {
+    std::ofstream f(dir + "/nav_index.data", std::ios::binary);
+    const int32_t hdr[2] = {nav.num_node, nav.dims};
+    f.write(reinterpret_cast<const char*>(hdr), sizeof(hdr));
+    f.write(reinterpret_cast<const char*>(nav.data.data()),
+            (std::streamsize)((size_t)nav.num_node * nav.dims * elem_size(data_type)));
+    if (!f) fail(QV_EIO, "cannot write " + dir + "/nav_index.data");
+  }
+  {
+    std::ofstream f(dir + "/map.txt");
+    for (int32_t i = 0; i < nav.num_node; i++) f << nav.mapping[(size_t)i] << "\n";
+    if (!f) fail(QV_EIO, "cannot write " + dir + "/map.txt");
+  }
+  std::vector<uint32_t> body;
+  for (int32_t i = 0; i < nav.num_node; i++) {
+    uint32_t d = 0;
+    while (d < (uint32_t)nav.max_m && nav.graph[(size_t)i * nav.max_m + d] >= 0) d++;
+    body.push_back(d);
+    for (uint32_t j = 0; j < d; j++) body.push_back((uint32_t)nav.graph[(size_t)i * nav.max_m + j]);
+  }
+  std::ofstream f(dir + "/nav_index", std::ios::binary);
+  const uint64_t fsize = 24 + 4 * (uint64_t)body.size(), frozen = 0;
+  const uint32_t max_m = (uint32_t)nav.max_m, start = (uint32_t)nav.start;
+  f.write(reinterpret_cast<const char*>(&fsize), 8);
+  f.write(reinterpret_cast<const char*>(&max_m), 4);
+  f.write(reinterpret_cast<const char*>(&start), 4);
+  f.write(reinterpret_cast<const char*>(&frozen), 8);
+  f.write(reinterpret_cast<const char*>(body.data()), (std::streamsize)(4 * body.size()));
+  if (!f) fail(QV_EIO, "cannot write " + dir + "/nav_index");
+}
+
 template <class T>
 std::vector<T> read_typed_bin(const std::string& path, int64_t& n, int64_t& d) {
   int nr = 0, nc = 0;

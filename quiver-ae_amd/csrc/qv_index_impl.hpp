@@ -20,6 +20,12 @@ struct qv_index {
   float* d_centroid = nullptr;
   float* d_pivots_t = nullptr;
   int32_t* d_chunk_off = nullptr;
+  // navigation graph (optional): vectors, [nodes][max_m] adjacency, base ids
+  uint8_t* d_nav_data = nullptr;
+  int32_t* d_nav_graph = nullptr;
+  int32_t* d_nav_map = nullptr;
+  int64_t nav_nodes = 0;
+  int32_t nav_max_m = 0, nav_start = 0;
   int64_t device_bytes = 0;
   int num_cus = 0;
   hipStream_t stream = nullptr;
@@ -66,6 +72,9 @@ qv_index* make_index(int device, const Layout& lay, const PQTables& pq, uint8_t*
                      uint8_t* d_codes, bool validate);
 
 void release_index(qv_index* ix);
+
+// Loads the nav graph of dir (nav_index, nav_index.data, map.txt) to the device.
+void load_nav(qv_index* ix, const std::string& dir);
 
 // Checks degree <= R, neighbour ids < n and duplicate-free lists on the device;
 // throws QV_EINDEX on the first violation.

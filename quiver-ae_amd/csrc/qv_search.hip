@@ -74,6 +74,13 @@ struct SearchArgs {
   const int32_t* terminate;        // host-coherent, may be null
   int32_t* ring;                   // host-coherent completion ring, may be null
   uint64_t spin_limit_ticks;       // watchdog on feed waits (100 MHz ticks)
+  // navigation graph for the per-query entry node (nav_data null: the medoid)
+  const uint8_t* nav_data;
+  const int32_t* nav_graph;
+  const int32_t* nav_map;
+  int64_t nav_nodes;
+  int32_t nav_max_m;
+  int32_t nav_start;
   // per-workgroup membership bitmaps of the beam (bit v set <=> v in the beam),
   // bits_words 32-bit words per workgroup, all zero between queries
   uint32_t* bits;
@@ -421,9 +428,14 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
     if (a.t_start && lane == 0) a.t_start[qid] = wall_ticks();
 
     Query<T, Q, MC> Qy(a, smem);
+    const float* q = a.queries + (int64_t)qid * a.dim;
+    // ---- entry node: the nav-graph search on the raw query when a nav graph is
+    // loaded (kernel_q1.cuh:148-174, 199-206), else the medoid.
+    const int32_t entry = a.nav_data ? nav_entry<T>(q, a.nav_data, a.nav_graph, a.nav_map, a.nav_nodes, a.dim,
+                                                    a.nav_max_m, a.nav_start, (int32_t)a.medoid)
+                                     : a.medoid;
     // ---- query into LDS: q - mu for the LUT, fl(fl(q - mu) + mu) for the exact
     // distance (pq_device.cuh:18-20, 33-35).
-    const float* q = a.queries + (int64_t)qid * a.dim;
     for (int i = lane; i < a.dim; i += kWave) {
       const float c = q[i] - a.centroid[i];
       Qy.qc[i] = c;
@@ -467,8 +479,8 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
       // One pipe lane (kernel_q1.cuh:199-397 boot, then 407-670): the node a
       // hop selects is the next one expanded, so its record is requested while
       // the hop finishes.
-      Qy.fetch(a.medoid, lane, nr);
-      int32_t v = a.medoid;
+      Qy.fetch(entry, lane, nr);
+      int32_t v = entry;
       while (true) {
         const int32_t nx = Qy.template hop<true>(v, nr);
         log_hop(v);
@@ -484,8 +496,8 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
     }
     {
     // ---- boot (kernel_q1.cuh:199-397)
-    int32_t first = expand(a.medoid);
-    log_hop(a.medoid);
+    int32_t first = expand(entry);
+    log_hop(entry);
     step = 1;
     if (check()) {
       stop = true;
@@ -691,6 +703,9 @@ void release_index(qv_index* ix) {
   hipFree(ix->d_counters);
   hipHostFree(ix->h_ctrl);
   hipFree(ix->d_bits);
+  hipFree(ix->d_nav_data);
+  hipFree(ix->d_nav_graph);
+  hipFree(ix->d_nav_map);
   hipFree(ix->d_pages);
   hipFree(ix->d_codes);
   hipFree(ix->d_centroid);
@@ -791,7 +806,35 @@ qv_index* open_index(const std::string& index_dir, const std::string& dtype_s,
   HIP_OK(hipMemcpy(d_codes, pq.codes.data(), code_bytes, hipMemcpyHostToDevice));
   pg.release();
   cg.release();
-  return make_index(device, lay, pq, d_pages, d_codes, true);
+  std::unique_ptr<qv_index, void (*)(qv_index*)> ix(make_index(device, lay, pq, d_pages, d_codes, true),
+                                                     release_index);
+  const std::string nav_dir = find_nav_dir(index_dir);  // search_setup.hpp:96-106
+  if (!nav_dir.empty()) load_nav(ix.get(), nav_dir);
+  return ix.release();
+}
+
+// NavGraph::init + copy_to_dev (nav_graph.cu:12-73) into this handle's device.
+void load_nav(qv_index* ix, const std::string& dir) {
+  NavGraphHost nav;
+  read_nav(dir, ix->lay.data_type, ix->lay.num_data, ix->lay.num_dims, nav);
+  HIP_OK(hipSetDevice(ix->device));
+  uint8_t* dd = nullptr;
+  int32_t *dg = nullptr, *dm = nullptr;
+  HIP_OK(hipMalloc(&dd, nav.data.size()));
+  HIP_OK(hipMalloc(&dg, sizeof(int32_t) * nav.graph.size()));
+  HIP_OK(hipMalloc(&dm, sizeof(int32_t) * nav.mapping.size()));
+  HIP_OK(hipMemcpy(dd, nav.data.data(), nav.data.size(), hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(dg, nav.graph.data(), sizeof(int32_t) * nav.graph.size(), hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(dm, nav.mapping.data(), sizeof(int32_t) * nav.mapping.size(), hipMemcpyHostToDevice));
+  hipFree(ix->d_nav_data);
+  hipFree(ix->d_nav_graph);
+  hipFree(ix->d_nav_map);
+  ix->d_nav_data = dd;
+  ix->d_nav_graph = dg;
+  ix->d_nav_map = dm;
+  ix->nav_nodes = nav.num_node;
+  ix->nav_max_m = nav.max_m;
+  ix->nav_start = nav.start;
 }
 
 qv_index* make_index(int device, const Layout& lay, const PQTables& pq, uint8_t* d_pages,
@@ -873,6 +916,12 @@ static SearchArgs base_args(qv_index* ix) {
   a.medoid = (int32_t)L.enter_point;
   a.bits = ix->d_bits;
   a.bits_words = ix->bits_words;
+  a.nav_data = ix->d_nav_data;
+  a.nav_graph = ix->d_nav_graph;
+  a.nav_map = ix->d_nav_map;
+  a.nav_nodes = ix->nav_nodes;
+  a.nav_max_m = ix->nav_max_m;
+  a.nav_start = ix->nav_start;
   return a;
 }
 
@@ -997,6 +1046,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   a.ef = ef;
   a.pipe_w = o.pipe_width;
   a.early_exit = o.early_exit;
+  if (o.skip_nav) a.nav_data = nullptr;  // --skip-nav (quiver_search.cu:241-246)
   a.warmup = o.gpruning_warmup;
   a.patience = o.gpruning_patience;
   a.out_ids = d_ids;
@@ -1161,6 +1211,8 @@ void qv_search_opts_default(qv_search_opts* o) {
   o->admission = QV_ADMIT_STREAMING;
   o->device_buffers = 0;
   o->timeout_s = 0.0;
+  o->skip_nav = 0;
+  o->reserved0 = 0;
 }
 
 int qv_index_open(const char* index_dir, const char* data_type, const char* memory_backend,
@@ -1170,6 +1222,14 @@ int qv_index_open(const char* index_dir, const char* data_type, const char* memo
     *out = nullptr;
     *out = qv::open_index(index_dir, data_type, memory_backend ? memory_backend : "heap",
                           memory_index_file ? memory_index_file : "", device);
+  });
+}
+
+int qv_index_load_nav(qv_index* ix, const char* nav_dir) {
+  return qv::guard([&] {
+    if (!ix || !nav_dir) qv::fail(QV_EINVAL, "null argument");
+    std::lock_guard<std::mutex> lk(ix->mu);
+    qv::load_nav(ix, nav_dir);
   });
 }
 
@@ -1191,6 +1251,8 @@ int qv_index_get_info(const qv_index* ix, qv_index_info* info) {
     HIP_OK(hipSetDevice(ix->device));
     info->slots_per_cu = qv::slots_per_cu(const_cast<qv_index*>(ix), 64);
     info->device_bytes = ix->device_bytes;
+    info->nav_nodes = ix->nav_nodes;
+    info->nav_max_m = ix->nav_max_m;
   });
 }
 

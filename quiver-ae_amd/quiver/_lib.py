@@ -51,6 +51,9 @@ class IndexInfo(C.Structure):
         ("device", C.c_int32),
         ("slots_per_cu", C.c_int32),
         ("device_bytes", C.c_int64),
+        ("nav_nodes", C.c_int64),
+        ("nav_max_m", C.c_int32),
+        ("reserved", C.c_int32),
     ]
 
 
@@ -67,6 +70,8 @@ class SearchOpts(C.Structure):
         ("admission", C.c_int32),
         ("device_buffers", C.c_int32),
         ("timeout_s", C.c_double),
+        ("skip_nav", C.c_int32),
+        ("reserved0", C.c_int32),
     ]
 
 
@@ -129,6 +134,8 @@ _I64 = C.c_int64
 SIGNATURES = {
     "qv_index_open": (_I32, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int, C.POINTER(_P)]),
     "qv_index_get_info": (_I32, [_P, C.POINTER(IndexInfo)]),
+    "qv_index_load_nav": (_I32, [_P, C.c_char_p]),
+    "qv_build_nav": (_I32, [_P, _P, _I64, _I32, _I32, C.POINTER(BuildParams), C.c_char_p]),
     "qv_index_close": (None, [_P]),
     "qv_search_opts_default": (None, [C.POINTER(SearchOpts)]),
     "qv_search": (_I32, [_P, _P, _I64, _I32, _I32, _I32, C.POINTER(SearchOpts), _P, _P, _P,

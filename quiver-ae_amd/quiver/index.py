@@ -168,8 +168,11 @@ class IndexQuiver:
         return {name: getattr(info, name) for name, _ in info._fields_}
 
     def _search_inprocess(self, array, topk, ef_search, early_exit_policy, timeout, extra_args):
-        if extra_args:
-            raise QuiverError("extra_args needs an external quiver_search binary")
+        extra = [str(x) for x in extra_args]
+        skip_nav = "--skip-nav" in extra
+        extra = [x for x in extra if x != "--skip-nav"]
+        if extra:
+            raise QuiverError("extra_args other than --skip-nav need an external quiver_search binary")
         if self.num_ssds:
             raise QuiverError("This binary was built without SPDK support")
         handle = self._open()
@@ -189,6 +192,7 @@ class IndexQuiver:
         if "QUIVER_ADMIT_MIN_BATCH" in env:
             opts.admit_min_batch = max(1, int(env["QUIVER_ADMIT_MIN_BATCH"]))
         opts.timeout_s = float(timeout) if timeout is not None else 0.0
+        opts.skip_nav = 1 if skip_nav else 0
         rep = _lib.SearchReport()
         rc = _lib.load().qv_search(
             handle, q.ctypes.data, n, d, topk, ef_search, C.byref(opts),
@@ -199,6 +203,12 @@ class IndexQuiver:
         _lib.check(rc)
         self.last_report = rep.as_dict()
         return ids, dists
+
+    def load_nav(self, nav_dir: str | os.PathLike[str]) -> None:
+        """Load (or replace) the navigation graph that picks each query's entry
+        node (nav_index, nav_index.data, map.txt).  An index directory holding
+        nav_index or nav/nav_index gets its graph at open without this call."""
+        _lib.check(_lib.load().qv_index_load_nav(self._open(), str(nav_dir).encode()))
 
     def close(self) -> None:
         if self._handle is not None:
@@ -357,6 +367,37 @@ def build_index(
     p.kmeans_iters, p.pq_train_max, p.seed, p.threads, p.passes = kmeans_iters, pq_train_max, seed, threads, passes
     _lib.check(_lib.load().qv_build_index_cpu(arr.ctypes.data, dtype, arr.shape[0], arr.shape[1],
                                               C.byref(p), str(out_prefix).encode()))
+
+
+def build_nav(
+    rows: npt.ArrayLike,
+    ids: npt.ArrayLike,
+    out_dir: str | os.PathLike[str],
+    *,
+    R: int = 28,
+    L: int = 64,
+    alpha: float = 1.2,
+    seed: int = 0x5EED5EED,
+    threads: int = 0,
+    passes: int = 2,
+) -> None:
+    """Build a navigation graph over `rows` (a sample of the base vectors whose
+    base ids are `ids`) and write nav_index, nav_index.data and map.txt."""
+    arr = np.ascontiguousarray(rows)
+    idv = np.ascontiguousarray(ids, dtype=np.int32)
+    if arr.ndim != 2 or idv.shape != (arr.shape[0],):
+        raise ValueError("rows must be 2D and ids one per row")
+    dtype = {np.dtype("u1"): _lib.QV_UINT8, np.dtype("i1"): _lib.QV_INT8,
+             np.dtype("<f4"): _lib.QV_FLOAT}.get(arr.dtype)
+    if dtype is None:
+        raise ValueError("rows dtype must be uint8, int8 or float32")
+    if not 1 <= R <= 32:
+        raise ValueError("R must be in [1, 32] (the nav graph's row limit)")
+    p = _lib.default_build_params()
+    p.R, p.L, p.alpha, p.seed, p.threads, p.passes = R, L, alpha, seed, threads, passes
+    Path(out_dir).mkdir(parents=True, exist_ok=True)
+    _lib.check(_lib.load().qv_build_nav(arr.ctypes.data, idv.ctypes.data, arr.shape[0], arr.shape[1], dtype,
+                                        C.byref(p), str(out_dir).encode()))
 
 
 def mixture(rows: int, dim: int, *, data_type: str = "uint8", num_centers: int = 1024,

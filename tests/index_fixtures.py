@@ -59,3 +59,21 @@ def exact_pq(vectors: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray, n
     offsets = np.arange(dim + 1, dtype=np.int32)
     codes = vectors.astype(np.uint8)
     return pivots, centroid, offsets, codes
+
+
+def write_nav(nav_dir: Path, data: np.ndarray, graph: np.ndarray, mapping: np.ndarray, start: int) -> None:
+    """The three nav-graph files NavGraph::init reads (src/shared/index/
+    nav_graph.cu:12-71): nav_index.data (i32 num_node, i32 dims, vectors),
+    map.txt (one base id per line), nav_index (u64 file size, u32 max degree,
+    u32 start, u64 frozen points, then per node a u32 degree and its ids)."""
+    d = Path(nav_dir)
+    d.mkdir(parents=True, exist_ok=True)
+    n, dims = data.shape
+    (d / "nav_index.data").write_bytes(struct.pack("<ii", n, dims) + np.ascontiguousarray(data).tobytes())
+    (d / "map.txt").write_text("".join(f"{int(x)}\n" for x in mapping))
+    max_m = graph.shape[1]
+    body = bytearray()
+    for i in range(n):
+        nb = [int(v) for v in graph[i] if v >= 0]
+        body += struct.pack(f"<I{len(nb)}I", len(nb), *nb)
+    (d / "nav_index").write_bytes(struct.pack("<QIIQ", 24 + len(body), max_m, start, 0) + bytes(body))
