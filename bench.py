@@ -65,6 +65,10 @@ def main() -> int:
                     help="run only the ADC microbenchmark leg (prints its JSON object)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="run one device-to-device copy of this size first (counter calibration)")
+    ap.add_argument("--graph-placement", default="hbm", choices=("hbm", "host"),
+                    help="page image in HBM (default) or in pinned host memory")
+    ap.add_argument("--nav-sample", type=int, default=0,
+                    help="build a nav graph over every K-th base vector and start queries from it (0: medoid)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1",
@@ -130,6 +134,23 @@ def main() -> int:
     _lib.check(L.qv_ground_truth(d_base.ptr, dtype_code, n, dim, d_q.ptr, nq, 10, d_gi.ptr, d_gd.ptr, 0))
     gt = d_gi.download(np.int32, (nq, 10))
     log(f"ground truth: {time.time() - t:.1f}s")
+
+    if args.graph_placement == "host":
+        _lib.check(L.qv_index_place_graph(h, _lib.QV_GRAPH_HOST))
+        log("page image moved to pinned host memory")
+    if args.nav_sample > 0:
+        import tempfile
+
+        import quiver
+
+        t = time.time()
+        sample = np.arange(0, n, args.nav_sample, dtype=np.int32)
+        rows = d_base.download(np.uint8 if is_u8 else np.float32, (n, dim))[sample]
+        nav_dir = tempfile.mkdtemp(prefix="qv_nav_")
+        quiver.build_nav(rows, sample, nav_dir, R=28, L=64)
+        del rows
+        _lib.check(L.qv_index_load_nav(h, nav_dir.encode()))
+        log(f"nav graph over {sample.size} sampled vectors: {time.time() - t:.1f}s")
 
     info = _lib.IndexInfo()
     _lib.check(L.qv_index_get_info(h, C.byref(info)))
@@ -236,6 +257,7 @@ def main() -> int:
         "config": {"workload": f"{args.workload}: {n} x {dim} {w['dtype']} mixture ({w['centers']} centres), "
                                f"Vamana R={w['R']} L={w['L']} alpha=1.2, PQ {w['M']}x256, {nq} queries, top-10",
                    "ef_search": ef, "early_exit": pname, "pipe_width": 1, "num_blocks": last.num_blocks,
+                   "graph_placement": args.graph_placement, "nav_nodes": int(info.nav_nodes),
                    "admission": "streaming (window = num_blocks)", "recall_at_10": round(recall, 4),
                    "p50_ms": round(p50, 3), "p99_ms": round(p99, 3), "avg_hops": round(last.avg_hops, 2),
                    "build_s": round(build_s, 1)},

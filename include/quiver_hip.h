@@ -25,7 +25,7 @@ extern "C" {
 #define QV_EIO -2         /* file missing, short or malformed */
 #define QV_EHIP -3        /* HIP runtime error */
 #define QV_ETIMEDOUT -4   /* search exceeded qv_search_opts.timeout_s */
-#define QV_EUNSUPPORTED -5/* feature outside this build (SPDK, mmap, R > 64, ...) */
+#define QV_EUNSUPPORTED -5/* feature outside this build (SPDK, R > 64, ...) */
 #define QV_ENOMEM -6      /* host or device allocation failed */
 #define QV_EINDEX -7      /* index content invalid (ids out of range, ...) */
 
@@ -72,12 +72,33 @@ typedef struct {
  * (src/shared/index/pq_search.cu:62-114), create_mem_loader_sync heap mode
  * (src/shared/io/mem_loader.cpp:28-44) and PQSearch::init_device
  * (src/shared/index/pq_search.cu:116-177).  The page image, the codes and the PQ
- * tables are placed in HBM of `device`.  memory_backend is "heap"; "mmap" returns
- * QV_EUNSUPPORTED.  memory_index_file may be NULL (defaults to the discovered
- * index file, as --memory-index-file does). */
+ * tables are placed in HBM of `device`.  memory_backend "heap" reads the page
+ * image with stdio (mem_loader.cpp:28-44), "mmap" maps the file read-only and
+ * checks its size as mem_loader.cpp:46-85 does; both copy it once, at open.
+ * memory_index_file may be NULL (defaults to the discovered index file, as
+ * --memory-index-file does). */
 int qv_index_open(const char* index_dir, const char* data_type,
                   const char* memory_backend, const char* memory_index_file,
                   int device, qv_index** out);
+
+/* Where the page image (vectors + adjacency, the bulk of an index) lives. */
+#define QV_GRAPH_HBM 0  /* device memory (default) */
+#define QV_GRAPH_HOST 1 /* pinned host memory the kernel reads over the host link,
+                           for indexes larger than HBM; codes, tables and search
+                           state stay in HBM.  The reference's own placement: its
+                           memory backend keeps the graph in host memory and its
+                           loader copies pages into GPU-visible buffers
+                           (mem_loader.cpp:98-117). */
+
+/* qv_index_open with an explicit page-image placement (QV_GRAPH_*). */
+int qv_index_open_ex(const char* index_dir, const char* data_type,
+                     const char* memory_backend, const char* memory_index_file,
+                     int device, int32_t graph_placement, qv_index** out);
+
+/* Moves the page image of an open handle (QV_GRAPH_HBM <-> QV_GRAPH_HOST),
+ * e.g. to serve a GPU-built index from host memory.  No reference counterpart:
+ * the reference fixes the placement by its loader choice at startup. */
+int qv_index_place_graph(qv_index* index, int32_t graph_placement);
 
 int qv_index_get_info(const qv_index* index, qv_index_info* out);
 
@@ -109,8 +130,10 @@ void qv_index_close(qv_index* index);
 /* Options of run_persistent_search (src/quiver/search.cuh:45-66) and of the
  * quiver_search CLI (bin/quiver_search.cu:61-147). */
 typedef struct {
-  int32_t num_blocks;        /* persistent workgroups (--num-blocks); 0 fills the GPU */
-  int32_t queries_per_block; /* --queries-per-block; only 1 is supported */
+  int32_t num_blocks;        /* --num-blocks; 0 fills the GPU */
+  int32_t queries_per_block; /* --queries-per-block, 1..8: num_blocks x this many query
+                                slots (search.cu:393-399), each a one-wave workgroup;
+                                the launch stops at the device's resident capacity */
   int32_t pipe_width;        /* --pipe-width, 1..16 */
   int32_t early_exit;        /* QV_EXIT_NONE / QV_EXIT_GPRUNING */
   int32_t gpruning_warmup;   /* 10 in the reference CLI */
@@ -131,8 +154,8 @@ typedef struct {
   double lat_avg_ms, lat_p50_ms, lat_p90_ms, lat_p99_ms, lat_p999_ms, lat_max_ms;
   double avg_hops;           /* expanded nodes per query (finish step) */
   double kernel_ms;          /* search kernel duration from HIP events */
-  int32_t num_blocks;
-  int32_t max_inflight;
+  int32_t num_blocks;        /* workgroups launched (= concurrent query slots) */
+  int32_t max_inflight;      /* admission window: slots + prefeed */
   int32_t early_stopped;     /* queries ended by gpruning */
   int32_t reserved;
   double total_hops;         /* expanded nodes over all queries */

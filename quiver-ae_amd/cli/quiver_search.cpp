@@ -30,6 +30,7 @@ const char* kUsage =
     "Usage: quiver_search --index-dir DIR --query FILE --data-type {uint8,int8,float}\n"
     "  [--topk 10] [--ef-search 30] [--repeat 20] [--ground-truth FILE]\n"
     "  [--memory-backend heap|mmap] [--memory-index-file FILE] [--ssd-list-file FILE]\n"
+    "  [--graph-placement hbm|host]\n"
     "  [--num-blocks 756] [--num-blocks-list L] [--pipe-width 2] [--queries-per-block 1]\n"
     "  [--poll-threads 6] [--runners-per-ssd 1] [--early-exit-policy gpruning|none]\n"
     "  [--result-prefix P] [--final-recall-csv F] [--skip-nav] [--help]\n";
@@ -113,7 +114,7 @@ int main(int argc, char** argv) {
                                "--spdk-runner-io-contexts", "--pipe-width", "--queries-per-block",
                                "--runners-per-ssd", "--num-blocks-list", "--recall-threshold",
                                "--step-recall-csv", "--final-recall-csv", "--result-prefix",
-                               "--early-exit-policy"};
+                               "--early-exit-policy", "--graph-placement"};
   const char* bool_flags[] = {"--skip-nav", "--per-step-recall", "--help"};
   for (auto* s : value_flags) f[s] = Flag{};
   for (auto* s : bool_flags) f[s] = Flag{"", false, true};
@@ -127,6 +128,7 @@ int main(int argc, char** argv) {
   f["--queries-per-block"].value = "1";
   f["--runners-per-ssd"].value = "1";
   f["--early-exit-policy"].value = "gpruning";
+  f["--graph-placement"].value = "hbm";
   for (int i = 1; i < argc; i++) {
     std::string a = argv[i];
     auto it = f.find(a);
@@ -224,8 +226,14 @@ int main(int argc, char** argv) {
 
   qv_index* ix = nullptr;
   const char* mem_file = f["--memory-index-file"].used ? f["--memory-index-file"].value.c_str() : nullptr;
-  if (qv_index_open(f["--index-dir"].value.c_str(), f["--data-type"].value.c_str(),
-                    f["--memory-backend"].value.c_str(), mem_file, 0, &ix) != QV_OK) {
+  const std::string placement = f["--graph-placement"].value;
+  if (placement != "hbm" && placement != "host") {
+    std::cerr << "--graph-placement must be hbm or host" << std::endl;
+    return 1;
+  }
+  if (qv_index_open_ex(f["--index-dir"].value.c_str(), f["--data-type"].value.c_str(),
+                       f["--memory-backend"].value.c_str(), mem_file, 0,
+                       placement == "host" ? QV_GRAPH_HOST : QV_GRAPH_HBM, &ix) != QV_OK) {
     std::cerr << qv_last_error() << std::endl;
     return 1;
   }

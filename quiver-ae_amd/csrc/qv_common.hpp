@@ -17,6 +17,7 @@ constexpr int kMaxDegree = 64;        // one wavefront lane per neighbour
 constexpr int kMaxEf = 448;           // beam + 64 new candidates fit 8 lane slots
 constexpr int kMaxTopk = 64;          // one top-k entry per lane
 constexpr int kMaxPipeWidth = 16;     // bin/common/cli_validation.hpp:9
+constexpr int kMaxQueriesPerBlock = 8; // bin/common/cli_validation.hpp:10
 
 // Error carrying a QV_* status; converted at the C ABI boundary.
 struct Error : std::runtime_error {

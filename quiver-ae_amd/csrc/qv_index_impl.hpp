@@ -15,7 +15,8 @@ struct qv_index {
   int device = 0;
   qv::Layout lay;
   int M = 0;
-  uint8_t* d_pages = nullptr;
+  uint8_t* d_pages = nullptr;  // HBM, or pinned host memory when pages_in_host
+  bool pages_in_host = false;
   uint8_t* d_codes = nullptr;
   float* d_centroid = nullptr;
   float* d_pivots_t = nullptr;
@@ -68,8 +69,9 @@ struct SearchRecord {
 
 // Creates a handle around device buffers the caller allocated with hipMalloc
 // (ownership moves to the handle) and host PQ tables; validates the graph.
+// With pages_in_host the page image is pinned host memory from hipHostMalloc.
 qv_index* make_index(int device, const Layout& lay, const PQTables& pq, uint8_t* d_pages,
-                     uint8_t* d_codes, bool validate);
+                     uint8_t* d_codes, bool validate, bool pages_in_host = false);
 
 void release_index(qv_index* ix);
 

@@ -13,7 +13,13 @@
 //     instead of merge-path rounds with block barriers;
 //   * a device work queue (atomic ticket) gated by a host-written feed count,
 //     completion published to a host ring so per-query latency is exact.
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include <algorithm>
+#include <cerrno>
 #include <chrono>
 #include <cmath>
 #include <cstring>
@@ -706,7 +712,10 @@ void release_index(qv_index* ix) {
   hipFree(ix->d_nav_data);
   hipFree(ix->d_nav_graph);
   hipFree(ix->d_nav_map);
-  hipFree(ix->d_pages);
+  if (ix->pages_in_host)
+    hipHostFree(ix->d_pages);
+  else
+    hipFree(ix->d_pages);
   hipFree(ix->d_codes);
   hipFree(ix->d_centroid);
   hipFree(ix->d_pivots_t);
@@ -717,22 +726,73 @@ void release_index(qv_index* ix) {
   delete ix;
 }
 
-// Copies a host file region to device memory through a pinned staging buffer.
-static void upload_index_pages(const std::string& path, int64_t num_pages, uint8_t* dst) {
+// Source of the page image: the file read with stdio (heap backend,
+// mem_loader.cpp:28-44) or mapped read-only (mmap backend, mem_loader.cpp:46-85,
+// including its size check).  Either way the pages are copied once, at open,
+// to where the kernel reads them.
+class PageSource {
+ public:
+  PageSource(const std::string& path, int64_t num_pages, bool use_mmap) : path_(path) {
+    if (!use_mmap) {
+      f_ = std::fopen(path.c_str(), "rb");
+      if (!f_) fail(QV_EIO, "Failed to open Mem Index: " + path);
+      if (std::fseek(f_, kPageSize, SEEK_SET) != 0) fail(QV_EIO, "Failed to seek Mem Index: " + path);
+      return;
+    }
+    fd_ = ::open(path.c_str(), O_RDONLY);
+    if (fd_ < 0) fail(QV_EIO, "Failed to open mmap Mem Index " + path + ": " + std::strerror(errno));
+    struct stat st {};
+    if (::fstat(fd_, &st) != 0) fail(QV_EIO, "Failed to stat mmap Mem Index " + path + ": " + std::strerror(errno));
+    const int64_t required = (num_pages + 1) * kPageSize;
+    if ((int64_t)st.st_size < required)
+      fail(QV_EIO, "mmap Mem Index " + path + " is too small: size=" + std::to_string((long long)st.st_size) +
+                       " required=" + std::to_string((long long)required));
+    len_ = (size_t)st.st_size;
+    void* m = ::mmap(nullptr, len_, PROT_READ, MAP_PRIVATE, fd_, 0);
+    if (m == MAP_FAILED) fail(QV_EIO, "Failed to mmap Mem Index " + path + ": " + std::strerror(errno));
+    map_ = static_cast<uint8_t*>(m);
+    ::madvise(map_, len_, MADV_SEQUENTIAL);
+  }
+  ~PageSource() {
+    if (f_) std::fclose(f_);
+    if (map_) ::munmap(map_, len_);
+    if (fd_ >= 0) ::close(fd_);
+  }
+  // Copies pages [p, p + cnt) of the image (file page p + 1) to host memory dst.
+  void read(int64_t p, int64_t cnt, uint8_t* dst) {
+    if (map_) {
+      std::memcpy(dst, map_ + (p + 1) * kPageSize, (size_t)(cnt * kPageSize));
+      return;
+    }
+    const int64_t got = (int64_t)std::fread(dst, kPageSize, (size_t)cnt, f_);
+    if (got != cnt)
+      fail(QV_EIO, "Mem Index Load FAILED: " + std::to_string(p + got) + " pages read from " + path_);
+  }
+
+ private:
+  std::string path_;
+  FILE* f_ = nullptr;
+  int fd_ = -1;
+  uint8_t* map_ = nullptr;
+  size_t len_ = 0;
+};
+
+// Copies the page image to HBM through a pinned staging buffer, or straight
+// into dst when dst is pinned host memory.
+static void upload_index_pages(PageSource& src, int64_t num_pages, uint8_t* dst, bool dst_in_host) {
   const int64_t chunk_pages = 16384;  // 64 MB
+  if (dst_in_host) {
+    for (int64_t p = 0; p < num_pages; p += chunk_pages)
+      src.read(p, std::min(chunk_pages, num_pages - p), dst + p * kPageSize);
+    return;
+  }
   uint8_t* stage = nullptr;
   HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&stage), (size_t)(chunk_pages * kPageSize),
                        hipHostMallocDefault));
   std::unique_ptr<uint8_t, void (*)(uint8_t*)> guard(stage, [](uint8_t* p) { hipHostFree(p); });
-  FILE* f = std::fopen(path.c_str(), "rb");
-  if (!f) fail(QV_EIO, "Failed to open Mem Index: " + path);
-  std::unique_ptr<FILE, int (*)(FILE*)> fg(f, &std::fclose);
-  if (std::fseek(f, kPageSize, SEEK_SET) != 0) fail(QV_EIO, "Failed to seek Mem Index: " + path);
   for (int64_t p = 0; p < num_pages; p += chunk_pages) {
     const int64_t cnt = std::min(chunk_pages, num_pages - p);
-    const int64_t got = (int64_t)std::fread(stage, kPageSize, (size_t)cnt, f);
-    if (got != cnt)
-      fail(QV_EIO, "Mem Index Load FAILED: " + std::to_string(p + got) + " pages read from " + path);
+    src.read(p, cnt, stage);
     HIP_OK(hipMemcpy(dst + p * kPageSize, stage, (size_t)(cnt * kPageSize), hipMemcpyHostToDevice));
   }
 }
@@ -767,11 +827,12 @@ void validate_graph(qv_index* ix) {
 }
 
 qv_index* open_index(const std::string& index_dir, const std::string& dtype_s,
-                     const std::string& backend, const std::string& mem_file, int device) {
+                     const std::string& backend, const std::string& mem_file, int device, int placement) {
   const int dtype = parse_data_type(dtype_s);
-  if (backend == "mmap") fail(QV_EUNSUPPORTED, "memory backend 'mmap' is not supported; use heap");
-  if (backend != "heap")
+  if (backend != "heap" && backend != "mmap")
     fail(QV_EINVAL, "Unsupported --memory-backend '" + backend + "'. Expected one of: heap, mmap");
+  if (placement != QV_GRAPH_HBM && placement != QV_GRAPH_HOST)
+    fail(QV_EINVAL, "graph placement must be QV_GRAPH_HBM or QV_GRAPH_HOST");
   const std::string index_file = find_index_file(index_dir);
   const std::string pages_file = mem_file.empty() ? index_file : mem_file;
   const std::string prefix = find_pq_prefix(index_dir);
@@ -789,6 +850,7 @@ qv_index* open_index(const std::string& index_dir, const std::string& dtype_s,
   if ((lay.data_size & 3) || (lay.node_size & 3))
     fail(QV_EUNSUPPORTED, "node records must be 4-byte aligned");
   if (lay.num_data > INT32_MAX) fail(QV_EUNSUPPORTED, "more than 2^31-1 points");
+  PageSource src(pages_file, lay.num_pages, backend == "mmap");
 
   int ndev = 0;
   HIP_OK(hipGetDeviceCount(&ndev));
@@ -796,18 +858,26 @@ qv_index* open_index(const std::string& index_dir, const std::string& dtype_s,
   HIP_OK(hipSetDevice(device));
   const size_t page_bytes = (size_t)(lay.num_pages * kPageSize);
   const size_t code_bytes = (size_t)lay.num_data * (size_t)pq.num_chunks;
+  const bool in_host = placement == QV_GRAPH_HOST;
   uint8_t* d_pages = nullptr;
   uint8_t* d_codes = nullptr;
-  HIP_OK(hipMalloc(&d_pages, page_bytes));
-  std::unique_ptr<uint8_t, void (*)(uint8_t*)> pg(d_pages, [](uint8_t* p) { (void)hipFree(p); });
+  if (in_host) {
+    // Pinned, device-mapped host memory, cached by the GPU (written once here,
+    // before any kernel reads it, and never again).
+    HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&d_pages), page_bytes, hipHostMallocNonCoherent));
+  } else {
+    HIP_OK(hipMalloc(&d_pages, page_bytes));
+  }
+  std::unique_ptr<uint8_t, void (*)(uint8_t*)> pg(
+      d_pages, in_host ? +[](uint8_t* p) { (void)hipHostFree(p); } : +[](uint8_t* p) { (void)hipFree(p); });
   HIP_OK(hipMalloc(&d_codes, std::max<size_t>(code_bytes, 64)));
   std::unique_ptr<uint8_t, void (*)(uint8_t*)> cg(d_codes, [](uint8_t* p) { (void)hipFree(p); });
-  upload_index_pages(pages_file, lay.num_pages, d_pages);
+  upload_index_pages(src, lay.num_pages, d_pages, in_host);
   HIP_OK(hipMemcpy(d_codes, pq.codes.data(), code_bytes, hipMemcpyHostToDevice));
   pg.release();
   cg.release();
-  std::unique_ptr<qv_index, void (*)(qv_index*)> ix(make_index(device, lay, pq, d_pages, d_codes, true),
-                                                     release_index);
+  std::unique_ptr<qv_index, void (*)(qv_index*)> ix(
+      make_index(device, lay, pq, d_pages, d_codes, true, in_host), release_index);
   const std::string nav_dir = find_nav_dir(index_dir);  // search_setup.hpp:96-106
   if (!nav_dir.empty()) load_nav(ix.get(), nav_dir);
   return ix.release();
@@ -838,12 +908,13 @@ void load_nav(qv_index* ix, const std::string& dir) {
 }
 
 qv_index* make_index(int device, const Layout& lay, const PQTables& pq, uint8_t* d_pages,
-                     uint8_t* d_codes, bool validate) {
+                     uint8_t* d_codes, bool validate, bool pages_in_host) {
   std::unique_ptr<qv_index, void (*)(qv_index*)> ix(new qv_index(), release_index);
   ix->device = device;
   ix->lay = lay;
   ix->M = pq.num_chunks;
   ix->d_pages = d_pages;
+  ix->pages_in_host = pages_in_host;
   ix->d_codes = d_codes;
   HIP_OK(hipSetDevice(device));
   hipDeviceProp_t prop;
@@ -855,7 +926,7 @@ qv_index* make_index(int device, const Layout& lay, const PQTables& pq, uint8_t*
   HIP_OK(hipMalloc(&ix->d_centroid, sizeof(float) * pq.centroid.size()));
   HIP_OK(hipMalloc(&ix->d_pivots_t, sizeof(float) * pq.pivots_t.size()));
   HIP_OK(hipMalloc(&ix->d_chunk_off, sizeof(int32_t) * pq.chunk_offsets.size()));
-  ix->device_bytes = (int64_t)(lay.num_pages * kPageSize + lay.num_data * pq.num_chunks +
+  ix->device_bytes = (int64_t)((pages_in_host ? 0 : lay.num_pages * kPageSize) + lay.num_data * pq.num_chunks +
                                4 * (int64_t)(pq.centroid.size() + pq.pivots_t.size()));
   HIP_OK(hipMemcpy(ix->d_centroid, pq.centroid.data(), sizeof(float) * pq.centroid.size(),
                    hipMemcpyHostToDevice));
@@ -997,8 +1068,8 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   if (topk <= 0 || topk > kMaxTopk) fail(QV_EINVAL, "topk must be in [1, 64]");
   if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 448]");
   if (o.pipe_width < 1 || o.pipe_width > kMaxPipeWidth) fail(QV_EINVAL, "--pipe-width must be in [1, 16]");
-  if (o.queries_per_block != 1)
-    fail(QV_EUNSUPPORTED, "--queries-per-block must be 1 in this build");
+  if (o.queries_per_block < 1 || o.queries_per_block > kMaxQueriesPerBlock)
+    fail(QV_EINVAL, "--queries-per-block must be in [1, 8]");
   if (o.early_exit != QV_EXIT_NONE && o.early_exit != QV_EXIT_GPRUNING)
     fail(QV_EINVAL, "early exit policy must be none or gpruning");
   if (o.num_blocks < 0) fail(QV_EINVAL, "--num-blocks must be positive");
@@ -1010,8 +1081,15 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   const LdsPlan pl = lds_plan(ix->M, (int)L.num_dims, P);
   const int spc = slots_per_cu(ix, ef);
   if (spc <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
-  const int num_blocks = o.num_blocks > 0 ? o.num_blocks : spc * ix->num_cus;
-  const int max_inflight = (int)std::min<int64_t>(nq, (int64_t)num_blocks + std::max(0, o.prefeed));
+  // Query slots (search.cu:393-399): num_blocks x queries_per_block.  Each slot
+  // is a one-wave workgroup, so the reference's Q-interleave -- a block
+  // switching between its slots while one waits on memory -- is the CU's own
+  // wave interleaving here.  Slots beyond what the device holds resident would
+  // only wait for a free CU, so the grid stops at the resident capacity; the
+  // admission window keeps the requested slot count.
+  const int64_t slots = (int64_t)(o.num_blocks > 0 ? o.num_blocks : spc * ix->num_cus) * o.queries_per_block;
+  const int num_blocks = (int)std::min<int64_t>(slots, (int64_t)spc * ix->num_cus);
+  const int max_inflight = (int)std::min<int64_t>(nq, slots + std::max(0, o.prefeed));
   ensure_bits(ix, num_blocks);
 
   const float* d_q = queries;
@@ -1221,7 +1299,50 @@ int qv_index_open(const char* index_dir, const char* data_type, const char* memo
     if (!index_dir || !data_type || !out) qv::fail(QV_EINVAL, "null argument");
     *out = nullptr;
     *out = qv::open_index(index_dir, data_type, memory_backend ? memory_backend : "heap",
-                          memory_index_file ? memory_index_file : "", device);
+                          memory_index_file ? memory_index_file : "", device, QV_GRAPH_HBM);
+  });
+}
+
+int qv_index_open_ex(const char* index_dir, const char* data_type, const char* memory_backend,
+                     const char* memory_index_file, int device, int32_t graph_placement, qv_index** out) {
+  return qv::guard([&] {
+    if (!index_dir || !data_type || !out) qv::fail(QV_EINVAL, "null argument");
+    *out = nullptr;
+    *out = qv::open_index(index_dir, data_type, memory_backend ? memory_backend : "heap",
+                          memory_index_file ? memory_index_file : "", device, graph_placement);
+  });
+}
+
+int qv_index_place_graph(qv_index* ix, int32_t graph_placement) {
+  return qv::guard([&] {
+    if (!ix) qv::fail(QV_EINVAL, "null argument");
+    if (graph_placement != QV_GRAPH_HBM && graph_placement != QV_GRAPH_HOST)
+      qv::fail(QV_EINVAL, "graph placement must be QV_GRAPH_HBM or QV_GRAPH_HOST");
+    std::lock_guard<std::mutex> lk(ix->mu);
+    const bool to_host = graph_placement == QV_GRAPH_HOST;
+    if (to_host == ix->pages_in_host) return;
+    HIP_OK(hipSetDevice(ix->device));
+    const size_t bytes = (size_t)(ix->lay.num_pages * qv::kPageSize);
+    uint8_t* p = nullptr;
+    if (to_host)
+      HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&p), bytes, hipHostMallocNonCoherent));
+    else
+      HIP_OK(hipMalloc(&p, bytes));
+    const hipError_t e = hipMemcpy(p, ix->d_pages, bytes, hipMemcpyDefault);
+    if (e != hipSuccess) {
+      if (to_host)
+        hipHostFree(p);
+      else
+        hipFree(p);
+      HIP_OK(e);
+    }
+    if (ix->pages_in_host)
+      hipHostFree(ix->d_pages);
+    else
+      hipFree(ix->d_pages);
+    ix->d_pages = p;
+    ix->pages_in_host = to_host;
+    ix->device_bytes += to_host ? -(int64_t)bytes : (int64_t)bytes;
   });
 }
 
@@ -1276,7 +1397,7 @@ int qv_index_save(const qv_index* ix, const char* out_prefix) {
     const Layout& L = ix->lay;
     HIP_OK(hipSetDevice(ix->device));
     std::vector<uint8_t> pages((size_t)(L.num_pages * kPageSize));
-    HIP_OK(hipMemcpy(pages.data(), ix->d_pages, pages.size(), hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(pages.data(), ix->d_pages, pages.size(), hipMemcpyDefault));
     const std::string pre = out_prefix;
     qv::write_index_image(pre + "_disk.index", L, pages.data());
     qv::PQTables t;
@@ -1298,7 +1419,7 @@ int qv_index_copy_out(const qv_index* ix, uint8_t* pages, uint8_t* codes, float*
     if (!ix) qv::fail(QV_EINVAL, "null index");
     const Layout& L = ix->lay;
     HIP_OK(hipSetDevice(ix->device));
-    if (pages) HIP_OK(hipMemcpy(pages, ix->d_pages, (size_t)(L.num_pages * kPageSize), hipMemcpyDeviceToHost));
+    if (pages) HIP_OK(hipMemcpy(pages, ix->d_pages, (size_t)(L.num_pages * kPageSize), hipMemcpyDefault));
     if (codes) HIP_OK(hipMemcpy(codes, ix->d_codes, (size_t)L.num_data * ix->M, hipMemcpyDeviceToHost));
     if (centroid) std::memcpy(centroid, ix->h_centroid.data(), sizeof(float) * ix->h_centroid.size());
     if (pivots) std::memcpy(pivots, ix->h_pivots.data(), sizeof(float) * ix->h_pivots.size());

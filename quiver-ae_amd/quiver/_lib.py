@@ -30,6 +30,8 @@ QV_EXIT_NONE = 0
 QV_EXIT_GPRUNING = 2
 QV_ADMIT_STREAMING = 0
 QV_ADMIT_BATCH = 1
+QV_GRAPH_HBM = 0
+QV_GRAPH_HOST = 1
 
 PKG_ROOT = Path(__file__).resolve().parents[1]
 LIB_PATH = PKG_ROOT / "lib" / "libquiver_hip.so"
@@ -133,6 +135,8 @@ _I64 = C.c_int64
 # name -> (restype, argtypes); every symbol declared in include/quiver_hip.h.
 SIGNATURES = {
     "qv_index_open": (_I32, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int, C.POINTER(_P)]),
+    "qv_index_open_ex": (_I32, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int, _I32, C.POINTER(_P)]),
+    "qv_index_place_graph": (_I32, [_P, _I32]),
     "qv_index_get_info": (_I32, [_P, C.POINTER(IndexInfo)]),
     "qv_index_load_nav": (_I32, [_P, C.c_char_p]),
     "qv_build_nav": (_I32, [_P, _P, _I64, _I32, _I32, C.POINTER(BuildParams), C.c_char_p]),

@@ -60,6 +60,7 @@ class IndexQuiver:
         runners_per_ssd: int = 1,
         env: Mapping[str, str] | None = None,
         device: int = 0,
+        graph_placement: str = "hbm",
     ) -> None:
         self.index_dir = Path(index_dir).expanduser().resolve()
         if not self.index_dir.is_dir():
@@ -88,6 +89,9 @@ class IndexQuiver:
         if memory_backend not in {"heap", "mmap"}:
             raise ValueError("memory_backend must be heap or mmap")
         self.memory_backend = memory_backend
+        if graph_placement not in {"hbm", "host"}:
+            raise ValueError("graph_placement must be hbm or host")
+        self.graph_placement = graph_placement
         self.binary = self._find_binary(binary)
         self.num_blocks = self._positive(num_blocks, "num_blocks")
         self.queries_per_block = self._positive(queries_per_block, "queries_per_block")
@@ -150,12 +154,13 @@ class IndexQuiver:
             lib = _lib.load()
             h = C.c_void_p()
             _lib.check(
-                lib.qv_index_open(
+                lib.qv_index_open_ex(
                     str(self.index_dir).encode(),
                     self.data_type.encode(),
                     self.memory_backend.encode(),
                     None,
                     self.device,
+                    _lib.QV_GRAPH_HOST if self.graph_placement == "host" else _lib.QV_GRAPH_HBM,
                     C.byref(h),
                 )
             )

@@ -49,10 +49,33 @@ def test_open_errors_are_reported_not_thrown(tmp_path):
     rc = lib.qv_index_open(str(tmp_path).encode(), b"complex64", b"heap", None, 0, C.byref(h))
     assert rc == _lib.QV_EINVAL and b"Unsupported data type" in lib.qv_last_error()
     rc = lib.qv_index_open(str(tmp_path).encode(), b"uint8", b"mmap", None, 0, C.byref(h))
-    assert rc == _lib.QV_EUNSUPPORTED
+    assert rc == _lib.QV_EIO  # no index files in an empty directory
+    rc = lib.qv_index_open_ex(str(tmp_path).encode(), b"uint8", b"heap", None, 0, 7, C.byref(h))
+    assert rc == _lib.QV_EINVAL and b"graph placement" in lib.qv_last_error()
     rc = lib.qv_index_open(str(tmp_path).encode(), b"uint8", b"disk", None, 0, C.byref(h))
     assert rc == _lib.QV_EINVAL
     lib.qv_index_close(None)  # accepted
+
+
+def test_mmap_backend_checks_file_size(tmp_path):
+    """--memory-backend mmap rejects an index file shorter than its pages, with
+    the reference's message (mem_loader.cpp:63-71), before any device work."""
+    import os
+
+    import numpy as np
+    from index_fixtures import exact_pq, write_index
+    from quiver import _lib
+
+    v = np.random.default_rng(0).integers(0, 256, (50, 8), dtype=np.uint8)
+    piv, cen, off, codes = exact_pq(v)
+    write_index(tmp_path / "t", v, [[(i + 1) % 50] for i in range(50)], 0, 4, piv, cen, off, codes)
+    f = tmp_path / "t_disk.index"
+    os.truncate(f, f.stat().st_size - 100)
+    lib = _lib.load()
+    h = C.c_void_p()
+    rc = lib.qv_index_open(str(tmp_path).encode(), b"uint8", b"mmap", None, 0, C.byref(h))
+    assert rc == _lib.QV_EIO
+    assert b"is too small: size=8092 required=8192" in lib.qv_last_error()
 
 
 def test_null_arguments_rejected():

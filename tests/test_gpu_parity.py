@@ -101,6 +101,106 @@ def test_search_batch_admission_and_hops(lib, small_u8_index):
     assert rep.qps > 0 and rep.lat_p99_ms >= rep.lat_p50_ms > 0
 
 
+@pytest.mark.parametrize("backend,placement", [("mmap", "hbm"), ("heap", "host"), ("mmap", "host")])
+def test_backends_and_graph_placement(lib, small_u8_index, backend, placement):
+    """The mmap backend and the page image in pinned host memory give the
+    oracle's answers, hop for hop."""
+    import quiver
+
+    ix = small_u8_index
+    _say(f"[gpu] backend={backend} placement={placement}")
+    index = quiver.IndexQuiver(ix["dir"], data_type="uint8", pipe_width=1, num_blocks=512,
+                               memory_backend=backend, graph_placement=placement)
+    ids, dists = index.search(ix["queries"], topk=10, ef_search=100, early_exit_policy="none")
+    info = index.info()
+    index.close()
+    host = O.HostIndex.from_files(ix["dir"], "uint8")
+    oids, odists, _, _ = O.search(host, ix["queries"].astype(np.float32), 10, 100, early_exit=O.EXIT_NONE)
+    np.testing.assert_array_equal(ids, oids)
+    np.testing.assert_array_equal(dists, odists)
+    pages = info["num_pages"] * 4096
+    assert (info["device_bytes"] < pages) == (placement == "host")
+
+
+def test_place_graph_round_trip(lib, small_u8_index):
+    """qv_index_place_graph moves the page image HBM -> host -> HBM; every
+    placement answers identically (ids, distances, hops)."""
+    from quiver import _lib
+
+    ix = small_u8_index
+    _say("[gpu] place_graph round trip")
+    L = _lib.load()
+    h = C.c_void_p()
+    _lib.check(L.qv_index_open(str(ix["dir"]).encode(), b"uint8", b"heap", None, 0, C.byref(h)))
+    q = np.ascontiguousarray(ix["queries"], dtype=np.float32)
+    n = q.shape[0]
+    outs = []
+    try:
+        for placement in (_lib.QV_GRAPH_HBM, _lib.QV_GRAPH_HOST, _lib.QV_GRAPH_HBM):
+            _lib.check(L.qv_index_place_graph(h, placement))
+            ids = np.empty((n, 10), np.int32)
+            dists = np.empty((n, 10), np.float32)
+            hops = np.empty(n, np.int32)
+            opts = _lib.default_search_opts()
+            opts.early_exit = _lib.QV_EXIT_NONE
+            rep = _lib.SearchReport()
+            _lib.check(L.qv_search(h, q.ctypes.data, n, 128, 10, 64, C.byref(opts), ids.ctypes.data,
+                                   dists.ctypes.data, None, C.byref(rep)))
+            _lib.check(L.qv_last_hops(h, hops.ctypes.data, n))
+            outs.append((ids, dists, hops))
+    finally:
+        L.qv_index_close(h)
+    for ids, dists, hops in outs[1:]:
+        np.testing.assert_array_equal(ids, outs[0][0])
+        np.testing.assert_array_equal(dists, outs[0][1])
+        np.testing.assert_array_equal(hops, outs[0][2])
+
+
+@pytest.mark.parametrize("num_blocks,qpb", [(64, 2), (100, 8), (500, 3)])
+def test_queries_per_block_slots(lib, small_u8_index, num_blocks, qpb):
+    """--queries-per-block Q gives num_blocks x Q query slots (search.cu:393-399);
+    answers are the oracle's for every slot count, and the launch is capped at
+    the device's resident capacity."""
+    from quiver import _lib
+
+    ix = small_u8_index
+    _say(f"[gpu] queries_per_block={qpb} num_blocks={num_blocks}")
+    L = _lib.load()
+    h = C.c_void_p()
+    _lib.check(L.qv_index_open(str(ix["dir"]).encode(), b"uint8", b"heap", None, 0, C.byref(h)))
+    q = np.ascontiguousarray(np.concatenate([ix["queries"]] * 8), dtype=np.float32)
+    n = q.shape[0]
+    ids = np.empty((n, 10), np.int32)
+    dists = np.empty((n, 10), np.float32)
+    hops = np.empty(n, np.int32)
+    info = _lib.IndexInfo()
+    try:
+        _lib.check(L.qv_index_get_info(h, C.byref(info)))
+        opts = _lib.default_search_opts()
+        opts.early_exit = _lib.QV_EXIT_GPRUNING
+        opts.num_blocks = num_blocks
+        opts.queries_per_block = qpb
+        rep = _lib.SearchReport()
+        _lib.check(L.qv_search(h, q.ctypes.data, n, 128, 10, 64, C.byref(opts), ids.ctypes.data,
+                               dists.ctypes.data, None, C.byref(rep)))
+        _lib.check(L.qv_last_hops(h, hops.ctypes.data, n))
+        ncu = C.c_int32()
+        mem = C.c_int64()
+        _lib.check(L.qv_device_info(0, None, 0, C.byref(ncu), C.byref(mem)))
+        assert rep.num_blocks == min(num_blocks * qpb, info.slots_per_cu * ncu.value)
+        assert rep.max_inflight == min(n, num_blocks * qpb)
+        opts.queries_per_block = 9
+        assert L.qv_search(h, q.ctypes.data, n, 128, 10, 64, C.byref(opts), ids.ctypes.data,
+                           dists.ctypes.data, None, C.byref(rep)) == _lib.QV_EINVAL
+    finally:
+        L.qv_index_close(h)
+    host = O.HostIndex.from_files(ix["dir"], "uint8")
+    oids, odists, _, ohops = O.search(host, q, 10, 64, early_exit=O.EXIT_GPRUNING)
+    np.testing.assert_array_equal(ids, oids)
+    np.testing.assert_array_equal(dists, odists)
+    np.testing.assert_array_equal(hops, ohops)
+
+
 def test_lut_matches_oracle(lib, small_u8_index):
     from quiver import _lib
 
