@@ -34,7 +34,7 @@ def lib():
 
 @pytest.mark.parametrize("pipe_width", [1, 2, 4])
 @pytest.mark.parametrize("policy", ["none", "gpruning"])
-@pytest.mark.parametrize("ef", [24, 64, 100, 200])
+@pytest.mark.parametrize("ef", [24, 64, 100, 200, 300, 448])
 def test_search_u8_bit_exact(lib, small_u8_index, pipe_width, policy, ef):
     import quiver
 
