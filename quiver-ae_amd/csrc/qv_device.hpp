@@ -289,20 +289,34 @@ __device__ __forceinline__ void load_vec_pre(const uint8_t* __restrict__ rec, in
   for (int k = 0; k < kVecPre; k++) x[k] = elem_raw<T>(rec, min((lane & 31) + 32 * k, dim - 1));
 }
 
-// exact_l2_ref with the first kVecPre elements of each lane taken from x.
-template <class T>
-__device__ __forceinline__ float exact_l2_pre(const uint32_t (&x)[kVecPre], const uint8_t* __restrict__ rec,
-                                              const float* __restrict__ qu_lds, int dim, int lane) {
-  float val = 0.f;
-  if (lane < 32) {
+// Query elements lane + 32k (k < kVecPre) of the first 32 lanes, kept in
+// registers for the whole query (0 past dim).
+__device__ __forceinline__ void load_query_pre(const float* __restrict__ qu_lds, int dim, int lane,
+                                               float (&qv)[kVecPre]) {
 #pragma unroll
-    for (int k = 0; k < kVecPre; k++) {
-      const int i = lane + 32 * k;
-      if (i < dim) {
-        const float diff = qu_lds[i] - raw_to_float<T>(x[k]);
-        val = __fmaf_rn(diff, diff, val);
-      }
-    }
+  for (int k = 0; k < kVecPre; k++) {
+    const int i = (lane & 31) + 32 * k;
+    const float v = qu_lds[min(i, dim - 1)];
+    qv[k] = i < dim ? v : 0.f;
+  }
+}
+
+// exact_l2_ref with the first kVecPre elements of each lane taken from x and
+// the matching query elements from qv.  Elements past dim contribute
+// fma(0, 0, val) = val, so the sum is the reference's bit for bit.
+template <class T>
+__device__ __forceinline__ float exact_l2_pre(const uint32_t (&x)[kVecPre], const float (&qv)[kVecPre],
+                                              const uint8_t* __restrict__ rec, const float* __restrict__ qu_lds,
+                                              int dim, int lane) {
+  float val = 0.f;
+  const bool lo = lane < 32;
+#pragma unroll
+  for (int k = 0; k < kVecPre; k++) {
+    const int i = lane + 32 * k;
+    const float diff = lo && i < dim ? qv[k] - raw_to_float<T>(x[k]) : 0.f;
+    val = __fmaf_rn(diff, diff, val);
+  }
+  if (lo) {
     for (int i = lane + 32 * kVecPre; i < dim; i += 32) {
       const float diff = qu_lds[i] - elem_to_float<T>(rec, i);
       val = __fmaf_rn(diff, diff, val);

@@ -129,6 +129,7 @@ struct Query {
   float* lut;
   float* qc;
   float* qu;
+  float quv[kVecPre];  // qu elements of this lane for the exact distance
   uint64_t* beam;
   uint32_t* bits;  // this workgroup's beam membership bitmap
   int sz;        // beam size (ctx.size)
@@ -179,7 +180,7 @@ struct Query {
   // Exact distance of v and the top-k insert (the reference's second warp).
   __device__ __forceinline__ void exact_and_topk(int32_t v, const uint32_t (&xv)[kVecPre], const uint8_t* rec,
                                                  int lane) {
-    const float e = exact_l2_pre<T>(xv, rec, qu, a.dim, lane);
+    const float e = exact_l2_pre<T>(xv, quv, rec, qu, a.dim, lane);
     last_e = e;
     const float dlast = read_lane_f32(td, a.topk - 1);
     if (fc < a.topk || e < dlast) topk_insert(td, ti, fc, a.topk, e, v);
@@ -450,6 +451,7 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
     __syncthreads();
     build_lut_lds(Qy.qc, a.pivots_t, a.chunk_off, a.num_chunks, Qy.lut);
     __syncthreads();
+    load_query_pre(Qy.qu, a.dim, lane, Qy.quv);
 
     GPrune g;
     int step = 0;
