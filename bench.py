@@ -281,6 +281,18 @@ def main() -> int:
     if not args.no_adc:
         result["adc"] = adc_leg(_lib, L, args.adc_codes, log)
 
+    # The search kernel is bound by random accesses, not by HBM bytes: one code
+    # row and one beam-membership bitmap word per neighbour evaluation plus the
+    # 64-byte lines of each expanded record, against the rate the gather-alone
+    # kernel reaches for random rows in the same run.
+    acc = 2 * last.total_evals + last.total_hops * ((info.node_size + 63) // 64)
+    rate = acc / (kernel_ms * 1e-3)
+    ceil_rate = result.get("adc", {}).get("gather_alone_rows_per_s")
+    roofline["random_access"] = {
+        "accesses_per_launch": int(acc), "achieved_per_s": round(rate, 1),
+        "ceiling_per_s": ceil_rate, "frac": round(rate / ceil_rate, 4) if ceil_rate else None,
+        "ceiling": "gather_kernel: random 32-byte rows of the 1B-code table, same run"}
+
     # ---- CPU baseline: the oracle (CPU restatement) on a bounded sample -------
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_leg(_lib, L, h, info, qf, ef, policy, pname, d_ids, nq, args.cpu_seconds)
