@@ -662,7 +662,7 @@ int64_t medoid_gpu(const T* d_base, int64_t n, int dim, hipStream_t st) {
   HIP_OK(hipMalloc(&d_mean, sizeof(float) * (size_t)dim));
   HIP_OK(hipMalloc(&d_best, sizeof(unsigned long long)));
   HIP_OK(hipMemcpy(d_mean, mean.data(), sizeof(float) * (size_t)dim, hipMemcpyHostToDevice));
-  HIP_OK(hipMemset(d_best, 0xff, sizeof(unsigned long long)));
+  HIP_OK(hipMemsetAsync(d_best, 0xff, sizeof(unsigned long long), st));
   hipLaunchKernelGGL(nearest_kernel<T>, dim3((unsigned)grid_of(n, 256)), dim3(256), 0, st, d_base, n, dim, d_mean,
                      d_best);
   HIP_OK(hipGetLastError());
@@ -714,7 +714,7 @@ qv_index* build_gpu_t(const T* d_base, int dtype, int64_t n, int dim, const qv_b
   uint8_t* d_codes = nullptr;
   HIP_OK(hipMalloc(&d_pages, (size_t)(lay.num_pages * kPageSize)));
   HIP_OK(hipMalloc(&d_codes, std::max<size_t>((size_t)n * pq.num_chunks, 64)));
-  HIP_OK(hipMemset(d_pages, 0, (size_t)(lay.num_pages * kPageSize)));
+  HIP_OK(hipMemsetAsync(d_pages, 0, (size_t)(lay.num_pages * kPageSize), st));
   HIP_OK(hipMemcpy(d_codes, pq.codes.data(), (size_t)n * pq.num_chunks, hipMemcpyHostToDevice));
   GLayout G{d_pages, n, lay.nodes_per_page, lay.node_size, lay.data_size, dim, prm.R};
   hipLaunchKernelGGL(init_pages_kernel<T>, dim3((unsigned)grid_of(n * (lay.data_size / 4 + 1), 256)), dim3(256), 0,

@@ -221,6 +221,47 @@ __device__ __forceinline__ float adc_sum(const CodeRow<MC>& cr, const float* __r
   return dist;
 }
 
+// The same ADC with every LUT entry recomputed from the pivots instead of
+// read from a per-query table: LUT[m][c] is the fused chain
+// acc = fma(q'_i - P[c][i], q'_i - P[c][i], acc) over the SC dims i of chunk m
+// from acc = 0 (the LUT build's own order), then dist += LUT[m][c] in chunk
+// order, so the result is the table ADC's bit for bit.  piv holds P row-major
+// with row stride prow floats (LDS, shared by the waves of a workgroup); qv
+// holds q' (LDS, read as broadcasts).
+template <int MC, int SC>
+__device__ __forceinline__ float adc_recompute(const CodeRow<MC>& cr, const float* __restrict__ qv,
+                                               const float* __restrict__ piv, int prow) {
+  float dist = 0.f;
+#pragma unroll
+  for (int m = 0; m < MC; m++) {
+    const int c = (int)((cr.w[m >> 2] >> ((m & 3) * 8)) & 0xffu);
+    const float* pr = piv + c * prow + m * SC;
+    float acc = 0.f;
+    if constexpr (SC == 4) {
+      const float4 pc = *reinterpret_cast<const float4*>(pr);
+      const float4 qq = *reinterpret_cast<const float4*>(qv + m * 4);
+      float d = qq.x - pc.x;
+      acc = __fmaf_rn(d, d, acc);
+      d = qq.y - pc.y;
+      acc = __fmaf_rn(d, d, acc);
+      d = qq.z - pc.z;
+      acc = __fmaf_rn(d, d, acc);
+      d = qq.w - pc.w;
+      acc = __fmaf_rn(d, d, acc);
+    } else {
+      static_assert(SC == 2, "chunks of 2 or 4 dimensions");
+      const float2 pc = *reinterpret_cast<const float2*>(pr);
+      const float2 qq = *reinterpret_cast<const float2*>(qv + m * 2);
+      float d = qq.x - pc.x;
+      acc = __fmaf_rn(d, d, acc);
+      d = qq.y - pc.y;
+      acc = __fmaf_rn(d, d, acc);
+    }
+    dist += acc;
+  }
+  return dist;
+}
+
 // Sequential fp32 ADC of one code row against an LDS LUT
 // (kernel_helpers.cuh:280-285): dist = 0; dist += LUT[j][code_j] for j = 0..M-1.
 template <int MC>

@@ -99,22 +99,30 @@ struct SearchArgs {
 
 enum : int32_t { kErrSpinTimeout = 1 };
 
-// Dynamic LDS carve-up shared by the kernel and its launcher.
+// Dynamic LDS carve-up of one query (one wave), shared by the kernel and its
+// launcher.  Q = beam positions per lane: the beam holds up to Q * 64 >= ef
+// entries.  With a per-query LUT (lut) the table comes first; the shared-
+// pivot kernel has none.
 struct LdsPlan {
   int lut_off, qc_off, qu_off, beam_off, total;
 };
 
-// Q = beam positions per lane: the beam holds up to Q * 64 >= ef entries.
-__host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q) {
+__host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool lut) {
   LdsPlan p;
   p.lut_off = 0;
-  p.qc_off = p.lut_off + num_chunks * kPivots * 4;
+  p.qc_off = p.lut_off + (lut ? num_chunks * kPivots * 4 : 0);
   int dpad = (dim + 3) & ~3;
   p.qu_off = p.qc_off + dpad * 4;
-  p.beam_off = (p.qu_off + dpad * 4 + 7) & ~7;
+  p.beam_off = (p.qu_off + dpad * 4 + 15) & ~15;
   p.total = p.beam_off + Q * kWave * 8;
   return p;
 }
+
+// Shared-pivot kernel: the 256 PQ pivots, row-major, rows padded to a
+// multiple of 4 floats plus 4 (16-byte aligned rows that start in different
+// LDS banks), ahead of the per-wave query areas.
+__host__ __device__ inline int piv_row(int dim) { return ((dim + 3) & ~3) + 4; }
+__host__ __device__ inline int piv_bytes(int dim) { return kPivots * piv_row(dim) * 4; }
 
 // Registers holding the start of a node record (see Query::fetch).
 struct NodeRec {
@@ -123,10 +131,13 @@ struct NodeRec {
   uint32_t xv[kVecPre];  // raw vector elements (load_vec_pre)
 };
 
-template <class T, int Q, int MC>
+// SC = 0: per-query LUT in LDS; SC > 0: LUT entries recomputed from the
+// shared pivots (chunks of SC dimensions).
+template <class T, int Q, int MC, int SC>
 struct Query {
   const SearchArgs& a;
   float* lut;
+  const float* piv;  // shared pivots (SC > 0)
   float* qc;
   float* qu;
   float quv[kVecPre];  // qu elements of this lane for the exact distance
@@ -146,16 +157,18 @@ struct Query {
   int evals;     // ADC evaluations so far
   float last_e;  // exact distance of the node expanded by the last hop
 
-  __device__ Query(const SearchArgs& args, char* smem)
-      : a(args), sz(0), u(INT32_MAX), bu(~0ull), td(__int_as_float(0x7f800000)), ti(-1), fc(0), evals(0) {
+  // smem: this query's LDS area; slot: this wave's bitmap index.
+  __device__ Query(const SearchArgs& args, char* smem, const float* pivots_lds, int64_t slot)
+      : a(args), piv(pivots_lds), sz(0), u(INT32_MAX), bu(~0ull), td(__int_as_float(0x7f800000)), ti(-1), fc(0),
+        evals(0) {
 #pragma unroll
     for (int k = 0; k < Q; k++) ck[k] = kPadKey;
-    LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q);
+    LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, SC == 0);
     lut = reinterpret_cast<float*>(smem + pl.lut_off);
     qc = reinterpret_cast<float*>(smem + pl.qc_off);
     qu = reinterpret_cast<float*>(smem + pl.qu_off);
     beam = reinterpret_cast<uint64_t*>(smem + pl.beam_off);
-    bits = a.bits + (int64_t)blockIdx.x * a.bits_words;
+    bits = a.bits + slot * a.bits_words;
   }
 
   __device__ __forceinline__ const uint8_t* record(int32_t v) const {
@@ -222,7 +235,10 @@ struct Query {
       adc_load<MC>(cr, a.codes, nbr);
       if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
       exact_and_topk(v, xv, rec, lane);
-      d = adc_sum<MC>(cr, lut);
+      if constexpr (SC > 0)
+        d = adc_recompute<MC, SC>(cr, qc, piv, piv_row(a.dim));
+      else
+        d = adc_sum<MC>(cr, lut);
     } else {
       if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
       d = adc_row<MC>(a.codes + (int64_t)nbr * a.num_chunks, lut, a.num_chunks);
@@ -398,9 +414,21 @@ struct GPrune {
   float last_top1 = __int_as_float(0x7f800000), last_topk = __int_as_float(0x7f800000);
 };
 
-template <class T, int Q, int MC>
-__global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
-  extern __shared__ __align__(16) char smem[];
+// Orders a query's LDS set-up before its reads: a workgroup barrier when the
+// workgroup is the query's one wave, a compiler fence otherwise (a wave's LDS
+// accesses complete in order).
+template <int SC>
+__device__ __forceinline__ void query_sync() {
+  if constexpr (SC == 0)
+    __syncthreads();
+  else
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
+// The persistent query loop of one wave: smem is its LDS area, piv the
+// shared pivots (SC > 0), slot its bitmap index.
+template <class T, int Q, int MC, int SC>
+__device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, const float* piv, int64_t slot) {
   const int lane = lane_id();
 
   while (true) {
@@ -434,7 +462,7 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
     if (qid < 0) break;
     if (a.t_start && lane == 0) a.t_start[qid] = wall_ticks();
 
-    Query<T, Q, MC> Qy(a, smem);
+    Query<T, Q, MC, SC> Qy(a, smem, piv, slot);
     const float* q = a.queries + (int64_t)qid * a.dim;
     // ---- entry node: the nav-graph search on the raw query when a nav graph is
     // loaded (kernel_q1.cuh:148-174, 199-206), else the medoid.
@@ -448,9 +476,11 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
       Qy.qc[i] = c;
       Qy.qu[i] = c + a.centroid[i];
     }
-    __syncthreads();
-    build_lut_lds(Qy.qc, a.pivots_t, a.chunk_off, a.num_chunks, Qy.lut);
-    __syncthreads();
+    query_sync<SC>();
+    if constexpr (SC == 0) {
+      build_lut_lds(Qy.qc, a.pivots_t, a.chunk_off, a.num_chunks, Qy.lut);
+      query_sync<SC>();
+    }
     load_query_pre(Qy.qu, a.dim, lane, Qy.quv);
 
     GPrune g;
@@ -566,8 +596,32 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
         __hip_atomic_store(&a.ring[pos], qid + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
       }
     }
-    __syncthreads();
+    query_sync<SC>();
   }
+}
+
+// One query per workgroup of one wave, its LUT in LDS.
+template <class T, int Q, int MC>
+__global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  run_queries<T, Q, MC, 0>(a, smem, nullptr, blockIdx.x);
+}
+
+// One workgroup per CU, one query per wave: the workgroup holds the pivots
+// once and every wave recomputes the LUT entries it needs (chunks of SC
+// dimensions), so the CU's LDS serves more queries than with a 32 KB LUT per
+// query.
+template <class T, int Q, int MC, int SC>
+__global__ __launch_bounds__(512) void search_kernel_sp(SearchArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  float* piv = reinterpret_cast<float*>(smem);
+  const int prow = piv_row(a.dim);
+  for (int idx = threadIdx.x; idx < a.dim * kPivots; idx += blockDim.x)
+    piv[(idx & (kPivots - 1)) * prow + (idx >> 8)] = a.pivots_t[idx];  // pivots_t is [dim][256]
+  __syncthreads();
+  const int waves = blockDim.x / kWave, w = threadIdx.x / kWave;
+  const LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, false);
+  run_queries<T, Q, MC, SC>(a, smem + piv_bytes(a.dim) + w * pl.total, piv, (int64_t)blockIdx.x * waves + w);
 }
 
 // Graph check run once at open: degree <= R, neighbour ids < n, no duplicate id
@@ -630,8 +684,37 @@ KernelFn pick_kernel(int dtype, int Q, int M) {
   return pick_q<float>(Q, M);
 }
 
+// Shared-pivot kernels: M = 32 chunks of 4 dimensions, M = 48 chunks of 2.
+template <class T, int MC, int SC>
+KernelFn pick_sp_q(int Q) {
+  if (Q == 1) return search_kernel_sp<T, 1, MC, SC>;
+  if (Q == 2) return search_kernel_sp<T, 2, MC, SC>;
+  if (Q == 4) return search_kernel_sp<T, 4, MC, SC>;
+  return search_kernel_sp<T, 7, MC, SC>;
+}
+
+template <class T>
+KernelFn pick_sp_t(int Q, int M) {
+  return M == 32 ? pick_sp_q<T, 32, 4>(Q) : pick_sp_q<T, 48, 2>(Q);
+}
+
+KernelFn pick_kernel_sp(int dtype, int Q, int M) {
+  if (dtype == QV_UINT8) return pick_sp_t<uint8_t>(Q, M);
+  if (dtype == QV_INT8) return pick_sp_t<int8_t>(Q, M);
+  return pick_sp_t<float>(Q, M);
+}
+
 // Beam positions per lane for ef (beam capacity 64 Q >= ef; kMaxEf = 448 = 64 * 7).
 int beam_chunks(int ef) { return ef <= 64 ? 1 : (ef <= 128 ? 2 : (ef <= 256 ? 4 : 7)); }
+
+// A search launch: kernel, workgroup size (waves = queries per workgroup),
+// dynamic LDS and the query slots (waves) one CU holds.
+struct LaunchPlan {
+  KernelFn kern = nullptr;
+  int waves = 1;
+  int lds = 0;
+  int slots_per_cu = 0;
+};
 
 }  // namespace
 
@@ -674,7 +757,11 @@ static void ensure_bits(qv_index* ix, int64_t slots) {
     ix->bits_dirty = true;
   }
   if (ix->bits_dirty) {
-    HIP_OK(hipMemset(ix->d_bits, 0, sizeof(uint32_t) * (size_t)(ix->bits_slots * ix->bits_words)));
+    // On the search stream, so the next kernel starts after it (a plain
+    // hipMemset runs on the null stream, which the non-blocking search stream
+    // does not wait for).
+    HIP_OK(hipMemsetAsync(ix->d_bits, 0, sizeof(uint32_t) * (size_t)(ix->bits_slots * ix->bits_words),
+                          ix->stream));
     ix->bits_dirty = false;
   }
 }
@@ -804,8 +891,8 @@ void validate_graph(qv_index* ix) {
   int64_t* d_bad = nullptr;
   HIP_OK(hipMalloc(&d_err, sizeof(int32_t)));
   HIP_OK(hipMalloc(&d_bad, sizeof(int64_t)));
-  HIP_OK(hipMemset(d_err, 0, sizeof(int32_t)));
-  HIP_OK(hipMemset(d_bad, 0x7f, sizeof(int64_t)));
+  HIP_OK(hipMemsetAsync(d_err, 0, sizeof(int32_t), ix->stream));
+  HIP_OK(hipMemsetAsync(d_bad, 0x7f, sizeof(int64_t), ix->stream));
   const Layout& L = ix->lay;
   const int blocks = (int)std::min<int64_t>((L.num_data + 3) / 4, 65536);
   hipLaunchKernelGGL(validate_kernel, dim3(blocks), dim3(256), 0, ix->stream, ix->d_pages,
@@ -943,18 +1030,46 @@ qv_index* make_index(int device, const Layout& lay, const PQTables& pq, uint8_t*
   return ix.release();
 }
 
-int slots_per_cu(qv_index* ix, int ef) {
-  const int P = beam_chunks(ef);
-  KernelFn k = pick_kernel(ix->lay.data_type, P, ix->M);
-  const LdsPlan pl = lds_plan(ix->M, (int)ix->lay.num_dims, P);
-  if (pl.total > 65536)
-    HIP_OK(hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, pl.total));
+// Resident workgroups of kernel k per CU at `waves` waves and `lds` bytes.
+static int occupancy(KernelFn k, int waves, int lds) {
+  HIP_OK(hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                             std::max(lds, 65536)));
   int nb = 0;
-  HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(k), 64,
-                                                      (size_t)pl.total));
+  HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(k), kWave * waves,
+                                                      (size_t)lds));
   return nb;
 }
+
+// The per-query-LUT kernel (one wave per workgroup, as many per CU as the LDS
+// holds), or the shared-pivot kernel when the index has chunks of 4 dims
+// (M = 32) or 2 dims (M = 48) and one workgroup of more waves fits a CU.
+LaunchPlan launch_plan(qv_index* ix, int ef) {
+  const int P = beam_chunks(ef);
+  const int M = ix->M, d = (int)ix->lay.num_dims;
+  LaunchPlan lut;
+  lut.kern = pick_kernel(ix->lay.data_type, P, M);
+  lut.waves = 1;
+  lut.lds = lds_plan(M, d, P, true).total;
+  lut.slots_per_cu = occupancy(lut.kern, 1, lut.lds);
+  const int sc = M == 32 ? 4 : (M == 48 ? 2 : 0);
+  bool uniform = sc > 0 && d == M * sc && (int)ix->h_chunk_off.size() == M + 1;
+  for (int m = 0; uniform && m <= M; m++) uniform = ix->h_chunk_off[(size_t)m] == m * sc;
+  if (!uniform) return lut;
+  int lds_cu = 0;
+  HIP_OK(hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, ix->device));
+  const int per_wave = lds_plan(M, d, P, false).total;
+  const int waves = std::min(8, (lds_cu - piv_bytes(d)) / per_wave);
+  if (waves <= lut.slots_per_cu) return lut;
+  LaunchPlan sp;
+  sp.kern = pick_kernel_sp(ix->lay.data_type, P, M);
+  sp.waves = waves;
+  sp.lds = piv_bytes(d) + waves * per_wave;
+  if (occupancy(sp.kern, waves, sp.lds) < 1) return lut;
+  sp.slots_per_cu = waves;
+  return sp;
+}
+
+int slots_per_cu(qv_index* ix, int ef) { return launch_plan(ix, ef).slots_per_cu; }
 
 // page = floor(v / npp) as (v * m) >> k with k = 32 + ceil(log2 npp) and
 // m = ceil(2^k / npp): the error term v (m npp - 2^k) / (npp 2^k) stays below
@@ -1007,13 +1122,12 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
   if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 448]");
   HIP_OK(hipSetDevice(ix->device));
   ensure_scratch(ix, nq, 1);
-  const int P = beam_chunks(ef);
-  KernelFn kern = pick_kernel(ix->lay.data_type, P, ix->M);
-  const LdsPlan pl = lds_plan(ix->M, (int)ix->lay.num_dims, P);
-  const int spc = slots_per_cu(ix, ef);
-  int nb = num_blocks > 0 ? num_blocks : spc * ix->num_cus;
-  nb = (int)std::min<int64_t>(nb, nq);
-  ensure_bits(ix, nb);
+  const LaunchPlan lp = launch_plan(ix, ef);
+  if (lp.slots_per_cu <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
+  int nb = num_blocks > 0 ? num_blocks : lp.slots_per_cu * ix->num_cus;
+  nb = (int)std::min<int64_t>(std::min<int64_t>(nb, nq), (int64_t)lp.slots_per_cu * ix->num_cus);
+  const int grid = (nb + lp.waves - 1) / lp.waves;
+  ensure_bits(ix, (int64_t)grid * lp.waves);
   SearchArgs a = base_args(ix);
   a.queries = d_queries;
   a.nq = (int32_t)nq;
@@ -1041,7 +1155,7 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
   a.rec_cap = rec.cap;
   HIP_OK(hipMemsetAsync(ix->d_counters, 0, 64, ix->stream));
   ix->bits_dirty = true;
-  hipLaunchKernelGGL(kern, dim3(nb), dim3(64), (size_t)pl.total, ix->stream, a);
+  hipLaunchKernelGGL(lp.kern, dim3(grid), dim3(kWave * lp.waves), (size_t)lp.lds, ix->stream, a);
   HIP_OK(hipGetLastError());
   HIP_OK(hipStreamSynchronize(ix->stream));
   int32_t counters[4] = {0, 0, 0, 0};
@@ -1078,10 +1192,8 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
 
   HIP_OK(hipSetDevice(ix->device));
   ensure_scratch(ix, nq, topk);
-  const int P = beam_chunks(ef);
-  KernelFn kern = pick_kernel(L.data_type, P, ix->M);
-  const LdsPlan pl = lds_plan(ix->M, (int)L.num_dims, P);
-  const int spc = slots_per_cu(ix, ef);
+  const LaunchPlan lp = launch_plan(ix, ef);
+  const int spc = lp.slots_per_cu;
   if (spc <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
   // Query slots (search.cu:393-399): num_blocks x queries_per_block.  Each slot
   // is a one-wave workgroup, so the reference's Q-interleave -- a block
@@ -1090,7 +1202,8 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   // only wait for a free CU, so the grid stops at the resident capacity; the
   // admission window keeps the requested slot count.
   const int64_t slots = (int64_t)(o.num_blocks > 0 ? o.num_blocks : spc * ix->num_cus) * o.queries_per_block;
-  const int num_blocks = (int)std::min<int64_t>(slots, (int64_t)spc * ix->num_cus);
+  const int grid = (int)((std::min<int64_t>(slots, (int64_t)spc * ix->num_cus) + lp.waves - 1) / lp.waves);
+  const int num_blocks = grid * lp.waves;  // query slots (waves) launched
   const int max_inflight = (int)std::min<int64_t>(nq, slots + std::max(0, o.prefeed));
   ensure_bits(ix, num_blocks);
 
@@ -1152,7 +1265,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   using clock = std::chrono::steady_clock;
   ix->bits_dirty = true;  // until every admitted query is seen to finish
   HIP_OK(hipEventRecord(ix->ev0, ix->stream));
-  hipLaunchKernelGGL(kern, dim3(num_blocks), dim3(64), (size_t)pl.total, ix->stream, a);
+  hipLaunchKernelGGL(lp.kern, dim3(grid), dim3(kWave * lp.waves), (size_t)lp.lds, ix->stream, a);
   HIP_OK(hipGetLastError());
   HIP_OK(hipEventRecord(ix->ev1, ix->stream));
 
