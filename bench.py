@@ -67,6 +67,8 @@ def main() -> int:
                     help="run one device-to-device copy of this size first (counter calibration)")
     ap.add_argument("--graph-placement", default="hbm", choices=("hbm", "host"),
                     help="page image in HBM (default) or in pinned host memory")
+    ap.add_argument("--search-kernel", default="auto", choices=("auto", "lut", "shared-pivots"),
+                    help="search kernel variant (auto: the one with more queries per CU)")
     ap.add_argument("--nav-sample", type=int, default=0,
                     help="build a nav graph over every K-th base vector and start queries from it (0: medoid)")
     args = ap.parse_args()
@@ -161,6 +163,7 @@ def main() -> int:
         o = _lib.default_search_opts()
         o.early_exit = policy
         o.pipe_width = pipe
+        o.kernel = _lib.KERNEL_NAMES[args.search_kernel]
         o.device_buffers = 1
         o.admission = _lib.QV_ADMIT_STREAMING
         rep = _lib.SearchReport()
@@ -229,6 +232,7 @@ def main() -> int:
     t1 = time.perf_counter()
     elapsed = t1 - t0
     recall = recall_of()
+    timed_ids = d_ids.download(np.int32, (nq, 10))  # the later legs reuse d_ids
     qps = args.steps * nq / elapsed
     p99 = float(np.median([r.lat_p99_ms for r in reps]))
     p50 = float(np.median([r.lat_p50_ms for r in reps]))
@@ -239,13 +243,14 @@ def main() -> int:
     # records of the expanded nodes + one PQ code row per neighbour
     # evaluation + queries in + top-k out; time from HIP events on its stream.
     kernel_ms = float(np.median([r.kernel_ms for r in reps]))
+    kname = "search_kernel_sp" if last.kernel == _lib.QV_KERNEL_SHARED_PIVOTS else "search_kernel"
     alg_bytes = (last.total_hops * info.node_size + last.total_evals * (info.num_chunks + 4)
                  + nq * (info.num_chunks * 256 * 4 + dim * 4 + 10 * 8))
     achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic(args.workload, ef, pname, log),
-                "kernel": "search_kernel", "kernel_ms": round(kernel_ms, 3),
+                "traffic": measured_traffic(args.workload, ef, pname, kname, log),
+                "kernel": kname, "kernel_ms": round(kernel_ms, 3),
                 "bytes_per_launch": int(alg_bytes), "hops_per_launch": int(last.total_hops),
                 "evals_per_launch": int(last.total_evals)}
 
@@ -271,7 +276,8 @@ def main() -> int:
         if at_095 is not None:
             lat_points.append(("0.95", at_095[0], at_095[1], at_095[3]))
         result["latency_mode"] = latency_leg(_lib, L, h, d_q, dim, nq, gt, d_ids, d_dists, lat_points,
-                                             [int(b) for b in args.latency_batches.split(",") if b], log)
+                                             [int(b) for b in args.latency_batches.split(",") if b],
+                                             _lib.KERNEL_NAMES[args.search_kernel], log)
     if at_095 is not None:
         result["config"]["at_recall_0.95"] = {"ef_search": at_095[0], "early_exit": at_095[3],
                                               "recall_at_10": round(at_095[4], 4), "qps": round(at_095[2], 1),
@@ -295,7 +301,8 @@ def main() -> int:
 
     # ---- CPU baseline: the oracle (CPU restatement) on a bounded sample -------
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_leg(_lib, L, h, info, qf, ef, policy, pname, d_ids, nq, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_leg(_lib, L, h, info, qf, ef, policy, pname, timed_ids, nq,
+                                         args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
     L.qv_index_close(h)
@@ -303,7 +310,7 @@ def main() -> int:
     return 0
 
 
-def latency_leg(_lib, L, h, d_q, dim, nq, gt, d_ids, d_dists, points, batches, log) -> list:
+def latency_leg(_lib, L, h, d_q, dim, nq, gt, d_ids, d_dists, points, batches, kernel, log) -> list:
     """Queries arrive in batches of B; each batch is one search call over
     device-resident queries and is admitted whole.  Per-query latency =
     completion - admission (qv_last_latencies); QPS = queries / wall time over
@@ -318,6 +325,7 @@ def latency_leg(_lib, L, h, d_q, dim, nq, gt, d_ids, d_dists, points, batches, l
             o = _lib.default_search_opts()
             o.early_exit = policy
             o.pipe_width = 1
+            o.kernel = kernel
             o.device_buffers = 1
             o.admission = _lib.QV_ADMIT_STREAMING
             buf = (C.c_double * b)()
@@ -343,11 +351,11 @@ def latency_leg(_lib, L, h, d_q, dim, nq, gt, d_ids, d_dists, points, batches, l
     return out
 
 
-def measured_traffic(workload: str, ef: int, policy: str, log):
-    """HBM bytes per search-kernel launch for this configuration, as measured by
-    the FETCH_SIZE and WRITE_SIZE counter runs summarised under profiles/
-    (scaled by a copy kernel of known size); None when not measured."""
-    key = f"traffic_bytes_per_launch[{workload} ef={ef} {policy}]"
+def measured_traffic(workload: str, ef: int, policy: str, kernel: str, log):
+    """HBM bytes per search-kernel launch for this configuration and kernel, as
+    measured by the FETCH_SIZE and WRITE_SIZE counter runs summarised under
+    profiles/ (scaled by a copy kernel of known size); None when not measured."""
+    key = f"traffic_bytes_per_launch[{workload} ef={ef} {policy} {kernel}]"
     for f in sorted((Path(__file__).resolve().parent / "profiles").glob("*.md")):
         for line in f.read_text().splitlines():
             if line.strip().startswith(key):
@@ -411,7 +419,7 @@ def adc_leg(_lib, L, ncodes: int, log) -> dict:
             "frac_of_gather_alone": round(gms / ms, 4)}
 
 
-def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, d_ids, nq, seconds: float) -> dict:
+def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, gpu_ids_all, nq, seconds: float) -> dict:
     sys.path.insert(0, str(ROOT / "oracle"))
     import qv_oracle as O
 
@@ -434,7 +442,7 @@ def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, d_ids, nq, seconds: float) 
     t = time.time()
     ids, _, _, _ = O.search(host, qf[:sample], 10, ef, early_exit=early, threads=threads)
     el = time.time() - t
-    gpu_ids = d_ids.download(np.int32, (nq, 10))[:sample]
+    gpu_ids = gpu_ids_all[:sample]
     same = bool(np.array_equal(ids, gpu_ids))
     return {"value": round(sample / el, 1), "unit": "queries/s", "cores": threads, "kind": "port",
             "sample": f"first {sample} of the {nq} queries, same index, ef={ef}, {pname}, "

@@ -44,6 +44,17 @@ extern "C" {
                                 run_persistent_search (src/quiver/search.cu:827-1051) */
 #define QV_ADMIT_BATCH 1     /* every query admitted when the clock starts */
 
+/* Search kernel variants (no counterpart in the reference, whose one kernel
+ * keeps a per-query LUT in shared memory).  Both give identical results. */
+#define QV_KERNEL_AUTO 0          /* per-query LUT while its resident slots hold every
+                                     query the call can have in flight (min(nq,
+                                     num_blocks x queries_per_block)), else shared
+                                     pivots where the index allows them */
+#define QV_KERNEL_LUT 1           /* per-query fp32 LUT in LDS, one wave per workgroup */
+#define QV_KERNEL_SHARED_PIVOTS 2 /* PQ pivots once per CU in LDS, each LUT entry
+                                     recomputed where it is read; needs chunks of
+                                     4 dims (M = 32) or 2 dims (M = 48) */
+
 typedef struct qv_index qv_index;
 
 /* shared::Layout (src/shared/common/layout.hpp:7-19) plus the PQ shape. */
@@ -59,7 +70,8 @@ typedef struct {
   int32_t data_type;      /* QV_UINT8 / QV_FLOAT / QV_INT8 */
   int32_t num_chunks;     /* PQ M */
   int32_t device;
-  int32_t slots_per_cu;   /* resident search workgroups per CU for this index */
+  int32_t slots_per_cu;   /* concurrent queries (waves) per CU of the kernel a full
+                             batch takes at ef <= 64 */
   int64_t device_bytes;   /* HBM held by the index */
   int64_t nav_nodes;      /* nodes of the loaded nav graph (0: none, entry = medoid) */
   int32_t nav_max_m;      /* its max degree */
@@ -132,8 +144,8 @@ void qv_index_close(qv_index* index);
 typedef struct {
   int32_t num_blocks;        /* --num-blocks; 0 fills the GPU */
   int32_t queries_per_block; /* --queries-per-block, 1..8: num_blocks x this many query
-                                slots (search.cu:393-399), each a one-wave workgroup;
-                                the launch stops at the device's resident capacity */
+                                slots (search.cu:393-399), one wave each; the launch
+                                stops at the device's resident capacity */
   int32_t pipe_width;        /* --pipe-width, 1..16 */
   int32_t early_exit;        /* QV_EXIT_NONE / QV_EXIT_GPRUNING */
   int32_t gpruning_warmup;   /* 10 in the reference CLI */
@@ -144,7 +156,7 @@ typedef struct {
   int32_t device_buffers;    /* 1: queries and outputs are device pointers */
   double timeout_s;          /* 0: no limit */
   int32_t skip_nav;          /* --skip-nav: medoid entry even with a nav graph loaded */
-  int32_t reserved0;
+  int32_t kernel;            /* QV_KERNEL_AUTO / QV_KERNEL_LUT / QV_KERNEL_SHARED_PIVOTS */
 } qv_search_opts;
 
 /* shared::RunReport (src/shared/common/run_report.hpp:32-56) for one search. */
@@ -157,7 +169,7 @@ typedef struct {
   int32_t num_blocks;        /* workgroups launched (= concurrent query slots) */
   int32_t max_inflight;      /* admission window: slots + prefeed */
   int32_t early_stopped;     /* queries ended by gpruning */
-  int32_t reserved;
+  int32_t kernel;            /* the search kernel that ran: QV_KERNEL_LUT or QV_KERNEL_SHARED_PIVOTS */
   double total_hops;         /* expanded nodes over all queries */
   double total_evals;        /* neighbour ADC evaluations over all queries */
 } qv_search_report;

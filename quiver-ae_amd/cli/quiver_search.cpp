@@ -30,7 +30,7 @@ const char* kUsage =
     "Usage: quiver_search --index-dir DIR --query FILE --data-type {uint8,int8,float}\n"
     "  [--topk 10] [--ef-search 30] [--repeat 20] [--ground-truth FILE]\n"
     "  [--memory-backend heap|mmap] [--memory-index-file FILE] [--ssd-list-file FILE]\n"
-    "  [--graph-placement hbm|host]\n"
+    "  [--graph-placement hbm|host] [--search-kernel auto|lut|shared-pivots]\n"
     "  [--num-blocks 756] [--num-blocks-list L] [--pipe-width 2] [--queries-per-block 1]\n"
     "  [--poll-threads 6] [--runners-per-ssd 1] [--early-exit-policy gpruning|none]\n"
     "  [--result-prefix P] [--final-recall-csv F] [--skip-nav] [--help]\n";
@@ -114,7 +114,7 @@ int main(int argc, char** argv) {
                                "--spdk-runner-io-contexts", "--pipe-width", "--queries-per-block",
                                "--runners-per-ssd", "--num-blocks-list", "--recall-threshold",
                                "--step-recall-csv", "--final-recall-csv", "--result-prefix",
-                               "--early-exit-policy", "--graph-placement"};
+                               "--early-exit-policy", "--graph-placement", "--search-kernel"};
   const char* bool_flags[] = {"--skip-nav", "--per-step-recall", "--help"};
   for (auto* s : value_flags) f[s] = Flag{};
   for (auto* s : bool_flags) f[s] = Flag{"", false, true};
@@ -129,6 +129,7 @@ int main(int argc, char** argv) {
   f["--runners-per-ssd"].value = "1";
   f["--early-exit-policy"].value = "gpruning";
   f["--graph-placement"].value = "hbm";
+  f["--search-kernel"].value = "auto";
   for (int i = 1; i < argc; i++) {
     std::string a = argv[i];
     auto it = f.find(a);
@@ -224,6 +225,14 @@ int main(int argc, char** argv) {
   std::cout << "[Quiver] runners_per_ssd=" << rps << (f["--runners-per-ssd"].used ? " (cli)" : "") << std::endl;
   std::cout << "[Quiver] early-exit policy=" << policy << std::endl;
 
+  const std::string kname = f["--search-kernel"].value;
+  const int32_t kernel = kname == "lut" ? QV_KERNEL_LUT
+                         : kname == "shared-pivots" ? QV_KERNEL_SHARED_PIVOTS
+                         : kname == "auto" ? QV_KERNEL_AUTO : -1;
+  if (kernel < 0) {
+    std::cerr << "--search-kernel must be auto, lut or shared-pivots" << std::endl;
+    return 1;
+  }
   qv_index* ix = nullptr;
   const char* mem_file = f["--memory-index-file"].used ? f["--memory-index-file"].value.c_str() : nullptr;
   const std::string placement = f["--graph-placement"].value;
@@ -263,6 +272,7 @@ int main(int argc, char** argv) {
     o.gpruning_warmup = 10;
     o.gpruning_patience = 8;
     o.skip_nav = f["--skip-nav"].used ? 1 : 0;
+    o.kernel = kernel;
     if (const char* e = std::getenv("QUIVER_PREFEED")) o.prefeed = std::atoi(e);
     if (const char* e = std::getenv("QUIVER_ADMIT_MIN_BATCH")) o.admit_min_batch = std::max(1, std::atoi(e));
     qv_search_report rep;
@@ -272,6 +282,8 @@ int main(int argc, char** argv) {
       return 1;
     }
     qv_last_hops(ix, hops.data(), nq);
+    std::cout << "[Quiver] search_kernel="
+              << (rep.kernel == QV_KERNEL_SHARED_PIVOTS ? "shared-pivots" : "lut") << std::endl;
     // format_run_report (src/shared/common/run_report.hpp:96-140)
     std::ostringstream os;
     os << std::fixed;

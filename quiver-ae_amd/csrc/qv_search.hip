@@ -714,6 +714,7 @@ struct LaunchPlan {
   int waves = 1;
   int lds = 0;
   int slots_per_cu = 0;
+  int variant = QV_KERNEL_LUT;
 };
 
 }  // namespace
@@ -1042,8 +1043,16 @@ static int occupancy(KernelFn k, int waves, int lds) {
 
 // The per-query-LUT kernel (one wave per workgroup, as many per CU as the LDS
 // holds), or the shared-pivot kernel when the index has chunks of 4 dims
-// (M = 32) or 2 dims (M = 48) and one workgroup of more waves fits a CU.
-LaunchPlan launch_plan(qv_index* ix, int ef) {
+// (M = 32) or 2 dims (M = 48), one workgroup of more waves fits a CU and more
+// than the LUT kernel's resident slots would be busy (`need`: queries the
+// call can have in flight).  A query alone runs faster with its own LUT (a
+// table read per code byte instead of a recompute); the shared pivots pay
+// when twice the queries per CU keep twice the random rows in flight.
+// `want` (QV_KERNEL_*) forces one; a forced shared-pivot plan the index or the
+// CU cannot take is QV_EUNSUPPORTED.
+LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
+  if (want != QV_KERNEL_AUTO && want != QV_KERNEL_LUT && want != QV_KERNEL_SHARED_PIVOTS)
+    fail(QV_EINVAL, "search kernel must be QV_KERNEL_AUTO, QV_KERNEL_LUT or QV_KERNEL_SHARED_PIVOTS");
   const int P = beam_chunks(ef);
   const int M = ix->M, d = (int)ix->lay.num_dims;
   LaunchPlan lut;
@@ -1051,25 +1060,35 @@ LaunchPlan launch_plan(qv_index* ix, int ef) {
   lut.waves = 1;
   lut.lds = lds_plan(M, d, P, true).total;
   lut.slots_per_cu = occupancy(lut.kern, 1, lut.lds);
+  if (want == QV_KERNEL_LUT) return lut;
+  const bool forced = want == QV_KERNEL_SHARED_PIVOTS;
+  if (!forced && lut.slots_per_cu > 0 && need <= (int64_t)lut.slots_per_cu * ix->num_cus) return lut;
   const int sc = M == 32 ? 4 : (M == 48 ? 2 : 0);
   bool uniform = sc > 0 && d == M * sc && (int)ix->h_chunk_off.size() == M + 1;
   for (int m = 0; uniform && m <= M; m++) uniform = ix->h_chunk_off[(size_t)m] == m * sc;
-  if (!uniform) return lut;
+  if (!uniform) {
+    if (forced) fail(QV_EUNSUPPORTED, "the shared-pivot kernel needs PQ chunks of 4 dims (M = 32) or 2 dims (M = 48)");
+    return lut;
+  }
   int lds_cu = 0;
   HIP_OK(hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, ix->device));
   const int per_wave = lds_plan(M, d, P, false).total;
   const int waves = std::min(8, (lds_cu - piv_bytes(d)) / per_wave);
-  if (waves <= lut.slots_per_cu) return lut;
+  if (!forced && waves <= lut.slots_per_cu) return lut;
   LaunchPlan sp;
   sp.kern = pick_kernel_sp(ix->lay.data_type, P, M);
   sp.waves = waves;
   sp.lds = piv_bytes(d) + waves * per_wave;
-  if (occupancy(sp.kern, waves, sp.lds) < 1) return lut;
+  sp.variant = QV_KERNEL_SHARED_PIVOTS;
+  if (waves < 1 || occupancy(sp.kern, waves, sp.lds) < 1) {
+    if (forced) fail(QV_EUNSUPPORTED, "the shared-pivot kernel does not fit on a compute unit");
+    return lut;
+  }
   sp.slots_per_cu = waves;
   return sp;
 }
 
-int slots_per_cu(qv_index* ix, int ef) { return launch_plan(ix, ef).slots_per_cu; }
+int slots_per_cu(qv_index* ix, int ef) { return launch_plan(ix, ef, QV_KERNEL_AUTO, INT64_MAX).slots_per_cu; }
 
 // page = floor(v / npp) as (v * m) >> k with k = 32 + ceil(log2 npp) and
 // m = ceil(2^k / npp): the error term v (m npp - 2^k) / (npp 2^k) stays below
@@ -1122,7 +1141,7 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
   if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 448]");
   HIP_OK(hipSetDevice(ix->device));
   ensure_scratch(ix, nq, 1);
-  const LaunchPlan lp = launch_plan(ix, ef);
+  const LaunchPlan lp = launch_plan(ix, ef, QV_KERNEL_AUTO, num_blocks > 0 ? std::min<int64_t>(nq, num_blocks) : nq);
   if (lp.slots_per_cu <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
   int nb = num_blocks > 0 ? num_blocks : lp.slots_per_cu * ix->num_cus;
   nb = (int)std::min<int64_t>(std::min<int64_t>(nb, nq), (int64_t)lp.slots_per_cu * ix->num_cus);
@@ -1192,7 +1211,8 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
 
   HIP_OK(hipSetDevice(ix->device));
   ensure_scratch(ix, nq, topk);
-  const LaunchPlan lp = launch_plan(ix, ef);
+  const int64_t requested = o.num_blocks > 0 ? (int64_t)o.num_blocks * o.queries_per_block : INT64_MAX;
+  const LaunchPlan lp = launch_plan(ix, ef, o.kernel, std::min<int64_t>(nq, requested));
   const int spc = lp.slots_per_cu;
   if (spc <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
   // Query slots (search.cu:393-399): num_blocks x queries_per_block.  Each slot
@@ -1362,6 +1382,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     rep->kernel_ms = kms;
     rep->num_blocks = num_blocks;
     rep->max_inflight = max_inflight;
+    rep->kernel = lp.variant;
     std::vector<int32_t> stopped((size_t)nq);
     HIP_OK(hipMemcpy(stopped.data(), ix->d_stopped, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost));
     rep->early_stopped = (int32_t)std::accumulate(stopped.begin(), stopped.end(), 0);
@@ -1405,7 +1426,7 @@ void qv_search_opts_default(qv_search_opts* o) {
   o->device_buffers = 0;
   o->timeout_s = 0.0;
   o->skip_nav = 0;
-  o->reserved0 = 0;
+  o->kernel = QV_KERNEL_AUTO;
 }
 
 int qv_index_open(const char* index_dir, const char* data_type, const char* memory_backend,

@@ -32,6 +32,10 @@ QV_ADMIT_STREAMING = 0
 QV_ADMIT_BATCH = 1
 QV_GRAPH_HBM = 0
 QV_GRAPH_HOST = 1
+QV_KERNEL_AUTO = 0
+QV_KERNEL_LUT = 1
+QV_KERNEL_SHARED_PIVOTS = 2
+KERNEL_NAMES = {"auto": QV_KERNEL_AUTO, "lut": QV_KERNEL_LUT, "shared-pivots": QV_KERNEL_SHARED_PIVOTS}
 
 PKG_ROOT = Path(__file__).resolve().parents[1]
 LIB_PATH = PKG_ROOT / "lib" / "libquiver_hip.so"
@@ -73,7 +77,7 @@ class SearchOpts(C.Structure):
         ("device_buffers", C.c_int32),
         ("timeout_s", C.c_double),
         ("skip_nav", C.c_int32),
-        ("reserved0", C.c_int32),
+        ("kernel", C.c_int32),
     ]
 
 
@@ -92,13 +96,13 @@ class SearchReport(C.Structure):
         ("num_blocks", C.c_int32),
         ("max_inflight", C.c_int32),
         ("early_stopped", C.c_int32),
-        ("reserved", C.c_int32),
+        ("kernel", C.c_int32),
         ("total_hops", C.c_double),
         ("total_evals", C.c_double),
     ]
 
     def as_dict(self) -> dict:
-        return {name: getattr(self, name) for name, _ in self._fields_ if name != "reserved"}
+        return {name: getattr(self, name) for name, _ in self._fields_}
 
 
 class BuildParams(C.Structure):

@@ -61,6 +61,7 @@ class IndexQuiver:
         env: Mapping[str, str] | None = None,
         device: int = 0,
         graph_placement: str = "hbm",
+        search_kernel: str = "auto",
     ) -> None:
         self.index_dir = Path(index_dir).expanduser().resolve()
         if not self.index_dir.is_dir():
@@ -92,6 +93,9 @@ class IndexQuiver:
         if graph_placement not in {"hbm", "host"}:
             raise ValueError("graph_placement must be hbm or host")
         self.graph_placement = graph_placement
+        if search_kernel not in _lib.KERNEL_NAMES:
+            raise ValueError("search_kernel must be auto, lut or shared-pivots")
+        self.search_kernel = search_kernel
         self.binary = self._find_binary(binary)
         self.num_blocks = self._positive(num_blocks, "num_blocks")
         self.queries_per_block = self._positive(queries_per_block, "queries_per_block")
@@ -198,6 +202,7 @@ class IndexQuiver:
             opts.admit_min_batch = max(1, int(env["QUIVER_ADMIT_MIN_BATCH"]))
         opts.timeout_s = float(timeout) if timeout is not None else 0.0
         opts.skip_nav = 1 if skip_nav else 0
+        opts.kernel = _lib.KERNEL_NAMES[self.search_kernel]
         rep = _lib.SearchReport()
         rc = _lib.load().qv_search(
             handle, q.ctypes.data, n, d, topk, ef_search, C.byref(opts),

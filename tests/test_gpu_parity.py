@@ -32,16 +32,22 @@ def lib():
     return _lib
 
 
+KERNELS = {"lut": 1, "shared-pivots": 2}
+
+
+@pytest.mark.parametrize("kernel", ["lut", "shared-pivots"])
 @pytest.mark.parametrize("pipe_width", [1, 2, 4])
 @pytest.mark.parametrize("policy", ["none", "gpruning"])
 @pytest.mark.parametrize("ef", [24, 64, 100, 200, 300, 448])
-def test_search_u8_bit_exact(lib, small_u8_index, pipe_width, policy, ef):
+def test_search_u8_bit_exact(lib, small_u8_index, pipe_width, policy, ef, kernel):
     import quiver
 
     ix = small_u8_index
-    _say(f"[gpu] search u8 pipe_width={pipe_width} policy={policy} ef={ef}")
-    index = quiver.IndexQuiver(ix["dir"], data_type="uint8", pipe_width=pipe_width, num_blocks=512)
+    _say(f"[gpu] search u8 kernel={kernel} pipe_width={pipe_width} policy={policy} ef={ef}")
+    index = quiver.IndexQuiver(ix["dir"], data_type="uint8", pipe_width=pipe_width, num_blocks=512,
+                               search_kernel=kernel)
     ids, dists = index.search(ix["queries"], topk=10, ef_search=ef, early_exit_policy=policy)
+    assert index.last_report["kernel"] == KERNELS[kernel]
     host = O.HostIndex.from_files(ix["dir"], "uint8")
     oids, odists, ofound, ohops = O.search(
         host, ix["queries"].astype(np.float32), 10, ef, pipe_width=pipe_width,
@@ -53,15 +59,18 @@ def test_search_u8_bit_exact(lib, small_u8_index, pipe_width, policy, ef):
     assert abs(O.recall(ids, ix["gt"], 10) - O.recall(oids, ix["gt"], 10)) <= 0.002
 
 
+@pytest.mark.parametrize("kernel", ["lut", "shared-pivots"])
 @pytest.mark.parametrize("pipe_width", [1, 2])
 @pytest.mark.parametrize("ef", [32, 90])
-def test_search_f32(lib, small_f32_index, pipe_width, ef):
+def test_search_f32(lib, small_f32_index, pipe_width, ef, kernel):
     import quiver
 
     ix = small_f32_index
-    _say(f"[gpu] search f32 pipe_width={pipe_width} ef={ef}")
-    index = quiver.IndexQuiver(ix["dir"], data_type="float32", pipe_width=pipe_width, num_blocks=256)
+    _say(f"[gpu] search f32 kernel={kernel} pipe_width={pipe_width} ef={ef}")
+    index = quiver.IndexQuiver(ix["dir"], data_type="float32", pipe_width=pipe_width, num_blocks=256,
+                               search_kernel=kernel)
     ids, dists = index.search(ix["queries"], topk=10, ef_search=ef, early_exit_policy="none")
+    assert index.last_report["kernel"] == KERNELS[kernel]
     host = O.HostIndex.from_files(ix["dir"], "float")
     oids, odists, _, _ = O.search(host, ix["queries"], 10, ef, pipe_width=pipe_width,
                                   early_exit=O.EXIT_NONE)
@@ -69,6 +78,63 @@ def test_search_f32(lib, small_f32_index, pipe_width, ef):
     np.testing.assert_array_equal(ids, oids)
     np.testing.assert_allclose(dists, odists, rtol=1e-5, atol=0)
     np.testing.assert_array_equal(dists, odists)
+
+
+@pytest.fixture(scope="module")
+def uneven_u8_index(tmp_path_factory):
+    """3k x 100 uint8, M = 32: PQ chunks of 3 and 4 dims."""
+    import quiver
+
+    d = tmp_path_factory.mktemp("uneven")
+    base = quiver.mixture(3000, 100, num_centers=16, seed=11)
+    queries = quiver.mixture(120, 100, num_centers=16, seed=11, first_row=10**6)
+    quiver.build_index(base, d / "u", R=24, L=40, num_chunks=32, threads=0)
+    return {"dir": d, "queries": queries}
+
+
+def test_uneven_chunks_take_the_lut_kernel(lib, uneven_u8_index):
+    """Chunks of unequal width: auto picks the per-query LUT kernel (bit-exact
+    against the oracle) and a forced shared-pivot search is refused."""
+    import quiver
+    from quiver._lib import QuiverError
+
+    ix = uneven_u8_index
+    _say("[gpu] uneven chunks auto + forced shared-pivots")
+    index = quiver.IndexQuiver(ix["dir"], data_type="uint8", pipe_width=1, num_blocks=128)
+    ids, dists = index.search(ix["queries"], topk=10, ef_search=64, early_exit_policy="none")
+    assert index.last_report["kernel"] == KERNELS["lut"]
+    index.close()
+    host = O.HostIndex.from_files(ix["dir"], "uint8")
+    oids, odists, _, _ = O.search(host, ix["queries"].astype(np.float32), 10, 64, early_exit=O.EXIT_NONE)
+    np.testing.assert_array_equal(ids, oids)
+    np.testing.assert_array_equal(dists, odists)
+    forced = quiver.IndexQuiver(ix["dir"], data_type="uint8", pipe_width=1, num_blocks=128,
+                                search_kernel="shared-pivots")
+    with pytest.raises(QuiverError, match="shared-pivot kernel needs"):
+        forced.search(ix["queries"], topk=10, ef_search=64, early_exit_policy="none")
+    forced.close()
+
+
+def test_auto_kernel_follows_queries_in_flight(lib, small_u8_index):
+    """Auto takes the per-query LUT kernel while its resident slots (4 per CU
+    at ef = 64: 1024 on 256 CUs) hold every query the call can have in flight,
+    and the shared-pivot kernel (8 per CU) beyond that; answers are the
+    oracle's either way."""
+    import quiver
+
+    ix = small_u8_index
+    q8 = np.ascontiguousarray(np.concatenate([ix["queries"]] * 8))  # 2400 queries
+    host = O.HostIndex.from_files(ix["dir"], "uint8")
+    oids, odists, _, _ = O.search(host, q8.astype(np.float32), 10, 64, early_exit=O.EXIT_NONE)
+    # num_blocks 4096: more slots than the device holds (the launch stops at capacity)
+    for nq, num_blocks, want in ((300, 4096, "lut"), (2400, 4096, "shared-pivots"), (2400, 512, "lut")):
+        _say(f"[gpu] auto kernel nq={nq} num_blocks={num_blocks}")
+        index = quiver.IndexQuiver(ix["dir"], data_type="uint8", pipe_width=1, num_blocks=num_blocks)
+        ids, dists = index.search(q8[:nq], topk=10, ef_search=64, early_exit_policy="none")
+        assert index.last_report["kernel"] == KERNELS[want], (nq, num_blocks)
+        index.close()
+        np.testing.assert_array_equal(ids, oids[:nq])
+        np.testing.assert_array_equal(dists, odists[:nq])
 
 
 def test_search_batch_admission_and_hops(lib, small_u8_index):
