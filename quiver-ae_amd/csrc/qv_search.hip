@@ -687,10 +687,15 @@ KernelFn pick_kernel(int dtype, int Q, int M) {
 // Shared-pivot kernels: M = 32 chunks of 4 dimensions, M = 48 chunks of 2.
 template <class T, int MC, int SC>
 KernelFn pick_sp_q(int Q) {
-  if (Q == 1) return search_kernel_sp<T, 1, MC, SC>;
-  if (Q == 2) return search_kernel_sp<T, 2, MC, SC>;
-  if (Q == 4) return search_kernel_sp<T, 4, MC, SC>;
-  return search_kernel_sp<T, 7, MC, SC>;
+  switch (Q) {
+    case 1: return search_kernel_sp<T, 1, MC, SC>;
+    case 2: return search_kernel_sp<T, 2, MC, SC>;
+    case 3: return search_kernel_sp<T, 3, MC, SC>;
+    case 4: return search_kernel_sp<T, 4, MC, SC>;
+    case 5: return search_kernel_sp<T, 5, MC, SC>;
+    case 6: return search_kernel_sp<T, 6, MC, SC>;
+    default: return search_kernel_sp<T, 7, MC, SC>;
+  }
 }
 
 template <class T>
@@ -705,7 +710,12 @@ KernelFn pick_kernel_sp(int dtype, int Q, int M) {
 }
 
 // Beam positions per lane for ef (beam capacity 64 Q >= ef; kMaxEf = 448 = 64 * 7).
+// The per-query-LUT kernel comes in Q = 1, 2, 4, 7 (its 32 KB LUT, not the
+// beam, sets how many queries a CU holds); the shared-pivot kernel in every Q
+// from 1 to 7, since there the beam's LDS decides between 6, 7 and 8 queries
+// per CU (at d = 128: 8 up to ef = 320, 7 up to 384, 6 up to 448).
 int beam_chunks(int ef) { return ef <= 64 ? 1 : (ef <= 128 ? 2 : (ef <= 256 ? 4 : 7)); }
+int beam_chunks_sp(int ef) { return (std::max(ef, 1) + kWave - 1) / kWave; }
 
 // A search launch: kernel, workgroup size (waves = queries per workgroup),
 // dynamic LDS and the query slots (waves) one CU holds.
@@ -1072,11 +1082,12 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
   }
   int lds_cu = 0;
   HIP_OK(hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, ix->device));
-  const int per_wave = lds_plan(M, d, P, false).total;
+  const int Psp = beam_chunks_sp(ef);
+  const int per_wave = lds_plan(M, d, Psp, false).total;
   const int waves = std::min(8, (lds_cu - piv_bytes(d)) / per_wave);
   if (!forced && waves <= lut.slots_per_cu) return lut;
   LaunchPlan sp;
-  sp.kern = pick_kernel_sp(ix->lay.data_type, P, M);
+  sp.kern = pick_kernel_sp(ix->lay.data_type, Psp, M);
   sp.waves = waves;
   sp.lds = piv_bytes(d) + waves * per_wave;
   sp.variant = QV_KERNEL_SHARED_PIVOTS;

@@ -38,7 +38,7 @@ KERNELS = {"lut": 1, "shared-pivots": 2}
 @pytest.mark.parametrize("kernel", ["lut", "shared-pivots"])
 @pytest.mark.parametrize("pipe_width", [1, 2, 4])
 @pytest.mark.parametrize("policy", ["none", "gpruning"])
-@pytest.mark.parametrize("ef", [24, 64, 100, 200, 300, 448])
+@pytest.mark.parametrize("ef", [24, 64, 100, 150, 200, 300, 350, 448])
 def test_search_u8_bit_exact(lib, small_u8_index, pipe_width, policy, ef, kernel):
     import quiver
 
