@@ -7,10 +7,12 @@
 //     query and the beam live in LDS; neighbour lists, vectors and PQ codes are
 //     read straight from HBM (no CPU poll threads, no 4 KB page copies), and the
 //     next node's record is requested while the current hop finishes;
-//   * the merge is built by rank: a per-workgroup bitmap answers "is this
-//     neighbour already in the beam", the few new candidates are ranked with
-//     ballots against a register copy of the beam and scattered into LDS,
-//     instead of merge-path rounds with block barriers;
+//   * the merge is built by rank: "is this neighbour already in the beam" is
+//     answered by a per-query bitmap in HBM (per-query-LUT kernel) or by the
+//     neighbour's own rank in the sorted LDS beam (shared-pivot kernel: a beam
+//     entry of the same id has the same key), and the few new candidates are
+//     scattered into LDS in place, instead of merge-path rounds with block
+//     barriers;
 //   * a device work queue (atomic ticket) gated by a host-written feed count,
 //     completion published to a host ring so per-query latency is exact.
 #include <fcntl.h>
@@ -87,14 +89,14 @@ struct SearchArgs {
   int64_t nav_nodes;
   int32_t nav_max_m;
   int32_t nav_start;
-  // per-workgroup membership bitmaps of the beam (bit v set <=> v in the beam),
-  // bits_words 32-bit words per workgroup, all zero between queries
-  uint32_t* bits;
-  int64_t bits_words;
   // optional record of expanded nodes (graph construction)
   int32_t* rec_ids;
   float* rec_dists;
   int32_t rec_cap;
+  // per-slot beam membership bitmaps of the per-query-LUT kernel (bit v set
+  // <=> v in the beam), bits_words 32-bit words per slot, zero between queries
+  uint32_t* bits;
+  int64_t bits_words;
 };
 
 enum : int32_t { kErrSpinTimeout = 1 };
@@ -102,7 +104,10 @@ enum : int32_t { kErrSpinTimeout = 1 };
 // Dynamic LDS carve-up of one query (one wave), shared by the kernel and its
 // launcher.  Q = beam positions per lane: the beam holds up to Q * 64 >= ef
 // entries.  With a per-query LUT (lut) the table comes first; the shared-
-// pivot kernel has none.
+// pivot kernel has none, and when every query element the exact distance
+// needs fits the lanes' registers (dim <= 32 kVecPre) its beam overlays the
+// query copy qu, which is only read once, into those registers, before the
+// first hop.
 struct LdsPlan {
   int lut_off, qc_off, qu_off, beam_off, total;
 };
@@ -111,10 +116,12 @@ __host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool
   LdsPlan p;
   p.lut_off = 0;
   p.qc_off = p.lut_off + (lut ? num_chunks * kPivots * 4 : 0);
-  int dpad = (dim + 3) & ~3;
+  const int dpad = (dim + 3) & ~3;
   p.qu_off = p.qc_off + dpad * 4;
-  p.beam_off = (p.qu_off + dpad * 4 + 15) & ~15;
-  p.total = p.beam_off + Q * kWave * 8;
+  const bool overlay = !lut && dim <= 32 * kVecPre;
+  p.beam_off = overlay ? p.qu_off : (p.qu_off + dpad * 4 + 15) & ~15;
+  const int beam_bytes = Q * kWave * 8;
+  p.total = p.beam_off + (overlay && dpad * 4 > beam_bytes ? dpad * 4 : beam_bytes);
   return p;
 }
 
@@ -142,7 +149,7 @@ struct Query {
   float* qu;
   float quv[kVecPre];  // qu elements of this lane for the exact distance
   uint64_t* beam;
-  uint32_t* bits;  // this workgroup's beam membership bitmap
+  uint32_t* bits;  // this slot's membership bitmap (SC == 0)
   int sz;        // beam size (ctx.size)
   // The beam in registers, chunk-major (lane l holds positions [l Q, l Q + Q),
   // kPadKey at and beyond sz), and its first unvisited entry u with key bu
@@ -157,6 +164,13 @@ struct Query {
   int evals;     // ADC evaluations so far
   float last_e;  // exact distance of the node expanded by the last hop
 
+  // Membership test: a bitmap in HBM (SC == 0), else the rank in the LDS
+  // beam.  The bitmap costs a random read per neighbour but nothing on the
+  // hop's critical path (the read overlaps the code rows); the rank costs a
+  // dependent LDS binary search after the ADC but no memory traffic, which
+  // pays when 8 queries per CU compete for the device's random accesses.
+  static constexpr bool kBits = SC == 0;
+
   // smem: this query's LDS area; slot: this wave's bitmap index.
   __device__ Query(const SearchArgs& args, char* smem, const float* pivots_lds, int64_t slot)
       : a(args), piv(pivots_lds), sz(0), u(INT32_MAX), bu(~0ull), td(__int_as_float(0x7f800000)), ti(-1), fc(0),
@@ -168,7 +182,7 @@ struct Query {
     qc = reinterpret_cast<float*>(smem + pl.qc_off);
     qu = reinterpret_cast<float*>(smem + pl.qu_off);
     beam = reinterpret_cast<uint64_t*>(smem + pl.beam_off);
-    bits = a.bits + slot * a.bits_words;
+    bits = kBits ? a.bits + slot * a.bits_words : nullptr;
   }
 
   __device__ __forceinline__ const uint8_t* record(int32_t v) const {
@@ -220,12 +234,16 @@ struct Query {
     // when a candidate wins.
     const bool spec = PF && u < sz;
 
-    // Beam membership of each neighbour.  The bitmap updates of the previous
-    // hop were issued before this hop's record arrived; waiting for every
-    // outstanding vector memory operation here (the record is complete by
-    // now) orders them before these reads, which bypass the vector L1.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    const uint32_t bword = __hip_atomic_load(bits + (nbr >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Beam membership of each neighbour from the bitmap.  The bitmap updates
+    // of the previous hop were issued before this hop's record arrived;
+    // waiting for every outstanding vector memory operation here (the record
+    // is complete by now) orders them before these reads, which bypass the
+    // vector L1.
+    uint32_t bword = 0;
+    if constexpr (kBits) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      bword = __hip_atomic_load(bits + (nbr >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     // ADC gather-sum over the neighbour's code row (LUT in LDS); the code rows
     // are in flight while the exact distance of v is computed.  Lanes without
     // a neighbour read code row 0 and discard the sum.
@@ -245,9 +263,8 @@ struct Query {
       exact_and_topk(v, xv, rec, lane);
     }
     const uint64_t nkey = has ? make_key(d, nbr, false) : sentinel_key(lane);
-
-    const bool in_beam = (bword >> (nbr & 31)) & 1u;
-    return merge_select<PF>(nkey, has && !in_beam, lane, nr, spec);
+    const bool fresh = kBits ? has && !((bword >> (nbr & 31)) & 1u) : has;
+    return merge_select<PF>(nkey, fresh, lane, nr, spec);
   }
 
   // Key at beam position pos (uniform) from the register copy.  Every chunk
@@ -292,7 +309,14 @@ struct Query {
   // most sz <= ef entries are compacted away.  So the new beam is the first ef
   // entries of  beam  U  {candidates whose id is not in the beam}, in key
   // order, and its first unvisited entry is taken and marked visited.
-  // fresh: lane holds a neighbour whose id is not in the beam (bitmap).
+  // fresh: lane holds a neighbour, not in the beam by the bitmap (kBits).
+  //
+  // Without the bitmap: a neighbour whose id is in the beam has that entry's
+  // key (the ADC of one code row against one query is one value), visited
+  // bit aside.  So the lower bound r of (c & ~1) in the sorted beam is both
+  // the candidate's rank and its membership test: c is in the beam iff
+  // beam[r] and c differ only in the visited bit.  Only neighbours below the
+  // end of a full beam need it.
   //
   // The selected node only depends on the smallest surviving candidate and
   // the old first unvisited entry, so it is found first and its record is
@@ -304,21 +328,42 @@ struct Query {
     const int ef = a.ef;
     // Candidates at or above the last entry of a full beam end beyond ef.
     const uint64_t last = sz >= ef ? beam_at(ef - 1) : ~0ull;
-    const bool valid = fresh && nkey < last;
+    const bool below = fresh && nkey < last;
+    int r = 0;  // rank in the beam (valid lanes)
+    bool valid = below;
+    if constexpr (!kBits) {
+      if (__ballot(below)) {
+        // r = #{beam entries e : e < (nkey & ~1)} by binary lifting over the
+        // LDS beam (sorted, sz entries); the steps are uniform across lanes.
+        const uint64_t c0 = nkey & ~1ull;
+        for (int step = sz > 0 ? 1 << (31 - __clz(sz)) : 0; step > 0; step >>= 1) {
+          const int p = r + step - 1;
+          const uint64_t e = beam[min(p, sz - 1)];
+          r += (p < sz && e < c0) ? step : 0;
+        }
+        const uint64_t at = beam[min(r, max(sz - 1, 0))];
+        valid = below && !(r < sz && (at >> 1) == (nkey >> 1));
+      }
+    }
     const uint64_t vm = __ballot(valid);
 
     if (vm == 0 && u >= sz) return -1;
-    // Smallest surviving candidate and its rank in the beam (entries below it
-    // with the visited bit ignored: e < c iff e < (c & ~1)).
+    // Smallest surviving candidate and its rank in the beam (with the bitmap:
+    // entries below it by ballots against the register beam, visited bit
+    // ignored: e < c iff e < (c & ~1)).
     int selpos = u;
     uint64_t selkey = bu;
     if (vm != 0) {
       const uint64_t kv0 = wave_min_u64(valid ? nkey : ~0ull);
-      int r0 = 0;
-#pragma unroll
-      for (int k = 0; k < Q; k++) r0 += __popcll(__ballot(ck[k] < (kv0 & ~1ull)));
       if (kv0 < bu) {
-        selpos = r0;
+        if constexpr (kBits) {
+          int r0 = 0;
+#pragma unroll
+          for (int k = 0; k < Q; k++) r0 += __popcll(__ballot(ck[k] < (kv0 & ~1ull)));
+          selpos = r0;
+        } else {
+          selpos = read_lane_i32(r, __ffsll((long long)__ballot(valid && nkey == kv0)) - 1);
+        }
         selkey = kv0;
       }
     }
@@ -333,27 +378,31 @@ struct Query {
     }
 
     // For each surviving candidate c (few per hop: most neighbours below the
-    // beam's end are already in it): its rank r in the beam, its rank t among
-    // the candidates, and the shift of every old entry at or above r.
-    int t = 0, r = 0;
+    // beam's end are already in it): its rank t among the candidates and the
+    // shift of every old entry at or above its rank in the beam.
+    int t = 0;
     uint32_t sh[Q];
 #pragma unroll
     for (int k = 0; k < Q; k++) sh[k] = 0u;
     for (uint64_t rest = vm; rest; rest &= rest - 1) {
       const int l = __ffsll((long long)rest) - 1;
       const uint64_t c = read_lane_u64(nkey, l);
-      const uint64_t c0 = c & ~1ull;
-      int rc = 0;
+      int rc;
+      if constexpr (kBits) {
+        rc = 0;
 #pragma unroll
-      for (int k = 0; k < Q; k++) rc += __popcll(__ballot(ck[k] < c0));
+        for (int k = 0; k < Q; k++) rc += __popcll(__ballot(ck[k] < (c & ~1ull)));
+        if (lane == l) r = rc;
+      } else {
+        rc = read_lane_i32(r, l);
+      }
       t += c < nkey ? 1 : 0;
-      if (lane == l) r = rc;
 #pragma unroll
       for (int k = 0; k < Q; k++) sh[k] += lane * Q + k >= rc ? 1u : 0u;
     }
 
-    // Scatter in place and keep the membership bitmap in step: entries pushed
-    // beyond ef leave it, inserted candidates join it.
+    // Scatter in place; entries pushed to ef or beyond drop out (and leave
+    // the bitmap), inserted candidates join it.
 #pragma unroll
     for (int k = 0; k < Q; k++) {
       const int pos = lane * Q + k;
@@ -361,7 +410,7 @@ struct Query {
       if (pos < sz) {
         if (g < ef) {
           beam[g] = g == selpos ? (ck[k] & ~1ull) : ck[k];
-        } else {
+        } else if constexpr (kBits) {
           const uint32_t id = key_id(ck[k]);
           atomicAnd(bits + (id >> 5), ~(1u << (id & 31)));
         }
@@ -370,8 +419,10 @@ struct Query {
     const int f = r + t;
     if (valid && f < ef) {
       beam[f] = f == selpos ? (nkey & ~1ull) : nkey;
-      const uint32_t id = key_id(nkey);
-      atomicOr(bits + (id >> 5), 1u << (id & 31));
+      if constexpr (kBits) {
+        const uint32_t id = key_id(nkey);
+        atomicOr(bits + (id >> 5), 1u << (id & 31));
+      }
     }
     sz = min(sz + (int)__popcll(vm), ef);
     // Register copy of the new beam (the wave's LDS accesses complete in order).
@@ -386,12 +437,14 @@ struct Query {
 
   // Clears the bitmap bits of the final beam (bitmaps are zero between queries).
   __device__ __forceinline__ void clear_bits(int lane) {
+    if constexpr (kBits) {
 #pragma unroll
-    for (int k = 0; k < Q; k++) {
-      const int pos = lane * Q + k;
-      if (pos < sz) {
-        const uint32_t id = key_id(ck[k]);
-        atomicAnd(bits + (id >> 5), ~(1u << (id & 31)));
+      for (int k = 0; k < Q; k++) {
+        const int pos = lane * Q + k;
+        if (pos < sz) {
+          const uint32_t id = key_id(ck[k]);
+          atomicAnd(bits + (id >> 5), ~(1u << (id & 31)));
+        }
       }
     }
   }
@@ -426,7 +479,7 @@ __device__ __forceinline__ void query_sync() {
 }
 
 // The persistent query loop of one wave: smem is its LDS area, piv the
-// shared pivots (SC > 0), slot its bitmap index.
+// shared pivots (SC > 0), slot its bitmap index (SC == 0).
 template <class T, int Q, int MC, int SC>
 __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, const float* piv, int64_t slot) {
   const int lane = lane_id();
@@ -482,6 +535,9 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       query_sync<SC>();
     }
     load_query_pre(Qy.qu, a.dim, lane, Qy.quv);
+    // qu may share its LDS with the beam (lds_plan): no beam store may move
+    // above these reads.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 
     GPrune g;
     int step = 0;
@@ -612,16 +668,16 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
 // dimensions), so the CU's LDS serves more queries than with a 32 KB LUT per
 // query.
 template <class T, int Q, int MC, int SC>
-__global__ __launch_bounds__(512) void search_kernel_sp(SearchArgs a) {
+__global__ __launch_bounds__(1024) void search_kernel_sp(SearchArgs a) {
   extern __shared__ __align__(16) char smem[];
   float* piv = reinterpret_cast<float*>(smem);
   const int prow = piv_row(a.dim);
   for (int idx = threadIdx.x; idx < a.dim * kPivots; idx += blockDim.x)
     piv[(idx & (kPivots - 1)) * prow + (idx >> 8)] = a.pivots_t[idx];  // pivots_t is [dim][256]
   __syncthreads();
-  const int waves = blockDim.x / kWave, w = threadIdx.x / kWave;
+  const int w = threadIdx.x / kWave;
   const LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, false);
-  run_queries<T, Q, MC, SC>(a, smem + piv_bytes(a.dim) + w * pl.total, piv, (int64_t)blockIdx.x * waves + w);
+  run_queries<T, Q, MC, SC>(a, smem + piv_bytes(a.dim) + w * pl.total, piv, 0);
 }
 
 // Graph check run once at open: degree <= R, neighbour ids < n, no duplicate id
@@ -753,9 +809,10 @@ static void free_scratch(qv_index* ix) {
   ix->cap_k = 0;
 }
 
-// Beam membership bitmaps, one per workgroup of the grid, zero between
-// queries (each query clears the bits of its final beam).  Reallocated when a
-// larger grid is launched and zeroed again after a search that did not finish.
+// Beam membership bitmaps of the per-query-LUT kernel, one per query slot,
+// zero between queries (each query clears the bits of its final beam).
+// Reallocated when more slots are launched and zeroed again after a search
+// that did not finish.
 static void ensure_bits(qv_index* ix, int64_t slots) {
   const int64_t words = ((ix->lay.num_data + 31) / 32 + 15) / 16 * 16;
   if (slots > ix->bits_slots || words != ix->bits_words) {
@@ -1084,7 +1141,7 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
   HIP_OK(hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, ix->device));
   const int Psp = beam_chunks_sp(ef);
   const int per_wave = lds_plan(M, d, Psp, false).total;
-  const int waves = std::min(8, (lds_cu - piv_bytes(d)) / per_wave);
+  const int waves = std::min(16, (lds_cu - piv_bytes(d)) / per_wave);
   if (!forced && waves <= lut.slots_per_cu) return lut;
   LaunchPlan sp;
   sp.kern = pick_kernel_sp(ix->lay.data_type, Psp, M);
@@ -1157,7 +1214,8 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
   int nb = num_blocks > 0 ? num_blocks : lp.slots_per_cu * ix->num_cus;
   nb = (int)std::min<int64_t>(std::min<int64_t>(nb, nq), (int64_t)lp.slots_per_cu * ix->num_cus);
   const int grid = (nb + lp.waves - 1) / lp.waves;
-  ensure_bits(ix, (int64_t)grid * lp.waves);
+  const bool use_bits = lp.variant == QV_KERNEL_LUT;
+  if (use_bits) ensure_bits(ix, (int64_t)grid * lp.waves);
   SearchArgs a = base_args(ix);
   a.queries = d_queries;
   a.nq = (int32_t)nq;
@@ -1184,13 +1242,13 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
   a.rec_dists = rec.dists;
   a.rec_cap = rec.cap;
   HIP_OK(hipMemsetAsync(ix->d_counters, 0, 64, ix->stream));
-  ix->bits_dirty = true;
+  if (use_bits) ix->bits_dirty = true;
   hipLaunchKernelGGL(lp.kern, dim3(grid), dim3(kWave * lp.waves), (size_t)lp.lds, ix->stream, a);
   HIP_OK(hipGetLastError());
   HIP_OK(hipStreamSynchronize(ix->stream));
   int32_t counters[4] = {0, 0, 0, 0};
   HIP_OK(hipMemcpy(counters, ix->d_counters, sizeof(counters), hipMemcpyDeviceToHost));
-  ix->bits_dirty = counters[1] < nq;  // conservative: zeroed again before the next launch
+  if (use_bits) ix->bits_dirty = counters[1] < nq;  // conservative: zeroed again before the next launch
   if (counters[1] != nq)
     fail(QV_EHIP, "record search finished " + std::to_string(counters[1]) + " of " + std::to_string(nq) + " queries");
 }
@@ -1236,7 +1294,8 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   const int grid = (int)((std::min<int64_t>(slots, (int64_t)spc * ix->num_cus) + lp.waves - 1) / lp.waves);
   const int num_blocks = grid * lp.waves;  // query slots (waves) launched
   const int max_inflight = (int)std::min<int64_t>(nq, slots + std::max(0, o.prefeed));
-  ensure_bits(ix, num_blocks);
+  const bool use_bits = lp.variant == QV_KERNEL_LUT;
+  if (use_bits) ensure_bits(ix, num_blocks);
 
   const float* d_q = queries;
   if (!o.device_buffers) {
@@ -1294,7 +1353,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   a.rec_cap = 0;
 
   using clock = std::chrono::steady_clock;
-  ix->bits_dirty = true;  // until every admitted query is seen to finish
+  if (use_bits) ix->bits_dirty = true;  // until every admitted query is seen to finish
   HIP_OK(hipEventRecord(ix->ev0, ix->stream));
   hipLaunchKernelGGL(lp.kern, dim3(grid), dim3(kWave * lp.waves), (size_t)lp.lds, ix->stream, a);
   HIP_OK(hipGetLastError());
@@ -1363,7 +1422,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   int32_t counters[4] = {0, 0, 0, 0};
   HIP_OK(hipMemcpy(counters, ix->d_counters, sizeof(counters), hipMemcpyDeviceToHost));
   // every query that took a ticket below nq ran to its end and cleared its bits
-  ix->bits_dirty = counters[1] < std::min<int64_t>(counters[0], nq);
+  if (use_bits) ix->bits_dirty = counters[1] < std::min<int64_t>(counters[0], nq);
   if (counters[2] & kErrSpinTimeout) fail(QV_ETIMEDOUT, "search kernel watchdog: feed wait exceeded its limit");
   if (timed_out || counters[1] < nq) {
     char buf[96];

@@ -253,9 +253,9 @@ def test_queries_per_block_slots(lib, small_u8_index, num_blocks, qpb):
         ncu = C.c_int32()
         mem = C.c_int64()
         _lib.check(L.qv_device_info(0, None, 0, C.byref(ncu), C.byref(mem)))
-        # whole workgroups: at most one workgroup's waves (8) above the request
+        # whole workgroups: less than one workgroup's waves (at most 16) above the request
         want = min(num_blocks * qpb, info.slots_per_cu * ncu.value)
-        assert want <= rep.num_blocks < want + 8 and rep.num_blocks <= info.slots_per_cu * ncu.value
+        assert want <= rep.num_blocks < want + 16 and rep.num_blocks <= info.slots_per_cu * ncu.value
         assert rep.max_inflight == min(n, num_blocks * qpb)
         opts.queries_per_block = 9
         assert L.qv_search(h, q.ctypes.data, n, 128, 10, 64, C.byref(opts), ids.ctypes.data,
