@@ -225,17 +225,18 @@ __device__ __forceinline__ float adc_sum(const CodeRow<MC>& cr, const float* __r
 // read from a per-query table: LUT[m][c] is the fused chain
 // acc = fma(q'_i - P[c][i], q'_i - P[c][i], acc) over the SC dims i of chunk m
 // from acc = 0 (the LUT build's own order), then dist += LUT[m][c] in chunk
-// order, so the result is the table ADC's bit for bit.  piv holds P row-major
-// with row stride prow floats (LDS, shared by the waves of a workgroup); qv
-// holds q' (LDS, read as broadcasts).
+// order, so the result is the table ADC's bit for bit.  piv holds P
+// chunk-major, entry (m, c) at float (m * 256 + c) * SC (LDS, shared by the
+// waves of a workgroup); qv holds q' (LDS, read as broadcasts).
 template <int MC, int SC>
 __device__ __forceinline__ float adc_recompute(const CodeRow<MC>& cr, const float* __restrict__ qv,
-                                               const float* __restrict__ piv, int prow) {
+                                               const float* __restrict__ piv) {
   float dist = 0.f;
+  const char* pb = reinterpret_cast<const char*>(piv);
 #pragma unroll
   for (int m = 0; m < MC; m++) {
-    const int c = (int)((cr.w[m >> 2] >> ((m & 3) * 8)) & 0xffu);
-    const float* pr = piv + c * prow + m * SC;
+    const uint32_t c = (cr.w[m >> 2] >> ((m & 3) * 8)) & 0xffu;
+    const float* pr = reinterpret_cast<const float*>(pb + (m * kPivots * SC * 4 + c * (SC * 4)));
     float acc = 0.f;
     if constexpr (SC == 4) {
       const float4 pc = *reinterpret_cast<const float4*>(pr);

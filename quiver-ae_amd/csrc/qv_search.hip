@@ -125,11 +125,12 @@ __host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool
   return p;
 }
 
-// Shared-pivot kernel: the 256 PQ pivots, row-major, rows padded to a
-// multiple of 4 floats plus 4 (16-byte aligned rows that start in different
-// LDS banks), ahead of the per-wave query areas.
-__host__ __device__ inline int piv_row(int dim) { return ((dim + 3) & ~3) + 4; }
-__host__ __device__ inline int piv_bytes(int dim) { return kPivots * piv_row(dim) * 4; }
+// Shared-pivot kernel: the PQ pivots chunk-major, [chunk m][code c][SC dims]
+// (entry (m, c) at float (m * 256 + c) * SC), ahead of the per-wave query
+// areas.  The SC floats one LUT entry needs are one aligned vector read, and
+// lanes reading different codes of one chunk hit consecutive 4 SC-byte slots,
+// so rows need no padding against bank conflicts.
+__host__ __device__ inline int piv_bytes(int dim) { return kPivots * dim * 4; }
 
 // Registers holding the start of a node record (see Query::fetch).
 struct NodeRec {
@@ -254,7 +255,7 @@ struct Query {
       if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
       exact_and_topk(v, xv, rec, lane);
       if constexpr (SC > 0)
-        d = adc_recompute<MC, SC>(cr, qc, piv, piv_row(a.dim));
+        d = adc_recompute<MC, SC>(cr, qc, piv);
       else
         d = adc_sum<MC>(cr, lut);
     } else {
@@ -671,9 +672,11 @@ template <class T, int Q, int MC, int SC>
 __global__ __launch_bounds__(1024) void search_kernel_sp(SearchArgs a) {
   extern __shared__ __align__(16) char smem[];
   float* piv = reinterpret_cast<float*>(smem);
-  const int prow = piv_row(a.dim);
-  for (int idx = threadIdx.x; idx < a.dim * kPivots; idx += blockDim.x)
-    piv[(idx & (kPivots - 1)) * prow + (idx >> 8)] = a.pivots_t[idx];  // pivots_t is [dim][256]
+  // pivots_t is [dim][256]; dim i = m SC + j of code c goes to (m 256 + c) SC + j
+  for (int idx = threadIdx.x; idx < a.dim * kPivots; idx += blockDim.x) {
+    const int i = idx >> 8, c = idx & (kPivots - 1);
+    piv[((i / SC) * kPivots + c) * SC + i % SC] = a.pivots_t[idx];
+  }
   __syncthreads();
   const int w = threadIdx.x / kWave;
   const LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, false);
