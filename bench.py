@@ -441,14 +441,18 @@ def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, gpu_ids_all, nq, seconds: f
     O.search(host, qf[:threads * 4], 10, ef, early_exit=early, threads=threads)
     per_q = (time.time() - t) / (threads * 4)
     sample = int(max(threads * 8, min(nq, seconds / max(per_q, 1e-9))))
+    secs = np.zeros(sample, np.float64)
     t = time.time()
-    ids, _, _, _ = O.search(host, qf[:sample], 10, ef, early_exit=early, threads=threads)
+    ids, _, _, _ = O.search(host, qf[:sample], 10, ef, early_exit=early, threads=threads, seconds=secs)
     el = time.time() - t
     gpu_ids = gpu_ids_all[:sample]
     same = bool(np.array_equal(ids, gpu_ids))
     return {"value": round(sample / el, 1), "unit": "queries/s", "cores": threads, "kind": "port",
             "sample": f"first {sample} of the {nq} queries, same index, ef={ef}, {pname}, "
                       f"{el:.1f}s wall on {threads} threads (OpenMP over queries)",
+            "p50_ms": round(float(np.percentile(secs, 50)) * 1e3, 3),
+            "p99_ms": round(float(np.percentile(secs, 99)) * 1e3, 3),
+            "label": "CPU restatement of the reference beam search (DiskANN unavailable offline)",
             "ids_identical_to_gpu": same}
 
 

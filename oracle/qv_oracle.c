@@ -9,10 +9,12 @@
  * --fmad=true; the bits of the reference binary itself cannot be observed here,
  * so this contraction is the one unpinnable assumption of the restatement.
  */
+#define _POSIX_C_SOURCE 199309L /* clock_gettime under -std=c11 */
 #include "qv_oracle.h"
 
 #include <math.h>
 #include <stdlib.h>
+#include <time.h>
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
@@ -547,18 +549,32 @@ done:
   return rc;
 }
 
+static double wall_seconds(void) {
+  struct timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
 int qvo_search(const qvo_index* ix, const float* queries, int64_t nq,
                const qvo_search_params* p, int threads, int32_t* ids,
                float* dists, int32_t* found, int32_t* hops) {
+  return qvo_search_timed(ix, queries, nq, p, threads, ids, dists, found, hops, NULL);
+}
+
+int qvo_search_timed(const qvo_index* ix, const float* queries, int64_t nq,
+                     const qvo_search_params* p, int threads, int32_t* ids,
+                     float* dists, int32_t* found, int32_t* hops, double* seconds) {
   int status = QVO_OK;
 #ifdef _OPENMP
   if (threads <= 0) threads = omp_get_num_procs();
 #pragma omp parallel for schedule(dynamic, 4) num_threads(threads)
 #endif
   for (int64_t i = 0; i < nq; i++) {
+    const double t0 = seconds ? wall_seconds() : 0.0;
     int rc = qvo_search_one(ix, queries + i * (int64_t)ix->dim, p,
                             ids + i * p->topk, dists + i * p->topk,
                             found ? found + i : NULL, hops ? hops + i : NULL);
+    if (seconds) seconds[i] = wall_seconds() - t0;
     if (rc != QVO_OK) {
 #ifdef _OPENMP
 #pragma omp critical

@@ -123,6 +123,11 @@ int qvo_search_one(const qvo_index* ix, const float* q, const qvo_search_params*
 int qvo_search(const qvo_index* ix, const float* queries, int64_t nq,
                const qvo_search_params* p, int threads, int32_t* ids,
                float* dists, int32_t* found, int32_t* hops);
+/* qvo_search that also writes each query's wall time in seconds (for the CPU
+ * baseline's per-query latency; seconds may be NULL). */
+int qvo_search_timed(const qvo_index* ix, const float* queries, int64_t nq,
+                     const qvo_search_params* p, int threads, int32_t* ids,
+                     float* dists, int32_t* found, int32_t* hops, double* seconds);
 
 /* Recall@k as the reference computes it: hits of results[i][0..k) in the set
  * gt[i][0..k), divided by n*k. */

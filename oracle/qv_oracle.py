@@ -91,6 +91,9 @@ def load() -> C.CDLL:
     lib.qvo_search.argtypes = [C.POINTER(OracleIndex), P, C.c_int64, C.POINTER(SearchParams), C.c_int,
                                P, P, P, P]
     lib.qvo_search.restype = C.c_int
+    lib.qvo_search_timed.argtypes = [C.POINTER(OracleIndex), P, C.c_int64, C.POINTER(SearchParams), C.c_int,
+                                     P, P, P, P, P]
+    lib.qvo_search_timed.restype = C.c_int
     lib.qvo_recall.argtypes = [P, P, C.c_int64, C.c_int, C.c_int]
     lib.qvo_recall.restype = C.c_double
     lib.qvo_adc_topk.argtypes = [P, C.c_int, P, P, C.c_int64, C.c_int, P, P, C.POINTER(C.c_double)]
@@ -261,9 +264,10 @@ def nav_entry(nav: HostNav, q: np.ndarray, fallback: int = -1) -> int:
 
 def search(ix: HostIndex, queries: np.ndarray, topk: int, ef: int, *, pipe_width: int = 1,
            early_exit: int = EXIT_GPRUNING, warmup: int = 10, patience: int = 8, threads: int = 0,
-           nav: HostNav | None = None):
+           nav: HostNav | None = None, seconds: np.ndarray | None = None):
     """Oracle search: returns (ids int32 [n,k], dists float32 [n,k], found, hops).
-    With `nav`, each query starts from its nav-graph entry instead of the medoid."""
+    With `nav`, each query starts from its nav-graph entry instead of the medoid.
+    With `seconds` (float64 [n]), each query's wall time is written there."""
     lib = load()
     q = np.ascontiguousarray(queries, dtype=np.float32)
     n = q.shape[0]
@@ -275,8 +279,14 @@ def search(ix: HostIndex, queries: np.ndarray, topk: int, ef: int, *, pipe_width
     p = SearchParams(topk, ef, pipe_width, early_exit, warmup, patience,
                      C.cast(C.pointer(ns), C.c_void_p) if ns is not None else None)
     cs = ix.c_struct()
-    rc = lib.qvo_search(C.byref(cs), _ptr(q), n, C.byref(p), threads, _ptr(ids), _ptr(dists),
-                        _ptr(found), _ptr(hops))
+    if seconds is not None:
+        if seconds.dtype != np.float64 or seconds.shape != (n,) or not seconds.flags.c_contiguous:
+            raise ValueError("seconds must be a contiguous float64 array of one entry per query")
+        rc = lib.qvo_search_timed(C.byref(cs), _ptr(q), n, C.byref(p), threads, _ptr(ids), _ptr(dists),
+                                  _ptr(found), _ptr(hops), _ptr(seconds))
+    else:
+        rc = lib.qvo_search(C.byref(cs), _ptr(q), n, C.byref(p), threads, _ptr(ids), _ptr(dists),
+                            _ptr(found), _ptr(hops))
     if rc != 0:
         raise RuntimeError(f"oracle search failed with status {rc}")
     return ids, dists, found, hops

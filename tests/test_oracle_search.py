@@ -104,3 +104,20 @@ def test_pipe_width_lanes_expand_more_per_round(small_u8_index):
     _, _, _, h4 = O.search(ix, q, 10, 64, pipe_width=4, early_exit=O.EXIT_NONE)
     # speculative lanes expand at least as many nodes in total
     assert h4.sum() >= h1.sum()
+
+
+def test_timed_search_matches_untimed(small_u8_index):
+    """The CPU baseline's timed search returns the same answers and one positive
+    wall time per query."""
+    ix = small_u8_index
+    host = O.HostIndex.from_files(ix["dir"], "uint8")
+    q = ix["queries"][:64].astype(np.float32)
+    ids0, d0, f0, h0 = O.search(host, q, 10, 64, early_exit=O.EXIT_NONE)
+    secs = np.zeros(q.shape[0], np.float64)
+    ids1, d1, f1, h1 = O.search(host, q, 10, 64, early_exit=O.EXIT_NONE, seconds=secs)
+    np.testing.assert_array_equal(ids0, ids1)
+    np.testing.assert_array_equal(d0, d1)
+    np.testing.assert_array_equal(h0, h1)
+    assert (secs > 0).all() and (secs < 10).all()
+    with pytest.raises(ValueError):
+        O.search(host, q, 10, 64, seconds=np.zeros(3))
