@@ -803,11 +803,13 @@ static void free_scratch(qv_index* ix) {
   hipFree(ix->d_tstart);
   hipFree(ix->d_tend);
   hipHostFree(ix->h_ring);
+  hipHostFree(ix->h_stage);
   ix->d_queries = nullptr;
   ix->d_ids = ix->d_found = ix->d_hops = ix->d_stopped = ix->d_evals = nullptr;
   ix->d_dists = nullptr;
   ix->d_tstart = ix->d_tend = nullptr;
   ix->h_ring = nullptr;
+  ix->h_stage = nullptr;
   ix->cap_q = 0;
   ix->cap_k = 0;
 }
@@ -858,6 +860,7 @@ static void ensure_scratch(qv_index* ix, int64_t nq, int k) {
   HIP_OK(hipMalloc(&ix->d_tend, sizeof(uint64_t) * (size_t)cq));
   HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_ring), sizeof(int32_t) * (size_t)cq,
                        hipHostMallocCoherent));
+  HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_stage), sizeof(int32_t) * (size_t)(4 + 3 * cq)));
   ix->cap_q = cq;
   ix->cap_k = ck;
 }
@@ -1256,11 +1259,11 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
     fail(QV_EHIP, "record search finished " + std::to_string(counters[1]) + " of " + std::to_string(nq) + " queries");
 }
 
-static double percentile_sorted(const std::vector<double>& v, double frac) {
-  if (v.empty()) return 0.0;
-  size_t i = (size_t)((double)v.size() * frac);
-  if (i >= v.size()) i = v.size() - 1;
-  return v[i];
+// Rank of the frac-quantile in a sorted array of n values (floor(n frac),
+// clamped to the last).
+static size_t percentile_rank(size_t n, double frac) {
+  const size_t i = (size_t)((double)n * frac);
+  return i >= n ? n - 1 : i;
 }
 
 void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, int ef,
@@ -1422,8 +1425,22 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   }
   const auto t1 = clock::now();
 
-  int32_t counters[4] = {0, 0, 0, 0};
-  HIP_OK(hipMemcpy(counters, ix->d_counters, sizeof(counters), hipMemcpyDeviceToHost));
+  // Counters, hop counts, stop flags and evaluation counts in one round trip
+  // through the pinned staging buffer.
+  int32_t* const st_counters = ix->h_stage;
+  int32_t* const st_hops = ix->h_stage + 4;
+  int32_t* const st_stopped = st_hops + ix->cap_q;
+  int32_t* const st_evals = st_stopped + ix->cap_q;
+  const size_t qbytes = sizeof(int32_t) * (size_t)nq;
+  HIP_OK(hipMemcpyAsync(st_counters, ix->d_counters, 4 * sizeof(int32_t), hipMemcpyDeviceToHost, ix->stream));
+  HIP_OK(hipMemcpyAsync(st_hops, ix->d_hops, qbytes, hipMemcpyDeviceToHost, ix->stream));
+  if (rep) {
+    HIP_OK(hipMemcpyAsync(st_stopped, ix->d_stopped, qbytes, hipMemcpyDeviceToHost, ix->stream));
+    HIP_OK(hipMemcpyAsync(st_evals, ix->d_evals, qbytes, hipMemcpyDeviceToHost, ix->stream));
+  }
+  HIP_OK(hipStreamSynchronize(ix->stream));
+  int32_t counters[4];
+  std::memcpy(counters, st_counters, sizeof(counters));
   // every query that took a ticket below nq ran to its end and cleared its bits
   if (use_bits) ix->bits_dirty = counters[1] < std::min<int64_t>(counters[0], nq);
   if (counters[2] & kErrSpinTimeout) fail(QV_ETIMEDOUT, "search kernel watchdog: feed wait exceeded its limit");
@@ -1432,8 +1449,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     std::snprintf(buf, sizeof(buf), "quiver_search exceeded the %g second timeout", o.timeout_s);
     fail(QV_ETIMEDOUT, buf);
   }
-  ix->last_hops.resize((size_t)nq);
-  HIP_OK(hipMemcpy(ix->last_hops.data(), ix->d_hops, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost));
+  ix->last_hops.assign(st_hops, st_hops + nq);
   if (!streaming) {
     // every query admitted at launch: latency = its completion tick - the first start tick
     std::vector<uint64_t> ts((size_t)nq), te((size_t)nq);
@@ -1456,25 +1472,31 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     rep->num_blocks = num_blocks;
     rep->max_inflight = max_inflight;
     rep->kernel = lp.variant;
-    std::vector<int32_t> stopped((size_t)nq);
-    HIP_OK(hipMemcpy(stopped.data(), ix->d_stopped, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost));
-    rep->early_stopped = (int32_t)std::accumulate(stopped.begin(), stopped.end(), 0);
+    rep->early_stopped = (int32_t)std::accumulate(st_stopped, st_stopped + nq, 0);
     double hop_sum = 0;
     for (int32_t h : ix->last_hops) hop_sum += h;
     rep->avg_hops = hop_sum / (double)nq;
     rep->total_hops = hop_sum;
-    std::vector<int32_t> ev((size_t)nq);
-    HIP_OK(hipMemcpy(ev.data(), ix->d_evals, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost));
     double ev_sum = 0;
-    for (int32_t e : ev) ev_sum += e;
+    for (int64_t i = 0; i < nq; i++) ev_sum += st_evals[i];
     rep->total_evals = ev_sum;
-    std::sort(lat_ms.begin(), lat_ms.end());
     rep->lat_avg_ms = std::accumulate(lat_ms.begin(), lat_ms.end(), 0.0) / (double)nq;
-    rep->lat_p50_ms = percentile_sorted(lat_ms, 0.50);
-    rep->lat_p90_ms = percentile_sorted(lat_ms, 0.90);
-    rep->lat_p99_ms = percentile_sorted(lat_ms, 0.99);
-    rep->lat_p999_ms = percentile_sorted(lat_ms, 0.999);
-    rep->lat_max_ms = lat_ms.back();
+    // Order statistics by successive selection (linear time; a full sort of
+    // 10k latencies costs about half a millisecond of host time per search).
+    double* const v = lat_ms.data();
+    const size_t n = lat_ms.size();
+    const double fr[4] = {0.50, 0.90, 0.99, 0.999};
+    double* const out[4] = {&rep->lat_p50_ms, &rep->lat_p90_ms, &rep->lat_p99_ms, &rep->lat_p999_ms};
+    size_t lo = 0;
+    for (int j = 0; j < 4; j++) {
+      const size_t r = percentile_rank(n, fr[j]);
+      if (r >= lo) {
+        std::nth_element(v + lo, v + r, v + n);
+        lo = r + 1;
+      }
+      *out[j] = v[r];
+    }
+    rep->lat_max_ms = *std::max_element(v, v + n);
   }
 }
 
