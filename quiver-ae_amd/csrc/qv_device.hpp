@@ -232,14 +232,12 @@ template <int MC, int SC>
 __device__ __forceinline__ float adc_recompute(const CodeRow<MC>& cr, const float* __restrict__ qv,
                                                const float* __restrict__ piv) {
   float dist = 0.f;
-  const char* pb = reinterpret_cast<const char*>(piv);
 #pragma unroll
   for (int m = 0; m < MC; m++) {
     const uint32_t c = (cr.w[m >> 2] >> ((m & 3) * 8)) & 0xffu;
-    const float* pr = reinterpret_cast<const float*>(pb + (m * kPivots * SC * 4 + c * (SC * 4)));
     float acc = 0.f;
     if constexpr (SC == 4) {
-      const float4 pc = *reinterpret_cast<const float4*>(pr);
+      const float4 pc = reinterpret_cast<const float4*>(piv)[m * kPivots + c];
       const float4 qq = *reinterpret_cast<const float4*>(qv + m * 4);
       float d = qq.x - pc.x;
       acc = __fmaf_rn(d, d, acc);
@@ -251,7 +249,7 @@ __device__ __forceinline__ float adc_recompute(const CodeRow<MC>& cr, const floa
       acc = __fmaf_rn(d, d, acc);
     } else {
       static_assert(SC == 2, "chunks of 2 or 4 dimensions");
-      const float2 pc = *reinterpret_cast<const float2*>(pr);
+      const float2 pc = reinterpret_cast<const float2*>(piv)[m * kPivots + c];
       const float2 qq = *reinterpret_cast<const float2*>(qv + m * 2);
       float d = qq.x - pc.x;
       acc = __fmaf_rn(d, d, acc);

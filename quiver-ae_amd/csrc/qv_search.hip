@@ -252,7 +252,11 @@ struct Query {
     if constexpr (MC > 0 && MC % 16 == 0) {
       CodeRow<MC> cr;
       adc_load<MC>(cr, a.codes, nbr);
-      if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
+      // Issued on every hop (v's own record when there is no unvisited entry
+      // to guess), so every path reaches the ADC with the same loads in
+      // flight and the compiler's wait for the code rows can leave the
+      // record outstanding.
+      if constexpr (PF) fetch(spec ? (int32_t)key_id(bu) : v, lane, nr);
       exact_and_topk(v, xv, rec, lane);
       if constexpr (SC > 0)
         d = adc_recompute<MC, SC>(cr, qc, piv);
@@ -268,18 +272,14 @@ struct Query {
     return merge_select<PF>(nkey, fresh, lane, nr, spec);
   }
 
-  // Key at beam position pos (uniform) from the register copy.  Every chunk
-  // is read out and selected by value, so the copy is never indexed
-  // dynamically (which would move it to scratch memory).
-  __device__ __forceinline__ uint64_t beam_at(int pos) const {
-    const int kk = pos % Q, l = pos / Q;
-    uint64_t x = read_lane_u64(ck[0], l);
+  // Without the bitmap, every LDS beam position at or beyond sz holds kPadKey
+  // (above every key): set once per query; merges only write below the new
+  // sz, which never shrinks.  The rank search then needs no bounds test.
+  __device__ __forceinline__ void pad_beam(int lane) {
+    if constexpr (!kBits) {
 #pragma unroll
-    for (int k = 1; k < Q; k++) {
-      const uint64_t v = read_lane_u64(ck[k], l);
-      x = kk == k ? v : x;
+      for (int k = 0; k < Q; k++) beam[k * kWave + lane] = kPadKey;
     }
-    return x;
   }
 
   // First unvisited entry of the beam from the register copy.
@@ -291,7 +291,9 @@ struct Query {
       if (m) first = min(first, (__ffsll((long long)m) - 1) * Q + k);
     }
     u = first;
-    bu = first < sz ? beam_at(first) : ~0ull;
+    // (the LDS beam is current: written before the register copy was reloaded,
+    // or by mark_visited; one broadcast read instead of 2 Q lane reads)
+    bu = first < sz ? beam[first] : ~0ull;
   }
 
   // Marks the entry at position pos visited (LDS and registers).
@@ -328,22 +330,27 @@ struct Query {
   __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool fresh, int lane, NodeRec& nr, bool spec) {
     const int ef = a.ef;
     // Candidates at or above the last entry of a full beam end beyond ef.
-    const uint64_t last = sz >= ef ? beam_at(ef - 1) : ~0ull;
+    const uint64_t last = sz >= ef ? beam[ef - 1] : ~0ull;
     const bool below = fresh && nkey < last;
     int r = 0;  // rank in the beam (valid lanes)
     bool valid = below;
     if constexpr (!kBits) {
       if (__ballot(below)) {
         // r = #{beam entries e : e < (nkey & ~1)} by binary lifting over the
-        // LDS beam (sorted, sz entries); the steps are uniform across lanes.
+        // LDS beam: sorted, kPadKey from sz to the capacity kCap = 64 Q, so
+        // a read clamped to kCap - 1 sees either a key of the beam or kPadKey
+        // (a below candidate is under the last key of a full beam, so even a
+        // full-capacity beam never lifts r past it).  Steps are uniform.
+        constexpr int kCap = Q * kWave;
+        constexpr int kTop = kCap >= 256 ? 256 : (kCap >= 128 ? 128 : 64);
         const uint64_t c0 = nkey & ~1ull;
-        for (int step = sz > 0 ? 1 << (31 - __clz(sz)) : 0; step > 0; step >>= 1) {
-          const int p = r + step - 1;
-          const uint64_t e = beam[min(p, sz - 1)];
-          r += (p < sz && e < c0) ? step : 0;
+#pragma unroll
+        for (int step = kTop; step > 0; step >>= 1) {
+          const uint64_t e = beam[min(r + step - 1, kCap - 1)];
+          r += e < c0 ? step : 0;
         }
-        const uint64_t at = beam[min(r, max(sz - 1, 0))];
-        valid = below && !(r < sz && (at >> 1) == (nkey >> 1));
+        const uint64_t at = beam[min(r, kCap - 1)];
+        valid = below && (at >> 1) != (nkey >> 1);
       }
     }
     const uint64_t vm = __ballot(valid);
@@ -539,6 +546,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     // qu may share its LDS with the beam (lds_plan): no beam store may move
     // above these reads.
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    Qy.pad_beam(lane);
 
     GPrune g;
     int step = 0;
