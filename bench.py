@@ -296,6 +296,8 @@ def main() -> int:
     acc = per_eval * last.total_evals + last.total_hops * ((info.node_size + 63) // 64)
     rate = acc / (kernel_ms * 1e-3)
     ceil_rate = result.get("adc", {}).get("gather_alone_rows_per_s")
+    if "adc" in result:
+        roofline["measured_read_peak_gbs"] = result["adc"]["stream_read_gbs"]
     roofline["random_access"] = {
         "accesses_per_launch": int(acc), "achieved_per_s": round(rate, 1),
         "ceiling_per_s": ceil_rate, "frac": round(rate / ceil_rate, 4) if ceil_rate else None,
@@ -412,13 +414,26 @@ def adc_leg(_lib, L, ncodes: int, log) -> dict:
     gms = float(np.median(gt[1:]))
     fold.close()
     log(f"gather alone: {gms:.3f} ms, {evals / gms / 1e6:.1f} G rows/s; ADC at {gms / ms:.1%} of that rate")
+    # the whole code table read sequentially: the measured streaming-read peak
+    fold = _lib.DeviceBuffer(_lib.QV_STREAM_READ_BLOCKS * 4)
+    st = []
+    for _ in range(4):
+        sms = C.c_float()
+        _lib.check(L.qv_stream_read_bench(codes.ptr, ncodes * M, fold.ptr, 0, C.byref(sms)))
+        st.append(sms.value)
+    sms = float(np.median(st[1:]))
+    fold.close()
+    stream_gbs = ncodes * M / (sms * 1e-3) / 1e9
+    log(f"streaming read of the {ncodes * M / 1e9:.0f} GB table: {sms:.3f} ms, {stream_gbs:.0f} GB/s")
     codes.close()
     ids.close()
     return {"kernel": "adc_bench_kernel", "codes": ncodes, "M": M, "queries": nq, "ids_per_query": per_q,
             "kernel_ms": round(ms, 4), "bytes_per_launch": int(alg), "achieved_gbs": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4), "evals_per_s": round(evals / (ms * 1e-3), 1),
             "gather_alone_ms": round(gms, 4), "gather_alone_rows_per_s": round(evals / (gms * 1e-3), 1),
-            "frac_of_gather_alone": round(gms / ms, 4)}
+            "frac_of_gather_alone": round(gms / ms, 4),
+            "stream_read_gbs": round(stream_gbs, 1),
+            "frac_of_stream_read": round(gbs / stream_gbs, 4)}
 
 
 def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, gpu_ids_all, nq, seconds: float) -> dict:

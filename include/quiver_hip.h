@@ -254,6 +254,15 @@ int qv_adc_bench(const float* d_luts, int32_t num_chunks, const uint8_t* d_codes
 int qv_gather_bench(const uint8_t* d_rows, int64_t num_rows, const int32_t* d_ids,
                     int64_t n, uint32_t* d_fold, int device, float* elapsed_ms);
 
+/* Sequential read of nbytes (a multiple of 16, 16-byte aligned) from d_src,
+ * XOR-folded into d_fold[min(QV_STREAM_READ_BLOCKS, ceil(nbytes / 4096))] (no
+ * reference counterpart; a measurement aid): the device's streaming read
+ * bandwidth, reported beside the nominal HBM peak.  elapsed_ms (may be NULL)
+ * receives the kernel time. */
+#define QV_STREAM_READ_BLOCKS 4096
+int qv_stream_read_bench(const uint8_t* d_src, int64_t nbytes, uint32_t* d_fold, int device,
+                         float* elapsed_ms);
+
 /* Counter-based fills for synthetic tables: 8-byte word w of the buffer is a
  * function of (seed, w) only; id i is uniform in [0, num_codes) and a function
  * of (seed, i) only. */

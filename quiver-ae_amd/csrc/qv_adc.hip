@@ -262,6 +262,33 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint8_t* __restrict__
   if (threadIdx.x == 0) fold[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
 }
 
+// Streaming read of nwords 16-byte words (grid-stride, four loads in flight
+// per thread), XOR-folded into one word per workgroup: the device's sequential
+// read bandwidth, the measured counterpart of the nominal HBM peak.
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ src, int64_t nwords,
+                                                          uint32_t* __restrict__ fold) {
+  __shared__ uint32_t part[4];
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t w = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  uint32_t x = 0;
+  for (; w + 3 * stride < nwords; w += 4 * stride) {
+    const u32x4 a = __builtin_nontemporal_load(src + w);
+    const u32x4 b = __builtin_nontemporal_load(src + w + stride);
+    const u32x4 c = __builtin_nontemporal_load(src + w + 2 * stride);
+    const u32x4 d = __builtin_nontemporal_load(src + w + 3 * stride);
+    x ^= (a[0] ^ a[1] ^ a[2] ^ a[3]) ^ (b[0] ^ b[1] ^ b[2] ^ b[3]) ^ (c[0] ^ c[1] ^ c[2] ^ c[3]) ^
+         (d[0] ^ d[1] ^ d[2] ^ d[3]);
+  }
+  for (; w < nwords; w += stride) {
+    const u32x4 a = __builtin_nontemporal_load(src + w);
+    x ^= a[0] ^ a[1] ^ a[2] ^ a[3];
+  }
+  for (int off = 32; off > 0; off >>= 1) x ^= (uint32_t)__shfl_xor((int)x, off);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) fold[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
+}
+
 // Device-to-device copy of 16-byte words (grid-stride); also the reference
 // kernel of known traffic against which HBM byte counters are scaled.
 __global__ __launch_bounds__(256) void copy_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src,
@@ -398,6 +425,30 @@ int qv_gather_bench(const uint8_t* d_rows, int64_t num_rows, const int32_t* d_id
     HIP_OK(hipEventCreate(&e1));
     HIP_OK(hipEventRecord(e0, 0));
     hipLaunchKernelGGL(gather_kernel, dim3((unsigned)blocks), dim3(256), 0, 0, d_rows, num_rows - 1, d_ids, n, d_fold);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipEventRecord(e1, 0));
+    HIP_OK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (elapsed_ms) *elapsed_ms = ms;
+  });
+}
+
+int qv_stream_read_bench(const uint8_t* d_src, int64_t nbytes, uint32_t* d_fold, int device, float* elapsed_ms) {
+  return qv::guard([&] {
+    if (!d_src || !d_fold || nbytes < 16 || (nbytes & 15) != 0) qv::fail(QV_EINVAL, "bad argument");
+    if ((reinterpret_cast<uintptr_t>(d_src) & 15) != 0) qv::fail(QV_EINVAL, "source must be 16-byte aligned");
+    HIP_OK(hipSetDevice(device));
+    const int64_t nwords = nbytes / 16;
+    const int64_t blocks = std::min<int64_t>(QV_STREAM_READ_BLOCKS, (nwords + 255) / 256);
+    hipEvent_t e0, e1;
+    HIP_OK(hipEventCreate(&e0));
+    HIP_OK(hipEventCreate(&e1));
+    HIP_OK(hipEventRecord(e0, 0));
+    hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(256), 0, 0,
+                       reinterpret_cast<const u32x4*>(d_src), nwords, d_fold);
     HIP_OK(hipGetLastError());
     HIP_OK(hipEventRecord(e1, 0));
     HIP_OK(hipEventSynchronize(e1));

@@ -32,6 +32,7 @@ QV_ADMIT_STREAMING = 0
 QV_ADMIT_BATCH = 1
 QV_GRAPH_HBM = 0
 QV_GRAPH_HOST = 1
+QV_STREAM_READ_BLOCKS = 4096
 QV_KERNEL_AUTO = 0
 QV_KERNEL_LUT = 1
 QV_KERNEL_SHARED_PIVOTS = 2
@@ -157,6 +158,7 @@ SIGNATURES = {
     "qv_adc_bench": (_I32, [_P, _I32, _P, _I64, _P, _I64, _I64, _I32, _P, _P, _P, C.c_int,
                             C.POINTER(C.c_float)]),
     "qv_gather_bench": (_I32, [_P, _I64, _P, _I64, _P, C.c_int, C.POINTER(C.c_float)]),
+    "qv_stream_read_bench": (_I32, [_P, _I64, _P, C.c_int, C.POINTER(C.c_float)]),
     "qv_fill_uniform_bytes": (_I32, [_P, _I64, C.c_uint64, C.c_int]),
     "qv_fill_uniform_ids": (_I32, [_P, _I64, _I64, C.c_uint64, C.c_int]),
     "qv_build_params_default": (None, [C.POINTER(BuildParams)]),

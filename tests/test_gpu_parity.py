@@ -345,6 +345,30 @@ def test_gather_bench_fold(lib):
     np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("nwords", [300 * 256 + 17, 4096 * 256 * 5 + 1234])
+def test_stream_read_bench_fold(lib, nwords):
+    """Workgroup b of the streaming read folds every 16-byte word w with
+    (w mod 256 B) // 256 == b, B = min(4096, ceil(nwords / 256)) workgroups."""
+    from quiver import _lib
+
+    _say(f"[gpu] stream read fold nwords={nwords}")
+    rng = np.random.default_rng(nwords)
+    words = rng.integers(0, 2**32, (nwords, 4), dtype=np.uint32)
+    blocks = min(_lib.QV_STREAM_READ_BLOCKS, (nwords + 255) // 256)
+    src = _lib.DeviceBuffer(words.nbytes).upload(words)
+    fold = _lib.DeviceBuffer(blocks * 4)
+    ms = C.c_float(0)
+    _lib.check(_lib.load().qv_stream_read_bench(src.ptr, words.nbytes, fold.ptr, 0, C.byref(ms)))
+    got = fold.download(np.uint32, (blocks,))
+    per_word = np.bitwise_xor.reduce(words, axis=1)
+    owner = (np.arange(nwords) % (blocks * 256)) // 256
+    want = np.zeros(blocks, np.uint32)
+    np.bitwise_xor.at(want, owner, per_word)
+    np.testing.assert_array_equal(got, want)
+    assert ms.value > 0
+    assert _lib.load().qv_stream_read_bench(src.ptr, 24, fold.ptr, 0, None) == _lib.QV_EINVAL
+
+
 def test_mixture_device_matches_host(lib):
     import quiver
     from quiver import _lib
