@@ -35,6 +35,8 @@ def test_help_and_required_flags():
     (["--early-exit-policy", "darth"], "invalid --early-exit-policy"),
     (["--num-blocks-list", "8,x"], "invalid integer in --num-blocks-list"),
     (["--bogus"], "Unknown argument"),
+    (["--search-kernel", "fast"], "--search-kernel must be auto, lut or shared-pivots"),
+    (["--graph-placement", "disk"], "--graph-placement must be hbm or host"),
 ])
 def test_validation(tmp_path, flags, msg):
     r = run("--index-dir", tmp_path, "--query", "q.u8bin", "--data-type", "uint8", *flags)
@@ -54,7 +56,8 @@ def test_missing_index_is_an_error(tmp_path):
 
 
 @pytest.mark.gpu
-def test_cli_search_report_and_results(small_u8_index, tmp_path):
+@pytest.mark.parametrize("kernel,want", [(None, "lut"), ("shared-pivots", "shared-pivots")])
+def test_cli_search_report_and_results(small_u8_index, tmp_path, kernel, want):
     import qv_oracle as O
 
     ix = small_u8_index
@@ -64,10 +67,13 @@ def test_cli_search_report_and_results(small_u8_index, tmp_path):
     gf = tmp_path / "gt.ibin"
     gf.write_bytes(struct.pack("<ii", 100, 10) + np.ascontiguousarray(ix["gt"][:100], np.int32).tobytes())
     print(f"[gpu] CLI search {ix['dir']}", flush=True)
+    extra = ["--search-kernel", kernel] if kernel else []
     r = run("--index-dir", ix["dir"], "--query", qf, "--data-type", "uint8", "--ef-search", "64",
             "--repeat", "2", "--pipe-width", "1", "--ground-truth", gf, "--result-prefix", tmp_path / "res",
-            "--early-exit-policy", "none", "--final-recall-csv", tmp_path / "r.csv")
+            "--early-exit-policy", "none", "--final-recall-csv", tmp_path / "r.csv", *extra)
     assert r.returncode == 0, r.stderr
+    # 200 queries on 756 slots: auto takes the per-query-LUT kernel
+    assert f"[Quiver] search_kernel={want}" in r.stdout
     assert "QPS:" in r.stdout and "QueryLatency(ms): avg=" in r.stdout and "Recall @ 10:" in r.stdout
     ids = np.fromfile(tmp_path / "res_ids.bin", dtype="<i4")
     n, k = ids[:2]

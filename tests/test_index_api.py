@@ -104,6 +104,10 @@ def test_constructor_validation(tmp_path: Path, fake_binary: Path) -> None:
         IndexQuiver(tmp_path, memory_backend="disk", binary=fake_binary)
     with pytest.raises(ValueError, match="num_blocks must be positive"):
         IndexQuiver(tmp_path, num_blocks=0, binary=fake_binary)
+    with pytest.raises(ValueError, match="search_kernel"):
+        IndexQuiver(tmp_path, search_kernel="fast", binary=fake_binary)
+    with pytest.raises(ValueError, match="graph_placement"):
+        IndexQuiver(tmp_path, graph_placement="disk", binary=fake_binary)
     with pytest.raises(ValueError, match="must not be empty"):
         IndexQuiver(tmp_path, ssds=[" "], binary=fake_binary)
     with pytest.raises(QuiverError, match="executable not found"):
