@@ -29,6 +29,7 @@ struct qv_index {
   int32_t nav_max_m = 0, nav_start = 0;
   int64_t device_bytes = 0;
   int num_cus = 0;
+  int lds_cu = 0;  // LDS bytes per CU
   hipStream_t stream = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   // search scratch (grown on demand, reused across calls)

@@ -25,7 +25,9 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <map>
 #include <memory>
+#include <tuple>
 #include <mutex>
 #include <numeric>
 #include <thread>
@@ -1091,6 +1093,7 @@ qv_index* make_index(int device, const Layout& lay, const PQTables& pq, uint8_t*
   hipDeviceProp_t prop;
   HIP_OK(hipGetDeviceProperties(&prop, device));
   ix->num_cus = prop.multiProcessorCount;
+  HIP_OK(hipDeviceGetAttribute(&ix->lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, device));
   HIP_OK(hipStreamCreateWithFlags(&ix->stream, hipStreamNonBlocking));
   HIP_OK(hipEventCreate(&ix->ev0));
   HIP_OK(hipEventCreate(&ix->ev1));
@@ -1112,13 +1115,24 @@ qv_index* make_index(int device, const Layout& lay, const PQTables& pq, uint8_t*
   return ix.release();
 }
 
-// Resident workgroups of kernel k per CU at `waves` waves and `lds` bytes.
-static int occupancy(KernelFn k, int waves, int lds) {
-  HIP_OK(hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                             std::max(lds, 65536)));
+// Resident workgroups of kernel k per CU at `waves` waves and `lds` bytes on
+// `device` (the current one).  The first query of a kernel on a device also
+// lets it take up to lds_cu bytes of dynamic LDS; answers are cached, since a
+// search asks for its plan on every call.
+static int occupancy(int device, int lds_cu, KernelFn k, int waves, int lds) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, const void*, int, int>, int> cache;
+  const void* f = reinterpret_cast<const void*>(k);
+  std::lock_guard<std::mutex> lk(mu);
+  const auto key = std::make_tuple(device, f, waves, lds);
+  const auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  const auto any = cache.lower_bound(std::make_tuple(device, f, INT32_MIN, INT32_MIN));
+  if (any == cache.end() || std::get<0>(any->first) != device || std::get<1>(any->first) != f)
+    HIP_OK(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, std::max(lds_cu, 65536)));
   int nb = 0;
-  HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(k), kWave * waves,
-                                                      (size_t)lds));
+  HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, kWave * waves, (size_t)lds));
+  cache.emplace(key, nb);
   return nb;
 }
 
@@ -1140,7 +1154,7 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
   lut.kern = pick_kernel(ix->lay.data_type, P, M);
   lut.waves = 1;
   lut.lds = lds_plan(M, d, P, true).total;
-  lut.slots_per_cu = occupancy(lut.kern, 1, lut.lds);
+  lut.slots_per_cu = occupancy(ix->device, ix->lds_cu, lut.kern, 1, lut.lds);
   if (want == QV_KERNEL_LUT) return lut;
   const bool forced = want == QV_KERNEL_SHARED_PIVOTS;
   if (!forced && lut.slots_per_cu > 0 && need <= (int64_t)lut.slots_per_cu * ix->num_cus) return lut;
@@ -1151,8 +1165,7 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
     if (forced) fail(QV_EUNSUPPORTED, "the shared-pivot kernel needs PQ chunks of 4 dims (M = 32) or 2 dims (M = 48)");
     return lut;
   }
-  int lds_cu = 0;
-  HIP_OK(hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, ix->device));
+  const int lds_cu = ix->lds_cu;
   const int Psp = beam_chunks_sp(ef);
   const int per_wave = lds_plan(M, d, Psp, false).total;
   const int waves = std::min(16, (lds_cu - piv_bytes(d)) / per_wave);
@@ -1162,7 +1175,7 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
   sp.waves = waves;
   sp.lds = piv_bytes(d) + waves * per_wave;
   sp.variant = QV_KERNEL_SHARED_PIVOTS;
-  if (waves < 1 || occupancy(sp.kern, waves, sp.lds) < 1) {
+  if (waves < 1 || occupancy(ix->device, ix->lds_cu, sp.kern, waves, sp.lds) < 1) {
     if (forced) fail(QV_EUNSUPPORTED, "the shared-pivot kernel does not fit on a compute unit");
     return lut;
   }
