@@ -794,7 +794,26 @@ struct LaunchPlan {
   int lds = 0;
   int slots_per_cu = 0;
   int variant = QV_KERNEL_LUT;
+  int lds_shared = 0;  // LDS of the workgroup beside its waves' (the shared pivots)
+  int lds_wave = 0;    // LDS per wave (query)
 };
+
+// Grid of a launch holding `slots` query slots.  A shared-pivot workgroup
+// that a full device would give lp.waves waves gets fewer when the slots do
+// not fill every CU, so the queries spread over all CUs instead of packing
+// into the first ones.
+struct LaunchShape {
+  int grid, waves, lds;
+};
+LaunchShape shape_launch(const LaunchPlan& lp, int64_t slots, int num_cus) {
+  LaunchShape sh;
+  sh.waves = lp.waves;
+  if (lp.variant == QV_KERNEL_SHARED_PIVOTS)
+    sh.waves = (int)std::max<int64_t>(1, std::min<int64_t>(lp.waves, (slots + num_cus - 1) / num_cus));
+  sh.grid = (int)((slots + sh.waves - 1) / sh.waves);
+  sh.lds = lp.variant == QV_KERNEL_SHARED_PIVOTS ? lp.lds_shared + sh.waves * lp.lds_wave : lp.lds;
+  return sh;
+}
 
 }  // namespace
 
@@ -1174,6 +1193,8 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
   sp.kern = pick_kernel_sp(ix->lay.data_type, Psp, M);
   sp.waves = waves;
   sp.lds = piv_bytes(d) + waves * per_wave;
+  sp.lds_shared = piv_bytes(d);
+  sp.lds_wave = per_wave;
   sp.variant = QV_KERNEL_SHARED_PIVOTS;
   if (waves < 1 || occupancy(ix->device, ix->lds_cu, sp.kern, waves, sp.lds) < 1) {
     if (forced) fail(QV_EUNSUPPORTED, "the shared-pivot kernel does not fit on a compute unit");
@@ -1240,9 +1261,10 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
   if (lp.slots_per_cu <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
   int nb = num_blocks > 0 ? num_blocks : lp.slots_per_cu * ix->num_cus;
   nb = (int)std::min<int64_t>(std::min<int64_t>(nb, nq), (int64_t)lp.slots_per_cu * ix->num_cus);
-  const int grid = (nb + lp.waves - 1) / lp.waves;
+  const LaunchShape ls = shape_launch(lp, nb, ix->num_cus);
+  const int grid = ls.grid;
   const bool use_bits = lp.variant == QV_KERNEL_LUT;
-  if (use_bits) ensure_bits(ix, (int64_t)grid * lp.waves);
+  if (use_bits) ensure_bits(ix, (int64_t)grid * ls.waves);
   SearchArgs a = base_args(ix);
   a.queries = d_queries;
   a.nq = (int32_t)nq;
@@ -1270,7 +1292,7 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
   a.rec_cap = rec.cap;
   HIP_OK(hipMemsetAsync(ix->d_counters, 0, 64, ix->stream));
   if (use_bits) ix->bits_dirty = true;
-  hipLaunchKernelGGL(lp.kern, dim3(grid), dim3(kWave * lp.waves), (size_t)lp.lds, ix->stream, a);
+  hipLaunchKernelGGL(lp.kern, dim3(grid), dim3(kWave * ls.waves), (size_t)ls.lds, ix->stream, a);
   HIP_OK(hipGetLastError());
   HIP_OK(hipStreamSynchronize(ix->stream));
   int32_t counters[4] = {0, 0, 0, 0};
@@ -1315,11 +1337,14 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   // is a one-wave workgroup, so the reference's Q-interleave -- a block
   // switching between its slots while one waits on memory -- is the CU's own
   // wave interleaving here.  Slots beyond what the device holds resident would
-  // only wait for a free CU, so the grid stops at the resident capacity; the
-  // admission window keeps the requested slot count.
+  // only wait for a free CU, and slots beyond the number of queries would find
+  // no ticket, so the grid stops at both; the admission window keeps the
+  // requested slot count.
   const int64_t slots = (int64_t)(o.num_blocks > 0 ? o.num_blocks : spc * ix->num_cus) * o.queries_per_block;
-  const int grid = (int)((std::min<int64_t>(slots, (int64_t)spc * ix->num_cus) + lp.waves - 1) / lp.waves);
-  const int num_blocks = grid * lp.waves;  // query slots (waves) launched
+  const int64_t launched = std::min<int64_t>(std::min<int64_t>(slots, (int64_t)spc * ix->num_cus), nq);
+  const LaunchShape ls = shape_launch(lp, launched, ix->num_cus);
+  const int grid = ls.grid;
+  const int num_blocks = grid * ls.waves;  // query slots (waves) launched
   const int max_inflight = (int)std::min<int64_t>(nq, slots + std::max(0, o.prefeed));
   const bool use_bits = lp.variant == QV_KERNEL_LUT;
   if (use_bits) ensure_bits(ix, num_blocks);
@@ -1382,7 +1407,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   using clock = std::chrono::steady_clock;
   if (use_bits) ix->bits_dirty = true;  // until every admitted query is seen to finish
   HIP_OK(hipEventRecord(ix->ev0, ix->stream));
-  hipLaunchKernelGGL(lp.kern, dim3(grid), dim3(kWave * lp.waves), (size_t)lp.lds, ix->stream, a);
+  hipLaunchKernelGGL(lp.kern, dim3(grid), dim3(kWave * ls.waves), (size_t)ls.lds, ix->stream, a);
   HIP_OK(hipGetLastError());
   HIP_OK(hipEventRecord(ix->ev1, ix->stream));
 

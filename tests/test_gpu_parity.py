@@ -132,6 +132,8 @@ def test_auto_kernel_follows_queries_in_flight(lib, small_u8_index):
         index = quiver.IndexQuiver(ix["dir"], data_type="uint8", pipe_width=1, num_blocks=num_blocks)
         ids, dists = index.search(q8[:nq], topk=10, ef_search=64, early_exit_policy="none")
         assert index.last_report["kernel"] == KERNELS[want], (nq, num_blocks)
+        # slots launched: no more than the queries (whole workgroups of at most 16 waves)
+        assert min(nq, num_blocks) <= index.last_report["num_blocks"] < min(nq, num_blocks) + 16
         index.close()
         np.testing.assert_array_equal(ids, oids[:nq])
         np.testing.assert_array_equal(dists, odists[:nq])
