@@ -3,10 +3,13 @@
 // Reference path (ruc-system/quiver-ae): persistent_search_kernel
 // (src/quiver/kernel_core/kernel_q1.cuh:20-757) driven by run_persistent_search
 // (src/quiver/search.cu:357-1361).  Differences by design:
-//   * one 64-lane wavefront per query; workgroups of one wave; the LUT, the
-//     query and the beam live in LDS; neighbour lists, vectors and PQ codes are
-//     read straight from HBM (no CPU poll threads, no 4 KB page copies), and the
-//     next node's record is requested while the current hop finishes;
+//   * one 64-lane wavefront per query, in one of two kernels: search_kernel
+//     (one-wave workgroups, the query's fp32 LUT in LDS) or search_kernel_sp
+//     (one workgroup of up to 16 waves per CU sharing the PQ pivots in LDS,
+//     each LUT entry recomputed where it is read); query and beam live in LDS;
+//     neighbour lists, vectors and PQ codes are read straight from HBM (no CPU
+//     poll threads, no 4 KB page copies), and the next node's record is
+//     requested while the current hop finishes;
 //   * the merge is built by rank: "is this neighbour already in the beam" is
 //     answered by a per-query bitmap in HBM (per-query-LUT kernel) or by the
 //     neighbour's own rank in the sorted LDS beam (shared-pivot kernel: a beam
