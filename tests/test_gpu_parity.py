@@ -81,6 +81,40 @@ def test_search_f32(lib, small_f32_index, pipe_width, ef, kernel):
 
 
 @pytest.fixture(scope="module")
+def small_i8_index(tmp_path_factory):
+    """6k x 128 int8 (the uint8 mixture shifted by -128), M = 32."""
+    import quiver
+
+    d = tmp_path_factory.mktemp("i8")
+    base = (quiver.mixture(6000, 128, num_centers=32, seed=21).astype(np.int16) - 128).astype(np.int8)
+    queries = (quiver.mixture(150, 128, num_centers=32, seed=21, first_row=10**6).astype(np.int16)
+               - 128).astype(np.int8)
+    quiver.build_index(base, d / "i8", R=32, L=48, num_chunks=32, threads=0)
+    return {"dir": d, "queries": queries}
+
+
+@pytest.mark.parametrize("kernel", ["lut", "shared-pivots"])
+@pytest.mark.parametrize("policy", ["none", "gpruning"])
+@pytest.mark.parametrize("ef", [64, 200])
+def test_search_i8_bit_exact(lib, small_i8_index, kernel, policy, ef):
+    """Signed 8-bit vectors (exact distances on sign-extended elements) through
+    both kernels, against the oracle."""
+    import quiver
+
+    ix = small_i8_index
+    _say(f"[gpu] search i8 kernel={kernel} policy={policy} ef={ef}")
+    index = quiver.IndexQuiver(ix["dir"], data_type="int8", pipe_width=1, num_blocks=512, search_kernel=kernel)
+    ids, dists = index.search(ix["queries"], topk=10, ef_search=ef, early_exit_policy=policy)
+    assert index.last_report["kernel"] == KERNELS[kernel]
+    index.close()
+    host = O.HostIndex.from_files(ix["dir"], "int8")
+    oids, odists, _, _ = O.search(host, ix["queries"].astype(np.float32), 10, ef,
+                                  early_exit=O.EXIT_GPRUNING if policy == "gpruning" else O.EXIT_NONE)
+    np.testing.assert_array_equal(ids, oids)
+    np.testing.assert_array_equal(dists, odists)
+
+
+@pytest.fixture(scope="module")
 def uneven_u8_index(tmp_path_factory):
     """3k x 100 uint8, M = 32: PQ chunks of 3 and 4 dims."""
     import quiver
