@@ -73,7 +73,7 @@ def main() -> int:
                     help="build a nav graph over every K-th base vector and start queries from it (0: medoid)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1",
+        print(json.dumps({"error": "bench.py measures one GPU only; run with --gpus 1",
                           "n_gpus": args.gpus}))
         return 2
 

@@ -2,7 +2,7 @@
  * qv_oracle.c -- CPU restatement of the Quiver query path (TEST INFRASTRUCTURE).
  *
  * Loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
- * leg, always as the checker.  Citations are ruc-system/quiver-ae paths.
+ * leg, always as the test oracle.  Citations are ruc-system/quiver-ae paths.
  *
  * Floating point: every `a += b * b` of the reference is written as fmaf(b, b, a)
  * because nvcc contracts that statement to one FFMA under its default

@@ -1,7 +1,7 @@
 /*
  * qv_oracle.h -- CPU restatement of the Quiver query path (TEST INFRASTRUCTURE).
  *
- * This library is the checker for the HIP path: only tests/, the smoke test and
+ * This library is the test oracle of the HIP path: only tests/, the smoke test and
  * bench.py's cpu_baseline leg may load it.  The product never links it.
  *
  * Every function restates a reference routine; the file:line it follows is in

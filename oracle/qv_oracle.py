@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (TEST INFRASTRUCTURE).
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's cpu_baseline leg import
-this module, always as the checker of the HIP path.  It reads DiskANN-format
+this module, always as the test oracle of the HIP path.  It reads DiskANN-format
 index files with its own NumPy reader (independent of the library's C++
 reader) and calls the C restatement in qv_oracle.c.
 """

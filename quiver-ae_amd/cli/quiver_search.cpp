@@ -190,7 +190,7 @@ int main(int argc, char** argv) {
     return 1;
   }
   if (f["--per-step-recall"].used) {
-    std::cerr << "--per-step-recall is not supported by this build" << std::endl;
+    std::cerr << "--per-step-recall is not supported by this binary" << std::endl;
     return 1;
   }
   std::vector<int> nb_list{num_blocks};

@@ -38,7 +38,7 @@ class IndexQuiver:
     Argument meaning, defaults and errors follow the reference binding.  The
     in-process engine keeps the graph, vectors and PQ codes resident in GPU
     memory (the heap memory backend); SSD options are accepted for
-    compatibility but the SPDK backend is not part of this build, so a search
+    compatibility but the SPDK backend is not part of this library, so a search
     with SSDs configured raises ``QuiverError`` unless an external ``binary``
     is used.
     """

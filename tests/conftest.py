@@ -14,7 +14,7 @@ for p in (ROOT / "quiver-ae_amd", ROOT / "oracle", ROOT / "tests"):
 
 
 def pytest_configure(config):
-    config.addinivalue_line("markers", "gpu: needs an MI355X (runs on the GPU box)")
+    config.addinivalue_line("markers", "gpu: needs an MI355X")
 
 
 @pytest.fixture(scope="session")
