@@ -423,6 +423,29 @@ __device__ __forceinline__ float nav_dist32(const float* __restrict__ q, const u
   return val;
 }
 
+// The same sum with the query's elements of this sub-lane in registers (qn[k] =
+// q[s + 32 k], 0 past dims) and the vector's elements already loaded (xr[k],
+// any value past dims): for dims <= 32 kNavPre.  Elements past dims add
+// fma(0, 0, val) = val, so the sum is nav_dist32's bit for bit.
+constexpr int kNavPre = 4;
+template <class T>
+__device__ __forceinline__ float nav_dist32_pre(const float (&qn)[kNavPre], const uint32_t (&xr)[kNavPre],
+                                                int dims, int lane) {
+  float val = 0.f;
+#pragma unroll
+  for (int k = 0; k < kNavPre; k++) {
+    const int i = (lane & 31) + 32 * k;
+    const float diff = i < dims ? qn[k] - raw_to_float<T>(xr[k]) : 0.f;
+    val = __fmaf_rn(diff, diff, val);
+  }
+  val += __uint_as_float(xor_lane32<16>(__float_as_uint(val), lane));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x108, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x104, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x102, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x101, 0xF, 0xF, false));
+  return val;
+}
+
 // Returns the mapped base id of the best nav node for query q (raw, before the
 // LUT's centring).  graph is [num_node][max_m] with -1 after the degree;
 // indexes past the end of graph read as -1.  With fewer than four distinct
@@ -431,7 +454,7 @@ __device__ __forceinline__ float nav_dist32(const float* __restrict__ q, const u
 // reference then reads nav_mapping[0x7fffffff].  Here that case returns
 // `fallback` (the medoid).
 template <class T>
-__device__ int32_t nav_entry(const float* __restrict__ q, const uint8_t* __restrict__ data,
+__device__ __forceinline__ int32_t nav_entry(const float* __restrict__ q, const uint8_t* __restrict__ data,
                              const int32_t* __restrict__ graph, const int32_t* __restrict__ mapping,
                              int64_t num_node, int dims, int max_m, int start, int32_t fallback) {
   const int lane = opaque_lane();
@@ -448,6 +471,14 @@ __device__ int32_t nav_entry(const float* __restrict__ q, const uint8_t* __restr
       pdist = d0;
     }
   }
+  // the query elements of this sub-lane, for the short-vector path
+  const bool pre = dims <= 32 * kNavPre;
+  float qn[kNavPre];
+#pragma unroll
+  for (int k = 0; k < kNavPre; k++) {
+    const int i = (lane & 31) + 32 * k;
+    qn[k] = q[min(i, dims - 1)];
+  }
   int idx = 0;
   while (idx != -1) {
     const int u = (int)(read_lane_u32(pid, idx) & 0x7fffffffu);
@@ -456,8 +487,55 @@ __device__ int32_t nav_entry(const float* __restrict__ q, const uint8_t* __restr
     // chunk (one warp of the reference) the first -1 ends the chunk, and the
     // slots it leaves keep their values.
     const int64_t e0 = (int64_t)max_m * u;
+    if (pre) {
+      // The 28 reads of the row in one load (lane i reads entry i), then every
+      // pair's vector elements requested before the first distance is summed.
+      const int32_t gv = lane < kNavR && e0 + lane < glen ? graph[e0 + lane] : -1;
+      const uint64_t neg = __ballot(lane < kNavR && gv == -1);
+      uint32_t okm = 0;  // neighbour i counts iff no -1 precedes it in its chunk
+#pragma unroll
+      for (int c = 0; c < kNavR / kNavChunk; c++) {
+        const uint32_t cm = (uint32_t)(neg >> (kNavChunk * c)) & ((1u << kNavChunk) - 1u);
+        const int first = cm ? __ffs((int)cm) - 1 : kNavChunk;
+        okm |= ((1u << first) - 1u) << (kNavChunk * c);
+      }
+      // Pairs in batches of kNavBatch: every pair of a batch has its vector
+      // elements requested before the first of them is summed.
+      constexpr int kNavBatch = 7;
+#pragma unroll
+      for (int b = 0; b < kNavR / 2; b += kNavBatch) {
+        uint32_t xr[kNavBatch][kNavPre];
+#pragma unroll
+        for (int jj = 0; jj < kNavBatch; jj++) {
+          const int j = b + jj;
+          if (j >= kNavR / 2) break;
+          // half h of the wave takes neighbour 2 j + h (node 0 when it does not count)
+          const int32_t v0 = (okm >> (2 * j)) & 1u ? read_lane_i32(gv, 2 * j) : 0;
+          const int32_t v1 = (okm >> (2 * j + 1)) & 1u ? read_lane_i32(gv, 2 * j + 1) : 0;
+          load_vec_pre<T>(data + (int64_t)(half ? v1 : v0) * row, dims, lane, xr[jj]);
+        }
+#pragma unroll
+        for (int jj = 0; jj < kNavBatch; jj++) {
+          const int j = b + jj;
+          if (j >= kNavR / 2) break;
+          const int i0 = 2 * j, i1 = 2 * j + 1;
+          const bool ok0 = (okm >> i0) & 1u, ok1 = (okm >> i1) & 1u;
+          if (!ok0 && !ok1) continue;
+          const float dh = nav_dist32_pre<T>(qn, xr[jj], dims, lane);
+          const float d0 = read_lane_f32(dh, 0), d1 = read_lane_f32(dh, 32);
+          if (ok0 && lane == kNavL + i0) {
+            pid = (uint32_t)read_lane_i32(gv, i0);
+            pdist = d0;
+          }
+          if (ok1 && lane == kNavL + i1) {
+            pid = (uint32_t)read_lane_i32(gv, i1);
+            pdist = d1;
+          }
+        }
+      }
+    }
     uint32_t broken = 0;  // chunks that met a -1
-    for (int j = 0; j < kNavR / 2; j++) {
+    for (int j = 0; !pre && j < kNavR / 2; j++) {
       const int i0 = 2 * j, i1 = 2 * j + 1;
       const int32_t v0 = e0 + i0 < glen ? graph[e0 + i0] : -1;
       const int32_t v1 = e0 + i1 < glen ? graph[e0 + i1] : -1;
