@@ -159,10 +159,11 @@ def main() -> int:
     d_ids = _lib.DeviceBuffer(nq * 10 * 4)
     d_dists = _lib.DeviceBuffer(nq * 10 * 4)
 
-    def run(ef: int, policy: int, pipe: int = 1):
+    def run(ef: int, policy: int, pipe: int = 1, skip_nav: int = 0):
         o = _lib.default_search_opts()
         o.early_exit = policy
         o.pipe_width = pipe
+        o.skip_nav = skip_nav
         o.kernel = _lib.KERNEL_NAMES[args.search_kernel]
         o.device_buffers = 1
         o.admission = _lib.QV_ADMIT_STREAMING
@@ -239,6 +240,14 @@ def main() -> int:
     last = reps[-1]
     log(f"timed: ef={ef} {pname} steps={args.steps} qps={qps:.0f} recall={recall:.4f} p50={p50:.3f} p99={p99:.3f}")
 
+    # with a nav graph: the same steps from the medoid, to price the nav search
+    medoid_entry = None
+    if info.nav_nodes > 0:
+        mreps = [run(ef, policy, skip_nav=1) for _ in range(args.steps)]
+        medoid_entry = {"kernel_ms": round(float(np.median([r.kernel_ms for r in mreps])), 3),
+                        "recall_at_10": round(recall_of(), 4), "avg_hops": round(mreps[-1].avg_hops, 2)}
+        log(f"medoid entry, same steps: {medoid_entry}")
+
     # roofline of the search kernel: algorithmic bytes per launch = node
     # records of the expanded nodes + one PQ code row per neighbour
     # evaluation + queries in + top-k out; time from HIP events on its stream.
@@ -265,7 +274,8 @@ def main() -> int:
                    "graph_placement": args.graph_placement, "nav_nodes": int(info.nav_nodes),
                    "admission": "streaming (window = num_blocks)", "recall_at_10": round(recall, 4),
                    "p50_ms": round(p50, 3), "p99_ms": round(p99, 3), "avg_hops": round(last.avg_hops, 2),
-                   "build_s": round(build_s, 1)},
+                   "build_s": round(build_s, 1),
+                   **({"medoid_entry": medoid_entry} if medoid_entry else {})},
         "roofline": roofline,
         "sweep": sweep,
     }
