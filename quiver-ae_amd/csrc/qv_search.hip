@@ -174,7 +174,7 @@ struct Query {
   // beam.  The bitmap costs a random read per neighbour but nothing on the
   // hop's critical path (the read overlaps the code rows); the rank costs a
   // dependent LDS binary search after the ADC but no memory traffic, which
-  // pays when 8 queries per CU compete for the device's random accesses.
+  // pays when 8 to 16 queries per CU compete for the device's random accesses.
   static constexpr bool kBits = SC == 0;
 
   // smem: this query's LDS area; slot: this wave's bitmap index.
@@ -784,8 +784,9 @@ KernelFn pick_kernel_sp(int dtype, int Q, int M) {
 // Beam positions per lane for ef (beam capacity 64 Q >= ef; kMaxEf = 448 = 64 * 7).
 // The per-query-LUT kernel comes in Q = 1, 2, 4, 7 (its 32 KB LUT, not the
 // beam, sets how many queries a CU holds); the shared-pivot kernel in every Q
-// from 1 to 7, since there the beam's LDS decides between 6, 7 and 8 queries
-// per CU (at d = 128: 8 up to ef = 320, 7 up to 384, 6 up to 448).
+// from 1 to 7, since there the beam's LDS decides how many queries a CU holds
+// (at d = 128: 16 up to ef = 192, 12 up to 256, 10 up to 320, 9 up to 384, 8 up to
+// 448).
 int beam_chunks(int ef) { return ef <= 64 ? 1 : (ef <= 128 ? 2 : (ef <= 256 ? 4 : 7)); }
 int beam_chunks_sp(int ef) { return (std::max(ef, 1) + kWave - 1) / kWave; }
 
