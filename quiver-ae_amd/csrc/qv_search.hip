@@ -107,8 +107,9 @@ struct SearchArgs {
 enum : int32_t { kErrSpinTimeout = 1 };
 
 // Dynamic LDS carve-up of one query (one wave), shared by the kernel and its
-// launcher.  Q = beam positions per lane: the beam holds up to Q * 64 >= ef
-// entries.  With a per-query LUT (lut) the table comes first; the shared-
+// launcher.  Q = beam positions per lane: the register beam holds Q * 64 >= ef
+// entries, the LDS beam cap of them (beam_cap).  With a per-query LUT (lut) the
+// table comes first; the shared-
 // pivot kernel has none, and when every query element the exact distance
 // needs fits the lanes' registers (dim <= 32 kVecPre) its beam overlays the
 // query copy qu, which is only read once, into those registers, before the
@@ -117,7 +118,12 @@ struct LdsPlan {
   int lut_off, qc_off, qu_off, beam_off, total;
 };
 
-__host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool lut) {
+// LDS beam entries: Q * 64 with the per-query LUT (its table, not the beam,
+// limits the queries per CU); ef rounded up to 8 with shared pivots, where the
+// beam's LDS decides how many queries a CU holds.
+__host__ __device__ inline int beam_cap(int ef, int Q, bool lut) { return lut ? Q * kWave : (ef + 7) & ~7; }
+
+__host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool lut, int ef) {
   LdsPlan p;
   p.lut_off = 0;
   p.qc_off = p.lut_off + (lut ? num_chunks * kPivots * 4 : 0);
@@ -125,7 +131,7 @@ __host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool
   p.qu_off = p.qc_off + dpad * 4;
   const bool overlay = !lut && dim <= 32 * kVecPre;
   p.beam_off = overlay ? p.qu_off : (p.qu_off + dpad * 4 + 15) & ~15;
-  const int beam_bytes = Q * kWave * 8;
+  const int beam_bytes = beam_cap(ef, Q, lut) * 8;
   p.total = p.beam_off + (overlay && dpad * 4 > beam_bytes ? dpad * 4 : beam_bytes);
   return p;
 }
@@ -157,6 +163,7 @@ struct Query {
   uint64_t* beam;
   uint32_t* bits;  // this slot's membership bitmap (SC == 0)
   int sz;        // beam size (ctx.size)
+  int cap;       // LDS beam entries (beam_cap >= ef)
   // The beam in registers, chunk-major (lane l holds positions [l Q, l Q + Q),
   // kPadKey at and beyond sz), and its first unvisited entry u with key bu
   // (INT32_MAX and ~0 when every entry is visited).  LDS holds the same beam
@@ -183,7 +190,8 @@ struct Query {
         evals(0) {
 #pragma unroll
     for (int k = 0; k < Q; k++) ck[k] = kPadKey;
-    LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, SC == 0);
+    LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, SC == 0, a.ef);
+    cap = beam_cap(a.ef, Q, SC == 0);
     lut = reinterpret_cast<float*>(smem + pl.lut_off);
     qc = reinterpret_cast<float*>(smem + pl.qc_off);
     qu = reinterpret_cast<float*>(smem + pl.qu_off);
@@ -277,13 +285,14 @@ struct Query {
     return merge_select<PF>(nkey, fresh, lane, nr, spec);
   }
 
-  // Without the bitmap, every LDS beam position at or beyond sz holds kPadKey
+  // Without the bitmap, every LDS beam position from sz to cap holds kPadKey
   // (above every key): set once per query; merges only write below the new
   // sz, which never shrinks.  The rank search then needs no bounds test.
   __device__ __forceinline__ void pad_beam(int lane) {
     if constexpr (!kBits) {
 #pragma unroll
-      for (int k = 0; k < Q; k++) beam[k * kWave + lane] = kPadKey;
+      for (int k = 0; k < Q; k++)
+        if (k * kWave + lane < cap) beam[k * kWave + lane] = kPadKey;
     }
   }
 
@@ -342,19 +351,21 @@ struct Query {
     if constexpr (!kBits) {
       if (__ballot(below)) {
         // r = #{beam entries e : e < (nkey & ~1)} by binary lifting over the
-        // LDS beam: sorted, kPadKey from sz to the capacity kCap = 64 Q, so
-        // a read clamped to kCap - 1 sees either a key of the beam or kPadKey
+        // LDS beam: sorted, kPadKey from sz to its capacity cap (>= ef), so
+        // a read clamped to cap - 1 sees either a key of the beam or kPadKey
         // (a below candidate is under the last key of a full beam, so even a
-        // full-capacity beam never lifts r past it).  Steps are uniform.
+        // full-capacity beam never lifts r past it).  Steps are uniform and
+        // cover 64 Q >= cap positions.
         constexpr int kCap = Q * kWave;
         constexpr int kTop = kCap >= 256 ? 256 : (kCap >= 128 ? 128 : 64);
+        const int top = cap - 1;
         const uint64_t c0 = nkey & ~1ull;
 #pragma unroll
         for (int step = kTop; step > 0; step >>= 1) {
-          const uint64_t e = beam[min(r + step - 1, kCap - 1)];
+          const uint64_t e = beam[min(r + step - 1, top)];
           r += e < c0 ? step : 0;
         }
-        const uint64_t at = beam[min(r, kCap - 1)];
+        const uint64_t at = beam[min(r, top)];
         valid = below && (at >> 1) != (nkey >> 1);
       }
     }
@@ -692,7 +703,7 @@ __global__ __launch_bounds__(1024) void search_kernel_sp(SearchArgs a) {
   }
   __syncthreads();
   const int w = threadIdx.x / kWave;
-  const LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, false);
+  const LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, false, a.ef);
   run_queries<T, Q, MC, SC>(a, smem + piv_bytes(a.dim) + w * pl.total, piv, 0);
 }
 
@@ -784,9 +795,9 @@ KernelFn pick_kernel_sp(int dtype, int Q, int M) {
 // Beam positions per lane for ef (beam capacity 64 Q >= ef; kMaxEf = 448 = 64 * 7).
 // The per-query-LUT kernel comes in Q = 1, 2, 4, 7 (its 32 KB LUT, not the
 // beam, sets how many queries a CU holds); the shared-pivot kernel in every Q
-// from 1 to 7, since there the beam's LDS decides how many queries a CU holds
-// (at d = 128: 16 up to ef = 192, 12 up to 256, 10 up to 320, 9 up to 384, 8 up to
-// 448).
+// from 1 to 7 (its LDS beam holds ef rounded up to 8 entries, and that decides
+// how many queries a CU holds: at d = 128, 16 up to ef = 192, then 15 at 208,
+// 13 at 240, 12 at 256, 11 at 288, 10 at 320, 9 at 384, 8 at 448).
 int beam_chunks(int ef) { return ef <= 64 ? 1 : (ef <= 128 ? 2 : (ef <= 256 ? 4 : 7)); }
 int beam_chunks_sp(int ef) { return (std::max(ef, 1) + kWave - 1) / kWave; }
 
@@ -1176,7 +1187,7 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
   LaunchPlan lut;
   lut.kern = pick_kernel(ix->lay.data_type, P, M);
   lut.waves = 1;
-  lut.lds = lds_plan(M, d, P, true).total;
+  lut.lds = lds_plan(M, d, P, true, ef).total;
   lut.slots_per_cu = occupancy(ix->device, ix->lds_cu, lut.kern, 1, lut.lds);
   if (want == QV_KERNEL_LUT) return lut;
   const bool forced = want == QV_KERNEL_SHARED_PIVOTS;
@@ -1190,7 +1201,7 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
   }
   const int lds_cu = ix->lds_cu;
   const int Psp = beam_chunks_sp(ef);
-  const int per_wave = lds_plan(M, d, Psp, false).total;
+  const int per_wave = lds_plan(M, d, Psp, false, ef).total;
   const int waves = std::min(16, (lds_cu - piv_bytes(d)) / per_wave);
   if (!forced && waves <= lut.slots_per_cu) return lut;
   LaunchPlan sp;
