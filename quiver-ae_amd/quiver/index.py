@@ -1,20 +1,27 @@
-"""NumPy interface with the reference's API (python/quiver/index.py:27-264).
+"""NumPy front end with the reference binding's interface
+(python/quiver/index.py:27-264): ``IndexQuiver(index_dir, ...).search(queries,
+topk, ef_search=...)`` returns ``(ids int32[n, topk], distances float32[n,
+topk])``.
 
-``IndexQuiver(index_dir, ...).search(queries, topk, ef_search=...)`` returns
-``(ids int32[n, topk], distances float32[n, topk])``.  By default the search
-runs in-process through libquiver_hip's C ABI on the GPU; when ``binary`` (or
-``QUIVER_BINARY``) names an engine executable, the call shells out to it with
-the reference's command line and reads its result files, exactly as the
-reference binding does.
+Two engines sit behind the one facade:
+
+* ``_LibraryEngine`` (default): libquiver_hip's C ABI in this process; the
+  graph, vectors and PQ codes stay resident in GPU memory between searches.
+* ``_ProcessEngine`` (when ``binary=`` or ``QUIVER_BINARY`` names an
+  executable): runs that ``quiver_search`` once per call with the reference's
+  command-line contract -- query file in, ``<prefix>_ids.bin`` /
+  ``<prefix>_distances.bin`` out -- so any engine speaking it can be plugged in.
+
+Argument names, defaults, accepted values and error messages are the
+reference binding's, because callers depend on them.
 """
 from __future__ import annotations
 
 import ctypes as C
 import os
-import shutil
-import struct
 import subprocess
 import tempfile
+from dataclasses import dataclass
 from pathlib import Path
 from typing import Mapping, Sequence
 
@@ -22,25 +29,202 @@ import numpy as np
 import numpy.typing as npt
 
 from . import _lib
+from ._binfile import read_matrix, write_matrix
 from ._lib import QuiverError
 
-_DATA_TYPES = {
-    "float": (np.dtype("<f4"), ".fbin"),
-    "float32": (np.dtype("<f4"), ".fbin"),
-    "uint8": (np.dtype("u1"), ".u8bin"),
-    "int8": (np.dtype("i1"), ".i8bin"),
-}
+# Element type of an index, by its canonical --data-type name: the dtype queries
+# are converted to and the query-file suffix (python/quiver/index.py:18-23).
+_ELEMENTS = {"float": ("<f4", ".fbin"), "uint8": ("u1", ".u8bin"), "int8": ("i1", ".i8bin")}
+_TYPE_ALIASES = {"float32": "float"}
+_POLICIES = ("gpruning", "none")
+
+
+def _positive(name: str, value) -> int:
+    number = int(value)
+    if number <= 0:
+        raise ValueError(f"{name} must be positive")
+    return number
+
+
+def _count_ssds(list_file: Path) -> int:
+    """Lines naming an SSD: non-blank and not a '#' comment."""
+    entries = (line.strip() for line in list_file.read_text().splitlines())
+    return sum(1 for entry in entries if entry and entry[0] != "#")
+
+
+@dataclass(frozen=True)
+class _EngineKnobs:
+    """The per-index engine settings both engines forward."""
+
+    num_blocks: int
+    queries_per_block: int
+    pipe_width: int
+    poll_threads: int
+    runners_per_ssd: int
+
+
+class _LibraryEngine:
+    """Searches through libquiver_hip's C ABI on one GPU."""
+
+    def __init__(self, owner: "IndexQuiver", device: int, graph_placement: str, search_kernel: str) -> None:
+        self._owner = owner
+        self._device = device
+        self._placement = _lib.QV_GRAPH_HOST if graph_placement == "host" else _lib.QV_GRAPH_HBM
+        self._kernel = _lib.KERNEL_NAMES[search_kernel]
+        self._handle: C.c_void_p | None = None
+        _lib.load()  # a missing library fails here, not at the first search
+
+    def handle(self) -> C.c_void_p:
+        if self._handle is None:
+            o = self._owner
+            handle = C.c_void_p()
+            _lib.check(_lib.load().qv_index_open_ex(
+                str(o.index_dir).encode(), o.data_type.encode(), o.memory_backend.encode(), None,
+                self._device, self._placement, C.byref(handle)))
+            self._handle = handle
+        return self._handle
+
+    def _options(self, policy: str, timeout: float | None, skip_nav: bool) -> _lib.SearchOpts:
+        knobs = self._owner._knobs
+        opts = _lib.default_search_opts()
+        opts.num_blocks = knobs.num_blocks
+        opts.queries_per_block = knobs.queries_per_block
+        opts.pipe_width = knobs.pipe_width
+        opts.early_exit = _lib.QV_EXIT_GPRUNING if policy == "gpruning" else _lib.QV_EXIT_NONE
+        opts.timeout_s = 0.0 if timeout is None else float(timeout)
+        opts.skip_nav = int(skip_nav)
+        opts.kernel = self._kernel
+        # the admission knobs the reference engine reads from its environment
+        # (src/quiver/search.cu:827-860)
+        env = {**os.environ, **self._owner.env}
+        if env.get("QUIVER_PREFEED"):
+            opts.prefeed = int(env["QUIVER_PREFEED"])
+        if env.get("QUIVER_ADMIT_MIN_BATCH"):
+            opts.admit_min_batch = max(1, int(env["QUIVER_ADMIT_MIN_BATCH"]))
+        return opts
+
+    def search(self, queries: np.ndarray, topk: int, ef_search: int, policy: str,
+               timeout: float | None, extra_args: Sequence[str]):
+        extra = [str(a) for a in extra_args]
+        skip_nav = "--skip-nav" in extra
+        if any(a != "--skip-nav" for a in extra):
+            raise QuiverError("extra_args other than --skip-nav need an external quiver_search binary")
+        if self._owner.num_ssds:
+            raise QuiverError("This binary was built without SPDK support")
+        handle = self.handle()
+        q = np.ascontiguousarray(queries, dtype=np.float32)  # load_queries_as_float
+        n, dim = q.shape
+        ids = np.empty((n, topk), np.int32)
+        dists = np.empty((n, topk), np.float32)
+        found = np.empty(n, np.int32)
+        report = _lib.SearchReport()
+        opts = self._options(policy, timeout, skip_nav)
+        rc = _lib.load().qv_search(handle, q.ctypes.data, n, dim, topk, ef_search, C.byref(opts),
+                                   ids.ctypes.data, dists.ctypes.data, found.ctypes.data, C.byref(report))
+        if rc == _lib.QV_ETIMEDOUT and timeout is not None:
+            raise QuiverError(f"quiver_search exceeded the {timeout:g} second timeout")
+        _lib.check(rc)  # any other failure (the kernel's own watchdog included) with the library's text
+        self._owner.last_report = report.as_dict()
+        return ids, dists
+
+    def close(self) -> None:
+        if self._handle is not None:
+            _lib.load().qv_index_close(self._handle)
+            self._handle = None
+
+
+class _ProcessEngine:
+    """Runs an external quiver_search per call (bin/quiver_search.cu:58-320)."""
+
+    def __init__(self, owner: "IndexQuiver", executable: Path) -> None:
+        self._owner = owner
+        self.executable = executable
+
+    def _argv(self, query_file: Path, result_prefix: Path, topk: int, ef_search: int, policy: str,
+              ssd_list: Path | None, extra_args: Sequence[str]) -> list[str]:
+        o, k = self._owner, self._owner._knobs
+        pairs = {
+            "--index-dir": o.index_dir, "--data-type": o.data_type, "--memory-backend": o.memory_backend,
+            "--query": query_file, "--result-prefix": result_prefix,
+            "--topk": topk, "--ef-search": ef_search, "--early-exit-policy": policy,
+            "--repeat": 1,  # one timed pass per call
+            "--num-blocks": k.num_blocks, "--queries-per-block": k.queries_per_block,
+            "--pipe-width": k.pipe_width, "--poll-threads": k.poll_threads,
+            "--runners-per-ssd": k.runners_per_ssd,
+        }
+        if ssd_list is not None:
+            pairs["--ssd-list-file"] = ssd_list
+        argv = [str(self.executable)]
+        for flag, value in pairs.items():
+            argv += [flag, str(value)]
+        return argv + [str(a) for a in extra_args]
+
+    def _environment(self) -> dict[str, str]:
+        env = dict(os.environ)
+        env.update(self._owner.env)
+        if self._owner.spdk_base_lba is not None:
+            env["SPDK_BASE_LBA"] = str(self._owner.spdk_base_lba)
+        return env
+
+    def search(self, queries: np.ndarray, topk: int, ef_search: int, policy: str,
+               timeout: float | None, extra_args: Sequence[str]):
+        o = self._owner
+        with tempfile.TemporaryDirectory(prefix="quiver-python-") as scratch:
+            work = Path(scratch)
+            query_file = work / ("queries" + o._query_suffix)
+            write_matrix(query_file, queries)
+            ssd_list = o.ssd_list_file
+            if ssd_list is None and o.ssds:
+                ssd_list = work / "ssds.txt"
+                ssd_list.write_text("\n".join(o.ssds) + "\n", encoding="ascii")
+            prefix = work / "result"
+            argv = self._argv(query_file, prefix, topk, ef_search, policy, ssd_list, extra_args)
+            with subprocess.Popen(argv, env=self._environment(), stdout=subprocess.PIPE,
+                                  stderr=subprocess.PIPE, text=True) as proc:
+                try:
+                    out, err = proc.communicate(timeout=timeout)
+                except subprocess.TimeoutExpired:
+                    proc.kill()
+                    proc.communicate()
+                    raise QuiverError(f"quiver_search exceeded the {timeout:g} second timeout") from None
+            if proc.returncode != 0:
+                detail = err.strip() or out.strip()
+                raise QuiverError(f"quiver_search exited with code {proc.returncode}: {detail}")
+            ids = read_matrix(work / "result_ids.bin", "i4")
+            dists = read_matrix(work / "result_distances.bin", "f4")
+        want = (queries.shape[0], topk)
+        if ids.shape != want or dists.shape != want:
+            raise QuiverError(f"unexpected result shape: ids={ids.shape}, distances={dists.shape}, "
+                              f"expected={want}")
+        return ids, dists
+
+    def close(self) -> None:
+        pass
+
+
+def _external_engine_path(binary: str | os.PathLike[str] | None) -> Path | None:
+    """The external engine named by `binary` or QUIVER_BINARY; None selects
+    the in-process engine.  A named path that is not an executable file is an
+    error."""
+    named = binary or os.environ.get("QUIVER_BINARY")
+    if not named:
+        return None
+    path = Path(named).expanduser().resolve()
+    if not (path.is_file() and os.access(path, os.X_OK)):
+        raise QuiverError(f"quiver_search executable not found (searched: {Path(named).expanduser()})")
+    return path
 
 
 class IndexQuiver:
     """Search a Quiver index with NumPy arrays.
 
-    Argument meaning, defaults and errors follow the reference binding.  The
-    in-process engine keeps the graph, vectors and PQ codes resident in GPU
-    memory (the heap memory backend); SSD options are accepted for
-    compatibility but the SPDK backend is not part of this library, so a search
-    with SSDs configured raises ``QuiverError`` unless an external ``binary``
-    is used.
+    The default engine keeps the graph, vectors and PQ codes resident in GPU
+    memory (the heap memory backend, or the mmap one).  SSD options are
+    accepted for compatibility; the SPDK backend is not part of this library,
+    so searching with SSDs configured raises ``QuiverError`` unless an
+    external ``binary`` is used.  Extra keyword arguments beyond the
+    reference's: ``device``, ``graph_placement`` ("hbm" or "host") and
+    ``search_kernel`` ("auto", "lut" or "shared-pivots").
     """
 
     def __init__(
@@ -63,65 +247,71 @@ class IndexQuiver:
         graph_placement: str = "hbm",
         search_kernel: str = "auto",
     ) -> None:
-        self.index_dir = Path(index_dir).expanduser().resolve()
-        if not self.index_dir.is_dir():
-            raise ValueError(f"index_dir is not a directory: {self.index_dir}")
+        root = Path(index_dir).expanduser().resolve()
+        if not root.is_dir():
+            raise ValueError(f"index_dir is not a directory: {root}")
+        self.index_dir = root
 
-        normalized_type = data_type.lower()
-        if normalized_type not in _DATA_TYPES:
+        canonical = _TYPE_ALIASES.get(data_type.lower(), data_type.lower())
+        if canonical not in _ELEMENTS:
             raise ValueError("data_type must be float32, float, uint8, or int8")
-        self.data_type = "float" if normalized_type == "float32" else normalized_type
-        self._numpy_dtype, self._query_suffix = _DATA_TYPES[normalized_type]
+        self.data_type = canonical
+        dtype, self._query_suffix = _ELEMENTS[canonical]
+        self._numpy_dtype = np.dtype(dtype)
 
         if ssds and ssd_list_file:
             raise ValueError("pass either ssds or ssd_list_file, not both")
-        self.ssds = tuple(str(ssd).strip() for ssd in (ssds or ()))
-        if any(not ssd for ssd in self.ssds):
+        self.ssds = tuple(str(s).strip() for s in ssds or ())
+        if "" in self.ssds:
             raise ValueError("SSD PCI addresses must not be empty")
-        self.ssd_list_file = (
-            Path(ssd_list_file).expanduser().resolve() if ssd_list_file else None
-        )
-        if self.ssd_list_file and not self.ssd_list_file.is_file():
+        self.ssd_list_file = Path(ssd_list_file).expanduser().resolve() if ssd_list_file else None
+        if self.ssd_list_file is not None and not self.ssd_list_file.is_file():
             raise ValueError(f"ssd_list_file does not exist: {self.ssd_list_file}")
         if spdk_base_lba is not None and spdk_base_lba < 0:
             raise ValueError("spdk_base_lba must be non-negative")
         self.spdk_base_lba = spdk_base_lba
 
-        if memory_backend not in {"heap", "mmap"}:
+        if memory_backend not in ("heap", "mmap"):
             raise ValueError("memory_backend must be heap or mmap")
         self.memory_backend = memory_backend
-        if graph_placement not in {"hbm", "host"}:
+        if graph_placement not in ("hbm", "host"):
             raise ValueError("graph_placement must be hbm or host")
         self.graph_placement = graph_placement
         if search_kernel not in _lib.KERNEL_NAMES:
             raise ValueError("search_kernel must be auto, lut or shared-pivots")
         self.search_kernel = search_kernel
-        self.binary = self._find_binary(binary)
-        self.num_blocks = self._positive(num_blocks, "num_blocks")
-        self.queries_per_block = self._positive(queries_per_block, "queries_per_block")
-        self.pipe_width = self._positive(pipe_width, "pipe_width")
-        self.poll_threads = self._positive(poll_threads, "poll_threads")
-        self.runners_per_ssd = self._positive(runners_per_ssd, "runners_per_ssd")
+
+        external = _external_engine_path(binary)
+        self._knobs = _EngineKnobs(
+            num_blocks=_positive("num_blocks", num_blocks),
+            queries_per_block=_positive("queries_per_block", queries_per_block),
+            pipe_width=_positive("pipe_width", pipe_width),
+            poll_threads=_positive("poll_threads", poll_threads),
+            runners_per_ssd=_positive("runners_per_ssd", runners_per_ssd),
+        )
         self.env = dict(env or {})
         self.device = int(device)
-        self._handle: C.c_void_p | None = None
         self.last_report: dict | None = None
-        if self.binary is None:
-            _lib.load()
+        self._engine = (_ProcessEngine(self, external) if external is not None
+                        else _LibraryEngine(self, self.device, graph_placement, search_kernel))
+
+    # the engine knobs, readable as attributes like the reference's
+    num_blocks = property(lambda self: self._knobs.num_blocks)
+    queries_per_block = property(lambda self: self._knobs.queries_per_block)
+    pipe_width = property(lambda self: self._knobs.pipe_width)
+    poll_threads = property(lambda self: self._knobs.poll_threads)
+    runners_per_ssd = property(lambda self: self._knobs.runners_per_ssd)
+
+    @property
+    def binary(self) -> Path | None:
+        """The external engine's path, or None for the in-process engine."""
+        return self._engine.executable if isinstance(self._engine, _ProcessEngine) else None
 
     @property
     def num_ssds(self) -> int:
         if self.ssds:
             return len(self.ssds)
-        if not self.ssd_list_file:
-            return 0
-        return len(
-            [
-                line
-                for line in self.ssd_list_file.read_text().splitlines()
-                if line.strip() and not line.lstrip().startswith("#")
-            ]
-        )
+        return _count_ssds(self.ssd_list_file) if self.ssd_list_file else 0
 
     def search(
         self,
@@ -134,96 +324,42 @@ class IndexQuiver:
         extra_args: Sequence[str] = (),
     ) -> tuple[npt.NDArray[np.int32], npt.NDArray[np.float32]]:
         """Return ``(ids, distances)`` with shape ``(len(queries), topk)``."""
-        topk = self._positive(topk, "topk")
-        ef_search = self._positive(ef_search, "ef_search")
-        if early_exit_policy not in {"gpruning", "none"}:
+        topk = _positive("topk", topk)
+        ef_search = _positive("ef_search", ef_search)
+        if early_exit_policy not in _POLICIES:
             raise ValueError("early_exit_policy must be gpruning or none")
         if timeout is not None and timeout <= 0:
             raise ValueError("timeout must be positive")
-
-        array = np.asarray(queries)
-        if array.ndim == 1:
-            array = array.reshape(1, -1)
-        if array.ndim != 2 or array.shape[0] == 0 or array.shape[1] == 0:
+        batch = np.asarray(queries)
+        if batch.ndim == 1:
+            batch = batch[np.newaxis, :]
+        if batch.ndim != 2 or 0 in batch.shape:
             raise ValueError("queries must be a non-empty 1D or 2D array")
-        array = np.ascontiguousarray(array, dtype=self._numpy_dtype)
+        batch = np.ascontiguousarray(batch, dtype=self._numpy_dtype)
+        return self._engine.search(batch, topk, ef_search, early_exit_policy, timeout, extra_args)
 
-        if self.binary is not None:
-            return self._search_subprocess(array, topk, ef_search, early_exit_policy, timeout, extra_args)
-        return self._search_inprocess(array, topk, ef_search, early_exit_policy, timeout, extra_args)
-
-    # ---- in-process engine (C ABI) ---------------------------------------
-    def _open(self) -> C.c_void_p:
-        if self._handle is None:
-            lib = _lib.load()
-            h = C.c_void_p()
-            _lib.check(
-                lib.qv_index_open_ex(
-                    str(self.index_dir).encode(),
-                    self.data_type.encode(),
-                    self.memory_backend.encode(),
-                    None,
-                    self.device,
-                    _lib.QV_GRAPH_HOST if self.graph_placement == "host" else _lib.QV_GRAPH_HBM,
-                    C.byref(h),
-                )
-            )
-            self._handle = h
-        return self._handle
+    # ---- in-process engine only -----------------------------------------
+    def _library(self) -> _LibraryEngine:
+        if not isinstance(self._engine, _LibraryEngine):
+            raise QuiverError("this IndexQuiver runs an external quiver_search binary")
+        return self._engine
 
     def info(self) -> dict:
+        """Layout and placement of the opened index (qv_index_get_info)."""
         info = _lib.IndexInfo()
-        _lib.check(_lib.load().qv_index_get_info(self._open(), C.byref(info)))
+        _lib.check(_lib.load().qv_index_get_info(self._library().handle(), C.byref(info)))
         return {name: getattr(info, name) for name, _ in info._fields_}
-
-    def _search_inprocess(self, array, topk, ef_search, early_exit_policy, timeout, extra_args):
-        extra = [str(x) for x in extra_args]
-        skip_nav = "--skip-nav" in extra
-        extra = [x for x in extra if x != "--skip-nav"]
-        if extra:
-            raise QuiverError("extra_args other than --skip-nav need an external quiver_search binary")
-        if self.num_ssds:
-            raise QuiverError("This binary was built without SPDK support")
-        handle = self._open()
-        q = np.ascontiguousarray(array, dtype=np.float32)
-        n, d = q.shape
-        ids = np.empty((n, topk), dtype=np.int32)
-        dists = np.empty((n, topk), dtype=np.float32)
-        found = np.empty((n,), dtype=np.int32)
-        opts = _lib.default_search_opts()
-        opts.num_blocks = self.num_blocks
-        opts.queries_per_block = self.queries_per_block
-        opts.pipe_width = self.pipe_width
-        opts.early_exit = _lib.QV_EXIT_GPRUNING if early_exit_policy == "gpruning" else _lib.QV_EXIT_NONE
-        env = {**os.environ, **self.env}
-        if "QUIVER_PREFEED" in env:
-            opts.prefeed = int(env["QUIVER_PREFEED"])
-        if "QUIVER_ADMIT_MIN_BATCH" in env:
-            opts.admit_min_batch = max(1, int(env["QUIVER_ADMIT_MIN_BATCH"]))
-        opts.timeout_s = float(timeout) if timeout is not None else 0.0
-        opts.skip_nav = 1 if skip_nav else 0
-        opts.kernel = _lib.KERNEL_NAMES[self.search_kernel]
-        rep = _lib.SearchReport()
-        rc = _lib.load().qv_search(
-            handle, q.ctypes.data, n, d, topk, ef_search, C.byref(opts),
-            ids.ctypes.data, dists.ctypes.data, found.ctypes.data, C.byref(rep),
-        )
-        if rc == _lib.QV_ETIMEDOUT:
-            raise QuiverError(f"quiver_search exceeded the {timeout:g} second timeout")
-        _lib.check(rc)
-        self.last_report = rep.as_dict()
-        return ids, dists
 
     def load_nav(self, nav_dir: str | os.PathLike[str]) -> None:
         """Load (or replace) the navigation graph that picks each query's entry
         node (nav_index, nav_index.data, map.txt).  An index directory holding
         nav_index or nav/nav_index gets its graph at open without this call."""
-        _lib.check(_lib.load().qv_index_load_nav(self._open(), str(nav_dir).encode()))
+        _lib.check(_lib.load().qv_index_load_nav(self._library().handle(), str(nav_dir).encode()))
 
     def close(self) -> None:
-        if self._handle is not None:
-            _lib.load().qv_index_close(self._handle)
-            self._handle = None
+        engine = getattr(self, "_engine", None)
+        if engine is not None:
+            engine.close()
 
     def __enter__(self) -> "IndexQuiver":
         return self
@@ -237,118 +373,8 @@ class IndexQuiver:
         except Exception:
             pass
 
-    # ---- external engine (reference command line) ------------------------
-    def _search_subprocess(self, array, topk, ef_search, early_exit_policy, timeout, extra_args):
-        with tempfile.TemporaryDirectory(prefix="quiver-python-") as temp_dir:
-            work = Path(temp_dir)
-            query_path = work / f"queries{self._query_suffix}"
-            result_prefix = work / "result"
-            self._write_bin(query_path, array)
-            ssd_list = self._materialize_ssd_list(work)
 
-            command = [
-                str(self.binary),
-                "--index-dir", str(self.index_dir),
-                "--query", str(query_path),
-                "--data-type", self.data_type,
-                "--topk", str(topk),
-                "--ef-search", str(ef_search),
-                "--repeat", "1",
-                "--num-blocks", str(self.num_blocks),
-                "--queries-per-block", str(self.queries_per_block),
-                "--pipe-width", str(self.pipe_width),
-                "--poll-threads", str(self.poll_threads),
-                "--runners-per-ssd", str(self.runners_per_ssd),
-                "--memory-backend", self.memory_backend,
-                "--early-exit-policy", early_exit_policy,
-                "--result-prefix", str(result_prefix),
-            ]
-            if ssd_list is not None:
-                command.extend(["--ssd-list-file", str(ssd_list)])
-            command.extend(str(arg) for arg in extra_args)
-
-            process_env = os.environ.copy()
-            process_env.update(self.env)
-            if self.spdk_base_lba is not None:
-                process_env["SPDK_BASE_LBA"] = str(self.spdk_base_lba)
-            try:
-                completed = subprocess.run(
-                    command, env=process_env, text=True, capture_output=True,
-                    check=False, timeout=timeout,
-                )
-            except subprocess.TimeoutExpired as error:
-                raise QuiverError(f"quiver_search exceeded the {timeout:g} second timeout") from error
-            if completed.returncode != 0:
-                detail = completed.stderr.strip() or completed.stdout.strip()
-                raise QuiverError(f"quiver_search exited with code {completed.returncode}: {detail}")
-
-            ids = self._read_bin(result_prefix.with_name("result_ids.bin"), np.int32)
-            distances = self._read_bin(result_prefix.with_name("result_distances.bin"), np.float32)
-            expected = (array.shape[0], topk)
-            if ids.shape != expected or distances.shape != expected:
-                raise QuiverError(
-                    f"unexpected result shape: ids={ids.shape}, "
-                    f"distances={distances.shape}, expected={expected}"
-                )
-            return ids, distances
-
-    def _materialize_ssd_list(self, work: Path) -> Path | None:
-        if self.ssd_list_file:
-            return self.ssd_list_file
-        if not self.ssds:
-            return None
-        path = work / "ssds.txt"
-        path.write_text("".join(f"{ssd}\n" for ssd in self.ssds), encoding="ascii")
-        return path
-
-    @staticmethod
-    def _write_bin(path: Path, values: npt.NDArray[np.generic]) -> None:
-        with path.open("wb") as output:
-            output.write(struct.pack("<ii", values.shape[0], values.shape[1]))
-            output.write(values.tobytes(order="C"))
-
-    @staticmethod
-    def _read_bin(path: Path, dtype: npt.DTypeLike) -> npt.NDArray[np.generic]:
-        if not path.is_file():
-            raise QuiverError(f"quiver_search did not create {path.name}")
-        with path.open("rb") as source:
-            header = source.read(8)
-            if len(header) != 8:
-                raise QuiverError(f"invalid result header in {path}")
-            count, dims = struct.unpack("<ii", header)
-            if count < 0 or dims < 0:
-                raise QuiverError(f"invalid result dimensions in {path}")
-            values = np.fromfile(source, dtype=np.dtype(dtype).newbyteorder("<"))
-        if values.size != count * dims:
-            raise QuiverError(f"truncated result data in {path}")
-        return values.reshape(count, dims)
-
-    @staticmethod
-    def _positive(value: int, name: str) -> int:
-        value = int(value)
-        if value <= 0:
-            raise ValueError(f"{name} must be positive")
-        return value
-
-    @staticmethod
-    def _find_binary(binary: str | os.PathLike[str] | None) -> Path | None:
-        """External engine path, or None for the in-process C-ABI engine."""
-        candidates: list[Path] = []
-        if binary:
-            candidates.append(Path(binary).expanduser())
-        elif os.environ.get("QUIVER_BINARY"):
-            candidates.append(Path(os.environ["QUIVER_BINARY"]).expanduser())
-        else:
-            return None
-        for candidate in candidates:
-            resolved = candidate.resolve()
-            if resolved.is_file() and os.access(resolved, os.X_OK):
-                return resolved
-        searched = ", ".join(str(path) for path in candidates) or "PATH"
-        raise QuiverError(f"quiver_search executable not found (searched: {searched})")
-
-
-# ---- helpers around the C ABI ---------------------------------------------
+# ---- index construction and synthetic data (C ABI) ------------------------
 
 def build_index(
     base: npt.ArrayLike,
