@@ -444,6 +444,12 @@ int64_t qvo_nav_entry(const qvo_nav* nav, const float* q, int64_t fallback) {
 int qvo_search_one(const qvo_index* ix, const float* q, const qvo_search_params* p,
                    int32_t* out_ids, float* out_dists, int32_t* out_found,
                    int32_t* out_hops) {
+  return qvo_search_trace(ix, q, p, out_ids, out_dists, out_found, out_hops, NULL, 0);
+}
+
+int qvo_search_trace(const qvo_index* ix, const float* q, const qvo_search_params* p,
+                     int32_t* out_ids, float* out_dists, int32_t* out_found,
+                     int32_t* out_hops, int32_t* trace, int trace_cap) {
   if (p->topk <= 0 || p->ef_search <= 0 || p->pipe_width < 1 || p->pipe_width > 16)
     return QVO_EINVAL;
   const int W = p->pipe_width;
@@ -490,6 +496,7 @@ int qvo_search_one(const qvo_index* ix, const float* q, const qvo_search_params*
   rc = merge_data(ix, &s, lut, entry);
   if (rc != QVO_OK) goto done;
   lane_req[0] = visit_select(ix, &s, q_used, entry);
+  if (trace && trace_cap > 0) trace[0] = (int32_t)entry;
   step = 1;
   if (gpruning_step(p, &s, &g, step)) {
     stop = 1;
@@ -514,6 +521,7 @@ int qvo_search_one(const qvo_index* ix, const float* q, const qvo_search_params*
       rc = merge_data(ix, &s, lut, lane_node[w]);
       if (rc != QVO_OK) goto done;
       lane_req[w] = visit_select(ix, &s, q_used, lane_node[w]);
+      if (trace && step < trace_cap) trace[step] = lane_node[w];
       ++step;
       if (gpruning_step(p, &s, &g, step)) {
         stop = 1;

@@ -117,6 +117,11 @@ float qvo_exact_l2(const float* q, const void* x, int dtype, int dim);
  * keys inside one adjacency list (outside the reference's domain). */
 int qvo_search_one(const qvo_index* ix, const float* q, const qvo_search_params* p,
                    int32_t* ids, float* dists, int32_t* found, int32_t* hops);
+/* qvo_search_one that also writes the node expanded at each step (trace[s] for
+ * step s + 1, the first trace_cap steps; the entry is step 1). */
+int qvo_search_trace(const qvo_index* ix, const float* q, const qvo_search_params* p,
+                     int32_t* ids, float* dists, int32_t* found, int32_t* hops,
+                     int32_t* trace, int trace_cap);
 
 /* All queries, OpenMP over queries with `threads` threads (<=0: all cores).
  * Returns the first non-OK status, else QVO_OK. */

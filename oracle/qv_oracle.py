@@ -88,6 +88,8 @@ def load() -> C.CDLL:
     lib.qvo_exact_l2.restype = C.c_float
     lib.qvo_search_one.argtypes = [C.POINTER(OracleIndex), P, C.POINTER(SearchParams), P, P, P, P]
     lib.qvo_search_one.restype = C.c_int
+    lib.qvo_search_trace.argtypes = [C.POINTER(OracleIndex), P, C.POINTER(SearchParams), P, P, P, P, P, C.c_int]
+    lib.qvo_search_trace.restype = C.c_int
     lib.qvo_search.argtypes = [C.POINTER(OracleIndex), P, C.c_int64, C.POINTER(SearchParams), C.c_int,
                                P, P, P, P]
     lib.qvo_search.restype = C.c_int
@@ -290,6 +292,27 @@ def search(ix: HostIndex, queries: np.ndarray, topk: int, ef: int, *, pipe_width
     if rc != 0:
         raise RuntimeError(f"oracle search failed with status {rc}")
     return ids, dists, found, hops
+
+
+def search_trace(ix: HostIndex, query: np.ndarray, topk: int, ef: int, *, pipe_width: int = 1,
+                 early_exit: int = EXIT_NONE, warmup: int = 10, patience: int = 8, cap: int = 4096):
+    """One query; returns (ids, dists, found, hops, expanded) where expanded[s]
+    is the node expanded at step s + 1 (the entry first)."""
+    lib = load()
+    q = np.ascontiguousarray(query, dtype=np.float32).reshape(-1)
+    ids = np.empty(topk, np.int32)
+    dists = np.empty(topk, np.float32)
+    found = np.empty(1, np.int32)
+    hops = np.empty(1, np.int32)
+    trace = np.full(cap, -1, np.int32)
+    p = SearchParams(topk, ef, pipe_width, early_exit, warmup, patience, None)
+    cs = ix.c_struct()
+    rc = lib.qvo_search_trace(C.byref(cs), _ptr(q), C.byref(p), _ptr(ids), _ptr(dists), _ptr(found),
+                              _ptr(hops), _ptr(trace), cap)
+    if rc != 0:
+        raise RuntimeError(f"oracle search failed with status {rc}")
+    h = int(hops[0])
+    return ids, dists, int(found[0]), h, [int(v) for v in trace[:min(h, cap)]]
 
 
 def lut(dim: int, centroid: np.ndarray, pivots_t: np.ndarray, chunk_id: np.ndarray,
