@@ -1464,7 +1464,18 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
           timed_out = true;
           break;
         }
-        if (hipStreamQuery(ix->stream) == hipSuccess) break;  // kernel ended early (error path)
+        if (hipStreamQuery(ix->stream) == hipSuccess) {
+          // The kernel has ended: every completion it published is visible
+          // now, including those written after the empty read above.
+          const auto now = clock::now();
+          while (done < nq) {
+            const int32_t e = __atomic_load_n(ix->h_ring + done, __ATOMIC_ACQUIRE);
+            if (e == 0) break;
+            lat_ms[(size_t)(e - 1)] = std::chrono::duration<double, std::milli>(now - admit[(size_t)(e - 1)]).count();
+            done++;
+          }
+          if (done < nq) break;  // it ended early (error path): nothing more will arrive
+        }
       }
     }
   }

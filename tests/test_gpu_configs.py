@@ -1,0 +1,177 @@
+"""The HIP path against the oracle at the benchmark shape (runs on the MI355X).
+
+Workload: 1M uint8 vectors of dimension 128 from the seeded mixture (1024
+centres in [32, 224], sigma 20), a Vamana graph R=64 / L=100 / alpha=1.2 with
+PQ 32x256 built on the GPU -- the shape every quoted throughput number uses
+(node records of 388 B, 10 per page, 32-byte code rows, all 64 neighbour lanes
+of a wave in use).  2000 queries from the same mixture, top-10.
+
+For every case ids, distances, found counts and hop counts must equal the
+oracle's (deterministic mode: pipe width 1 unless stated, one query per wave),
+and Recall@10 against the GPU brute force must be within 0.002 of the
+oracle's.  Also covered: the latency mode (open-loop batches of 1, 16 and 256
+queries, streaming admission, automatic kernel choice) and the host-forced
+give-up path (a deadline that fires mid-batch, then a search on the same handle).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import qv_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+N, DIM, NQ, K = 1_000_000, 128, 2000, 10
+KERNEL = {"lut": 1, "shared-pivots": 2, "auto": 0}
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def c1():
+    from quiver import _lib
+
+    if _lib.device_count() == 0:
+        pytest.skip("no GPU")
+    L = _lib.load()
+    _say("[gpu] C1: 1M x 128 u8 mixture, GPU build R=64 L=100 alpha=1.2 PQ 32x256")
+    mix = _lib.Mixture(0x5EED_0001, 1024, DIM, _lib.QV_UINT8, 32.0, 224.0, 20.0, 1)
+    d_base = _lib.DeviceBuffer(N * DIM)
+    _lib.check(L.qv_mixture_fill_device(C.byref(mix), 0, N, d_base.ptr, 0))
+    q = np.empty((NQ + 8000, DIM), np.uint8)  # the last 8000 only feed the give-up test
+    _lib.check(L.qv_mixture_fill_host(C.byref(mix), 1 << 40, q.shape[0], q.ctypes.data))
+    qf = q.astype(np.float32)
+    p = _lib.default_build_params()
+    p.R, p.L, p.alpha, p.num_chunks, p.kmeans_iters, p.passes = 64, 100, 1.2, 32, 15, 2
+    h = C.c_void_p()
+    _lib.check(L.qv_build_index_gpu(d_base.ptr, _lib.QV_UINT8, N, DIM, C.byref(p), 0, C.byref(h)))
+    info = _lib.IndexInfo()
+    _lib.check(L.qv_index_get_info(h, C.byref(info)))
+    assert (info.max_m0, info.node_size, info.nodes_per_page, info.num_chunks) == (64, 388, 10, 32)
+    d_q = _lib.DeviceBuffer(NQ * DIM * 4).upload(qf[:NQ])
+    d_gi, d_gd = _lib.DeviceBuffer(NQ * K * 4), _lib.DeviceBuffer(NQ * K * 4)
+    _lib.check(L.qv_ground_truth(d_base.ptr, _lib.QV_UINT8, N, DIM, d_q.ptr, NQ, K, d_gi.ptr, d_gd.ptr, 0))
+    gt = d_gi.download(np.int32, (NQ, K))
+    d_base.close()
+    pages = np.empty(info.num_pages * 4096, np.uint8)
+    codes = np.empty((N, 32), np.uint8)
+    centroid = np.empty(DIM, np.float32)
+    pivots = np.empty((256, DIM), np.float32)
+    offs = np.empty(33, np.int32)
+    _lib.check(L.qv_index_copy_out(h, pages.ctypes.data, codes.ctypes.data, centroid.ctypes.data,
+                                   pivots.ctypes.data, offs.ctypes.data))
+    host = O.HostIndex.from_arrays(O.UINT8, DIM, N, 64, int(info.enter_point), pages, codes, centroid,
+                                   pivots, offs)
+    degs = pages.reshape(-1, 4096)[:, :3880].reshape(-1, 10, 388)[:, :, 128:132].copy().view(np.uint32).ravel()[:N]
+    assert degs.max() <= 64 and degs.mean() > 30, "the R=64 graph must fill most neighbour lanes"
+    yield {"lib": _lib, "L": L, "h": h, "q": qf, "gt": gt, "host": host, "cache": {}}
+    L.qv_index_close(h)
+
+
+def _search(c, queries, ef, policy, kernel="auto", pipe=1, num_blocks=0, timeout=0.0):
+    lib, L = c["lib"], c["L"]
+    n = queries.shape[0]
+    ids = np.empty((n, K), np.int32)
+    dists = np.empty((n, K), np.float32)
+    found = np.empty(n, np.int32)
+    o = lib.default_search_opts()
+    o.early_exit = lib.QV_EXIT_GPRUNING if policy == "gpruning" else lib.QV_EXIT_NONE
+    o.pipe_width = pipe
+    o.kernel = KERNEL[kernel]
+    o.num_blocks = num_blocks
+    o.timeout_s = timeout
+    rep = lib.SearchReport()
+    q = np.ascontiguousarray(queries, np.float32)
+    rc = L.qv_search(c["h"], q.ctypes.data, n, DIM, K, ef, C.byref(o), ids.ctypes.data, dists.ctypes.data,
+                     found.ctypes.data, C.byref(rep))
+    if rc != 0:
+        return rc, None
+    hops = np.empty(n, np.int32)
+    lib.check(L.qv_last_hops(c["h"], hops.ctypes.data, n))
+    return rc, (ids, dists, found, hops, rep)
+
+
+def _oracle(c, ef, policy, pipe=1, n=NQ):
+    key = (ef, policy, pipe, n)
+    if key not in c["cache"]:
+        c["cache"][key] = O.search(c["host"], c["q"][:n], K, ef, pipe_width=pipe,
+                                   early_exit=O.EXIT_GPRUNING if policy == "gpruning" else O.EXIT_NONE)
+    return c["cache"][key]
+
+
+def _same(got, want, what):
+    ids, dists, found, hops = got[:4]
+    oids, odists, ofound, ohops = want
+    bad = np.nonzero(np.any(ids != oids, axis=1))[0]
+    assert bad.size == 0, f"{what}: {bad.size} queries with other ids, first {bad[:5]}"
+    np.testing.assert_array_equal(dists, odists, err_msg=what)
+    np.testing.assert_array_equal(found, ofound, err_msg=what)
+    np.testing.assert_array_equal(hops, ohops, err_msg=what)
+
+
+@pytest.mark.parametrize("kernel", ["lut", "shared-pivots"])
+@pytest.mark.parametrize("policy", ["none", "gpruning"])
+@pytest.mark.parametrize("ef", [45, 64, 128, 240, 288])
+def test_c1_matches_oracle(c1, kernel, policy, ef):
+    _say(f"[gpu] C1 kernel={kernel} policy={policy} ef={ef}")
+    rc, got = _search(c1, c1["q"][:NQ], ef, policy, kernel)
+    assert rc == 0, c1["lib"].load().qv_last_error()
+    assert got[4].kernel == KERNEL[kernel]
+    want = _oracle(c1, ef, policy)
+    _same(got, want, f"{kernel} {policy} ef={ef}")
+    r_gpu, r_ora = O.recall(got[0], c1["gt"], K), O.recall(want[0], c1["gt"], K)
+    assert abs(r_gpu - r_ora) <= 0.002
+    if policy == "none" and ef >= 240:
+        assert r_gpu >= 0.90, f"Recall@10 {r_gpu:.4f} at ef={ef}"
+
+
+@pytest.mark.parametrize("pipe", [2, 4])
+def test_c1_pipe_lanes_match_oracle(c1, pipe):
+    _say(f"[gpu] C1 pipe_width={pipe}")
+    for kernel in ("lut", "shared-pivots"):
+        rc, got = _search(c1, c1["q"][:500], 128, "gpruning", kernel, pipe=pipe)
+        assert rc == 0
+        _same(got, _oracle(c1, 128, "gpruning", pipe=pipe, n=500), f"{kernel} W={pipe}")
+
+
+@pytest.mark.parametrize("batch", [1, 16, 256])
+def test_c1_latency_mode_batches(c1, batch):
+    """Open-loop arrival at a fixed batch size: each batch is one qv_search
+    call (streaming admission, automatic kernel); answers do not depend on
+    how queries are batched."""
+    n = 200 if batch == 1 else 1024
+    _say(f"[gpu] C1 latency mode batch={batch} queries={n}")
+    ids = np.empty((n, K), np.int32)
+    dists = np.empty((n, K), np.float32)
+    found = np.empty(n, np.int32)
+    hops = np.empty(n, np.int32)
+    for s in range(0, n, batch):
+        rc, got = _search(c1, c1["q"][s:s + batch], 240, "none", "auto")
+        assert rc == 0
+        ids[s:s + batch], dists[s:s + batch], found[s:s + batch], hops[s:s + batch] = got[:4]
+        assert got[4].lat_max_ms > 0
+    want = tuple(a[:n] for a in _oracle(c1, 240, "none"))
+    _same((ids, dists, found, hops), want, f"batch {batch}")
+
+
+def test_deadline_gives_up_then_next_search_is_exact(c1):
+    """A deadline that fires mid-batch: qv_search returns QV_ETIMEDOUT once
+    the host has raised the terminate word and every wave has left on its own;
+    the handle stays usable, and the per-query-LUT kernel's membership bitmaps
+    (left dirty by the unfinished queries) are cleared before the next launch."""
+    lib = c1["lib"]
+    _say("[gpu] deadline: 10k queries, ef=448, 32 query slots, 5 ms limit")
+    for kernel in ("lut", "shared-pivots"):
+        rc, _ = _search(c1, c1["q"], 448, "none", kernel, num_blocks=32, timeout=0.005)
+        assert rc == lib.QV_ETIMEDOUT, (kernel, rc)
+        assert "timeout" in lib.load().qv_last_error().decode()
+        rc, got = _search(c1, c1["q"][:NQ], 128, "none", "lut")
+        assert rc == 0
+        _same(got, _oracle(c1, 128, "none"), f"LUT kernel after a {kernel} give-up")
