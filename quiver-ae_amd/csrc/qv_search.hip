@@ -830,6 +830,49 @@ LaunchShape shape_launch(const LaunchPlan& lp, int64_t slots, int num_cus) {
   return sh;
 }
 
+// ---- scratch of the allocation-free search entry point (qv_search_noalloc) --
+// One fixed array per device, held from module load to process end:
+//   [0, 256)                     dispatch counters (ticket, done, error bits)
+//   [256, +4 kNoAllocMaxQueries) per-query hop counts
+//   [.., +4 kNoAllocMaxQueries)  per-query ADC evaluation counts
+//   [kNoAllocBitsOff, end)       beam-membership bitmaps of the per-query-LUT
+//                                kernel (zero between queries, as ensure_bits'),
+//                                as many query slots as fit
+// Host code never uses the symbol's name as an address: each device's copy is
+// looked up once with hipGetSymbolAddress.
+constexpr int64_t kNoAllocBytes = QV_NOALLOC_SCRATCH_BYTES;
+constexpr int64_t kNoAllocMaxQueries = QV_NOALLOC_MAX_QUERIES;
+constexpr int64_t kNoAllocHopsOff = 256;
+constexpr int64_t kNoAllocEvalsOff = kNoAllocHopsOff + 4 * kNoAllocMaxQueries;
+constexpr int64_t kNoAllocBitsOff = kNoAllocEvalsOff + 4 * kNoAllocMaxQueries;
+static_assert(kNoAllocBitsOff < kNoAllocBytes, "no room for bitmaps");
+__device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
+// Zero fill by vector stores (no hipMemsetAsync: a caller may capture the
+// stream into a graph, where memset nodes are avoided).
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t words) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+// totals[0] += sum of hops, totals[1] += sum of evals (64-bit).
+__global__ __launch_bounds__(256) void sum_counts_kernel(const int32_t* hops, const int32_t* evals, int64_t n,
+                                                         unsigned long long* totals) {
+  unsigned long long h = 0, e = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    h += (unsigned long long)hops[i];
+    e += (unsigned long long)evals[i];
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    h += shfl_xor64(h, off);
+    e += shfl_xor64(e, off);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicAdd(&totals[0], h);
+    atomicAdd(&totals[1], e);
+  }
+}
+
 }  // namespace
 
 // ============================================================== host side ===
@@ -1572,6 +1615,164 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   }
 }
 
+// ---- allocation-free search -------------------------------------------------
+// Per device: the address of its copy of `scratch` (hipGetSymbolAddress, once,
+// with the device current) and whether its bitmap region is known to be zero.
+struct NoAllocDevice {
+  uint8_t* ptr = nullptr;
+  bool bits_clean = false;
+};
+static std::mutex g_noalloc_mu;
+static NoAllocDevice g_noalloc[64];
+
+static NoAllocDevice& noalloc_device(int device) {
+  if (device < 0 || device >= 64) fail(QV_EINVAL, "device out of range");
+  NoAllocDevice& nd = g_noalloc[device];
+  if (!nd.ptr) {
+    void* p = nullptr;
+    HIP_OK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) fail(QV_EHIP, "hipGetSymbolAddress returned no address for the search scratch");
+    nd.ptr = static_cast<uint8_t*>(p);
+  }
+  return nd;
+}
+
+static void zero_words(uint8_t* p, int64_t bytes, hipStream_t s) {
+  const int64_t words = bytes / 4;
+  const int blocks = (int)std::min<int64_t>((words + 255) / 256, 4096);
+  hipLaunchKernelGGL(zero_words_kernel, dim3(blocks), dim3(256), 0, s, reinterpret_cast<uint32_t*>(p), words);
+  HIP_OK(hipGetLastError());
+}
+
+// qv_search with every query admitted at launch, device buffers only, and its
+// scratch taken from the fixed per-device array: no device or pinned-host
+// allocation, no memset.  The per-query-LUT kernel launches no more query
+// slots than the array's bitmap region holds (with the automatic choice the
+// shared-pivot kernel is taken instead when the index allows it).
+void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, int topk, int ef,
+                    const qv_search_opts& o, int32_t* d_ids, float* d_dists, int32_t* d_found,
+                    qv_search_report* rep) {
+  std::lock_guard<std::mutex> lk(ix->mu);
+  const Layout& L = ix->lay;
+  if (nq <= 0 || nq > kNoAllocMaxQueries)
+    fail(QV_EINVAL, "qv_search_noalloc takes 1 to " + std::to_string(kNoAllocMaxQueries) +
+                        " queries per call (its fixed scratch holds their counts); got " + std::to_string(nq));
+  if (dim != L.num_dims)
+    fail(QV_EINVAL, "Query dimension mismatch: queries have " + std::to_string(dim) +
+                        " dims, but the index expects " + std::to_string(L.num_dims));
+  if (topk <= 0 || topk > kMaxTopk) fail(QV_EINVAL, "topk must be in [1, 64]");
+  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 448]");
+  if (o.pipe_width < 1 || o.pipe_width > kMaxPipeWidth) fail(QV_EINVAL, "--pipe-width must be in [1, 16]");
+  if (o.queries_per_block < 1 || o.queries_per_block > kMaxQueriesPerBlock)
+    fail(QV_EINVAL, "--queries-per-block must be in [1, 8]");
+  if (o.early_exit != QV_EXIT_NONE && o.early_exit != QV_EXIT_GPRUNING)
+    fail(QV_EINVAL, "early exit policy must be none or gpruning");
+  if (o.num_blocks < 0) fail(QV_EINVAL, "--num-blocks must be positive");
+  if (o.timeout_s != 0.0) fail(QV_EINVAL, "qv_search_noalloc has no deadline (timeout_s must be 0)");
+  if (!d_queries || !d_ids || !d_dists) fail(QV_EINVAL, "null argument");
+
+  std::lock_guard<std::mutex> dlk(g_noalloc_mu);  // one device array: calls on one GPU are serialised here
+  HIP_OK(hipSetDevice(ix->device));
+  NoAllocDevice& nd = noalloc_device(ix->device);
+  uint8_t* const base = nd.ptr;
+  const int64_t requested = o.num_blocks > 0 ? (int64_t)o.num_blocks * o.queries_per_block : INT64_MAX;
+  LaunchPlan lp = launch_plan(ix, ef, o.kernel, std::min<int64_t>(nq, requested));
+  const int64_t bits_words = ((L.num_data + 31) / 32 + 15) / 16 * 16;
+  const int64_t bits_slots = (kNoAllocBytes - kNoAllocBitsOff) / (4 * bits_words);
+  const int64_t slots = (int64_t)(o.num_blocks > 0 ? o.num_blocks : lp.slots_per_cu * ix->num_cus) * o.queries_per_block;
+  int64_t launched = std::min<int64_t>(std::min<int64_t>(slots, (int64_t)lp.slots_per_cu * ix->num_cus), nq);
+  if (lp.variant == QV_KERNEL_LUT && launched > bits_slots && o.kernel == QV_KERNEL_AUTO) {
+    try {
+      LaunchPlan sp = launch_plan(ix, ef, QV_KERNEL_SHARED_PIVOTS, std::min<int64_t>(nq, requested));
+      lp = sp;
+      launched = std::min<int64_t>(std::min<int64_t>(slots, (int64_t)lp.slots_per_cu * ix->num_cus), nq);
+    } catch (const Error&) {
+      // the index takes only the per-query-LUT kernel: fewer slots below
+    }
+  }
+  if (lp.slots_per_cu <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
+  const bool use_bits = lp.variant == QV_KERNEL_LUT;
+  if (use_bits) {
+    if (bits_slots < 1)
+      fail(QV_EUNSUPPORTED, "index of " + std::to_string((long long)L.num_data) +
+                                " points: one query slot's membership bitmap (" + std::to_string(4 * bits_words) +
+                                " bytes) exceeds qv_search_noalloc's scratch (" +
+                                std::to_string(kNoAllocBytes - kNoAllocBitsOff) + " bytes)");
+    launched = std::min(launched, bits_slots);
+  }
+  const LaunchShape ls = shape_launch(lp, launched, ix->num_cus);
+
+  int32_t* const counters = reinterpret_cast<int32_t*>(base);
+  int32_t* const hops = reinterpret_cast<int32_t*>(base + kNoAllocHopsOff);
+  int32_t* const evals = reinterpret_cast<int32_t*>(base + kNoAllocEvalsOff);
+  uint32_t* const bits = reinterpret_cast<uint32_t*>(base + kNoAllocBitsOff);
+  zero_words(base, kNoAllocHopsOff, ix->stream);  // counters and the 64-bit totals
+  if (use_bits && !nd.bits_clean) zero_words(base + kNoAllocBitsOff, kNoAllocBytes - kNoAllocBitsOff, ix->stream);
+
+  SearchArgs a = base_args(ix);
+  a.queries = d_queries;
+  a.nq = (int32_t)nq;
+  a.topk = topk;
+  a.ef = ef;
+  a.pipe_w = o.pipe_width;
+  a.early_exit = o.early_exit;
+  if (o.skip_nav) a.nav_data = nullptr;
+  a.warmup = o.gpruning_warmup;
+  a.patience = o.gpruning_patience;
+  a.out_ids = d_ids;
+  a.out_dists = d_dists;
+  a.out_found = d_found;
+  a.out_hops = hops;
+  a.out_stopped = nullptr;
+  a.out_evals = evals;
+  a.t_start = nullptr;
+  a.t_end = nullptr;
+  a.counters = counters;
+  a.feed_count = nullptr;  // every query admitted at launch
+  a.terminate = nullptr;
+  a.ring = nullptr;
+  a.spin_limit_ticks = 0;
+  a.rec_ids = nullptr;
+  a.rec_dists = nullptr;
+  a.rec_cap = 0;
+  a.bits = use_bits ? bits : nullptr;
+  a.bits_words = use_bits ? bits_words : 0;
+
+  const auto t0 = std::chrono::steady_clock::now();
+  if (use_bits) nd.bits_clean = false;  // until every query is seen to finish
+  HIP_OK(hipEventRecord(ix->ev0, ix->stream));
+  hipLaunchKernelGGL(lp.kern, dim3(ls.grid), dim3(kWave * ls.waves), (size_t)ls.lds, ix->stream, a);
+  HIP_OK(hipGetLastError());
+  HIP_OK(hipEventRecord(ix->ev1, ix->stream));
+  unsigned long long* const totals = reinterpret_cast<unsigned long long*>(base + 64);
+  hipLaunchKernelGGL(sum_counts_kernel, dim3((unsigned)std::min<int64_t>((nq + 255) / 256, 1024)), dim3(256), 0,
+                     ix->stream, hops, evals, nq, totals);
+  HIP_OK(hipGetLastError());
+  HIP_OK(hipStreamSynchronize(ix->stream));
+  const auto t1 = std::chrono::steady_clock::now();
+  int32_t c[4] = {0, 0, 0, 0};
+  unsigned long long tot[2] = {0, 0};
+  HIP_OK(hipMemcpy(c, counters, sizeof(c), hipMemcpyDeviceToHost));
+  HIP_OK(hipMemcpy(tot, totals, sizeof(tot), hipMemcpyDeviceToHost));
+  if (use_bits) nd.bits_clean = c[1] >= std::min<int64_t>(c[0], nq);  // every started query cleared its bits
+  if (c[1] != nq)
+    fail(QV_EHIP, "search kernel finished " + std::to_string(c[1]) + " of " + std::to_string(nq) + " queries");
+  if (rep) {
+    std::memset(rep, 0, sizeof(*rep));
+    rep->search_time_s = std::chrono::duration<double>(t1 - t0).count();
+    rep->qps = (double)nq / rep->search_time_s;
+    float kms = 0.f;
+    HIP_OK(hipEventElapsedTime(&kms, ix->ev0, ix->ev1));
+    rep->kernel_ms = kms;
+    rep->num_blocks = ls.grid * ls.waves;
+    rep->max_inflight = (int32_t)nq;
+    rep->kernel = lp.variant;
+    rep->total_hops = (double)tot[0];
+    rep->total_evals = (double)tot[1];
+    rep->avg_hops = (double)tot[0] / (double)nq;
+  }
+}
+
 }  // namespace qv
 
 // ================================================================ C ABI ====
@@ -1691,6 +1892,18 @@ int qv_search(qv_index* ix, const float* queries, int64_t nq, int32_t dim, int32
     qv_search_opts_default(&o);
     if (opts) o = *opts;
     qv::search(ix, queries, nq, dim, topk, ef, o, ids, dists, found, rep);
+  });
+}
+
+int qv_search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int32_t dim, int32_t topk,
+                      int32_t ef, const qv_search_opts* opts, int32_t* d_ids, float* d_dists,
+                      int32_t* d_found, qv_search_report* rep) {
+  return qv::guard([&] {
+    if (!ix) qv::fail(QV_EINVAL, "null argument");
+    qv_search_opts o;
+    qv_search_opts_default(&o);
+    if (opts) o = *opts;
+    qv::search_noalloc(ix, d_queries, nq, dim, topk, ef, o, d_ids, d_dists, d_found, rep);
   });
 }
 

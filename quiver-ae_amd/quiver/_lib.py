@@ -33,6 +33,8 @@ QV_ADMIT_BATCH = 1
 QV_GRAPH_HBM = 0
 QV_GRAPH_HOST = 1
 QV_STREAM_READ_BLOCKS = 4096
+QV_NOALLOC_SCRATCH_BYTES = 32 * 1024 * 1024
+QV_NOALLOC_MAX_QUERIES = 1024 * 1024
 QV_KERNEL_AUTO = 0
 QV_KERNEL_LUT = 1
 QV_KERNEL_SHARED_PIVOTS = 2
@@ -149,6 +151,8 @@ SIGNATURES = {
     "qv_search_opts_default": (None, [C.POINTER(SearchOpts)]),
     "qv_search": (_I32, [_P, _P, _I64, _I32, _I32, _I32, C.POINTER(SearchOpts), _P, _P, _P,
                          C.POINTER(SearchReport)]),
+    "qv_search_noalloc": (_I32, [_P, _P, _I64, _I32, _I32, _I32, C.POINTER(SearchOpts), _P, _P, _P,
+                                 C.POINTER(SearchReport)]),
     "qv_last_hops": (_I32, [_P, _P, _I64]),
     "qv_last_latencies": (_I32, [_P, _P, _I64]),
     "qv_last_error": (C.c_char_p, []),
