@@ -19,6 +19,7 @@
 #include <rocprim/device/device_radix_sort.hpp>
 
 #include <algorithm>
+#include <type_traits>
 #include <chrono>
 #include <cmath>
 #include <cstring>
@@ -176,26 +177,6 @@ __device__ __forceinline__ void wave_sort_asc_full(uint64_t (&b)[P]) {
 }
 
 template <class T>
-__device__ __forceinline__ float vec_dist(const uint32_t* a, const uint32_t* b, int ds4, int32_t na, int32_t nb) {
-  if constexpr (sizeof(T) == 4) {
-    float s = 0.f;
-    for (int w = 0; w < ds4; w++) {
-      const float d = __uint_as_float(a[w]) - __uint_as_float(b[w]);
-      s = __fmaf_rn(d, d, s);
-    }
-    return s;
-  } else if constexpr (std::is_signed<T>::value) {
-    int32_t acc = 0;
-    for (int w = 0; w < ds4; w++) acc = __builtin_amdgcn_sdot4((int)a[w], (int)b[w], acc, false);
-    return (float)(na + nb - 2 * acc);
-  } else {
-    uint32_t acc = 0;
-    for (int w = 0; w < ds4; w++) acc = __builtin_amdgcn_udot4(a[w], b[w], acc, false);
-    return (float)((int64_t)na + (int64_t)nb - 2 * (int64_t)acc);
-  }
-}
-
-template <class T>
 __device__ __forceinline__ int32_t vec_norm(const uint32_t* a, int ds4) {
   if constexpr (sizeof(T) == 4) {
     return 0;
@@ -212,162 +193,450 @@ __device__ __forceinline__ int32_t vec_norm(const uint32_t* a, int ds4) {
 
 struct PruneArgs {
   GLayout L;
-  int mode;                  // 0: forward (search record + own list), 1: reverse (segments)
-  const int32_t* centers;    // forward: batch point ids
+  int mode;                  // 0: forward (search record), 1: reverse (marked segments), 2: flush
+  const int32_t* centers;    // modes 0 and 2: node ids
   int64_t num_centers;
   const int32_t* rec_ids;    // forward: [num_centers][rec_cap]
   const int32_t* hops;       // forward: [num_centers]
   int rec_cap;
   const uint64_t* pairs;     // reverse: sorted (target << 32 | source)
   const int32_t* heads;      // reverse: segment starts
+  const int32_t* marks;      // reverse: indexes into heads of the segments to prune
   int64_t num_pairs;
+  uint32_t* pend;            // [n][P] pending reverse edges (the slack beyond R)
+  int32_t* pcnt;             // [n] pending count
+  int P;
   float alpha;
   int cmax;                  // candidate capacity after dedupe
-  int ds4p;                  // padded row stride (dwords) of the LDS vector table
+  int stride;                // LDS row stride in dwords: a multiple of 4, stride / 4 odd, >= the row
+  int G;                     // lanes that fetch one row together (power of two, >= 4)
 };
 
-// One wave per centre: gather candidates, exact distances, sort, dedupe, then
-// either keep them all (<= R) or RobustPrune; writes the centre's list.
+// LDS of one prune wave: keys [cmax] u64, norms [cmax] i32, the centre row and
+// cmax candidate rows at `stride` dwords (16-byte aligned), then the output list.
+// The candidate rows double as the fetch phase's (id, distance) table.
+struct PruneLds {
+  int norms_off, cvec_off, vecs_off, outl_off, total;
+};
+__host__ __device__ inline PruneLds prune_lds_plan(int cmax, int stride, int R) {
+  PruneLds p;
+  p.norms_off = 8 * cmax;
+  p.cvec_off = (12 * cmax + 15) & ~15;
+  p.vecs_off = p.cvec_off + 4 * stride;
+  const int vec_bytes = 4 * cmax * stride > 8 * kMaxCand ? 4 * cmax * stride : 8 * kMaxCand;
+  p.outl_off = p.vecs_off + vec_bytes;
+  p.total = p.outl_off + 4 * R;
+  return p;
+}
+
+// Partial squared distance between the centre words c and row words x (8-bit
+// data: x.x - 2 c.x, the centre's norm added once per row; float: (c - x)^2).
+template <class T>
+struct RowAcc {
+  using type = typename std::conditional<sizeof(T) == 4, float, int32_t>::type;
+  __device__ static __forceinline__ type add(type acc, uint32_t c, uint32_t x) {
+    if constexpr (sizeof(T) == 4) {
+      const float d = __uint_as_float(c) - __uint_as_float(x);
+      return __fmaf_rn(d, d, acc);
+    } else if constexpr (std::is_signed<T>::value) {
+      return acc + __builtin_amdgcn_sdot4((int)x, (int)x, 0, false) - 2 * __builtin_amdgcn_sdot4((int)c, (int)x, 0, false);
+    } else {
+      return acc + (int32_t)__builtin_amdgcn_udot4(x, x, 0u, false) -
+             2 * (int32_t)__builtin_amdgcn_udot4(c, x, 0u, false);
+    }
+  }
+  __device__ static __forceinline__ type norm_add(type acc, uint32_t x) {
+    if constexpr (sizeof(T) == 4) return acc;
+    else if constexpr (std::is_signed<T>::value) return acc + __builtin_amdgcn_sdot4((int)x, (int)x, 0, false);
+    else return acc + (int32_t)__builtin_amdgcn_udot4(x, x, 0u, false);
+  }
+};
+
+template <class V>
+__device__ __forceinline__ V group_sum(V v, int G) {
+  for (int off = G >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// Squared distance of two LDS rows read 16 bytes at a time (q4 pieces; words
+// past the row are zero in both).  Float: the same dimension order as a
+// sequential loop; 8-bit data: exact integers from the dot product and norms.
+template <class T>
+__device__ __forceinline__ float lds_row_dist(const uint32_t* a, const uint32_t* b, int q4, int32_t na, int32_t nb) {
+  const uint4* a4 = reinterpret_cast<const uint4*>(a);
+  const uint4* b4 = reinterpret_cast<const uint4*>(b);
+  if constexpr (sizeof(T) == 4) {
+    float s = 0.f;
+    for (int q = 0; q < q4; q++) {
+      const uint4 x = a4[q], y = b4[q];
+      float d = __uint_as_float(x.x) - __uint_as_float(y.x);
+      s = __fmaf_rn(d, d, s);
+      d = __uint_as_float(x.y) - __uint_as_float(y.y);
+      s = __fmaf_rn(d, d, s);
+      d = __uint_as_float(x.z) - __uint_as_float(y.z);
+      s = __fmaf_rn(d, d, s);
+      d = __uint_as_float(x.w) - __uint_as_float(y.w);
+      s = __fmaf_rn(d, d, s);
+    }
+    return s;
+  } else if constexpr (std::is_signed<T>::value) {
+    int32_t acc = 0;
+    for (int q = 0; q < q4; q++) {
+      const uint4 x = a4[q], y = b4[q];
+      acc = __builtin_amdgcn_sdot4((int)x.x, (int)y.x, acc, false);
+      acc = __builtin_amdgcn_sdot4((int)x.y, (int)y.y, acc, false);
+      acc = __builtin_amdgcn_sdot4((int)x.z, (int)y.z, acc, false);
+      acc = __builtin_amdgcn_sdot4((int)x.w, (int)y.w, acc, false);
+    }
+    return (float)(na + nb - 2 * acc);
+  } else {
+    uint32_t acc = 0;
+    for (int q = 0; q < q4; q++) {
+      const uint4 x = a4[q], y = b4[q];
+      acc = __builtin_amdgcn_udot4(x.x, y.x, acc, false);
+      acc = __builtin_amdgcn_udot4(x.y, y.y, acc, false);
+      acc = __builtin_amdgcn_udot4(x.z, y.z, acc, false);
+      acc = __builtin_amdgcn_udot4(x.w, y.w, acc, false);
+    }
+    return (float)((int64_t)na + (int64_t)nb - 2 * (int64_t)acc);
+  }
+}
+
+// LDS areas of a prune wave.
+struct PruneSmem {
+  uint64_t* keys;
+  int32_t* norms;
+  uint32_t* cvec;
+  uint32_t* vecs;
+  uint32_t* outl;
+};
+
+// Prune of one centre over its C0 candidates (cand(i) -> node id, or -1 to
+// skip): exact distances from the centre, sort by (distance, id), dedupe, then
+// the list is the candidates themselves when they fit in R, else
+// RobustPrune(alpha, R) over them.  SL slots of 64 lanes hold the sort
+// (C0 <= 64 SL).  The centre's pending edges are cleared: the caller put them
+// among the candidates.
+// Candidate rows are fetched cooperatively: G lanes per row, lane p of a row
+// reading words p, p + G, ... (a contiguous G-word run per load instruction),
+// 64 / G rows per instruction and two instructions' rows in flight, so the
+// fetch costs a few memory round trips per centre instead of one per word.
+template <class T, int SL, class F>
+__device__ __forceinline__ void prune_one(const PruneArgs& a, const PruneSmem& m, int64_t center, int C0, F cand) {
+  using Acc = RowAcc<T>;
+  using AccT = typename Acc::type;
+  const GLayout& L = a.L;
+  const int lane = lane_id();
+  const int ds4 = (int)(L.data_size / 4);
+  const int S = a.stride;
+  const int w4 = (ds4 + 3) & ~3;  // row words read by lds_row_dist (zero past ds4)
+  const int G = a.G, rpr = kWave / G, p = lane & (G - 1), sub = lane / G;
+  const int kk = (ds4 + G - 1) / G;  // words per lane per row
+  uint32_t* cand_id = m.vecs;            // fetch phase: [kMaxCand] ids (~0u: none)
+  uint32_t* cand_d = m.vecs + kMaxCand;  // fetch phase: [kMaxCand] distance bits
+  uint32_t* crec = reinterpret_cast<uint32_t*>(node_rec(L, center));
+  uint32_t* cnb = crec + ds4;
+  const int32_t cnorm = vec_norm<T>(m.cvec, ds4);
+
+  // ---- distances centre -> candidates, rows fetched by groups of G lanes
+  for (int r0 = 0; r0 < C0; r0 += 2 * rpr) {
+    const int i0 = r0 + sub, i1 = r0 + rpr + sub;
+    const int64_t id0 = i0 < C0 ? cand(i0) : -1;
+    const int64_t id1 = i1 < C0 ? cand(i1) : -1;
+    const uint32_t* x0 = reinterpret_cast<const uint32_t*>(node_rec(L, id0 >= 0 ? id0 : center));
+    const uint32_t* x1 = reinterpret_cast<const uint32_t*>(node_rec(L, id1 >= 0 ? id1 : center));
+    AccT s0 = 0, s1 = 0;
+    for (int k0 = 0; k0 < kk; k0 += 4) {
+      uint32_t v0[4], v1[4], cw[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int w = p + G * (k0 + t);
+        const bool ok = k0 + t < kk && w < ds4;
+        v0[t] = ok ? x0[w] : 0u;
+        v1[t] = ok ? x1[w] : 0u;
+        cw[t] = ok ? m.cvec[w] : 0u;
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        s0 = Acc::add(s0, cw[t], v0[t]);
+        s1 = Acc::add(s1, cw[t], v1[t]);
+      }
+    }
+    s0 = group_sum(s0, G);
+    s1 = group_sum(s1, G);
+    if (p == 0) {
+      float d0, d1;
+      if constexpr (sizeof(T) == 4) {
+        d0 = s0;
+        d1 = s1;
+      } else {
+        d0 = (float)(cnorm + s0);
+        d1 = (float)(cnorm + s1);
+      }
+      if (i0 < C0) {
+        cand_id[i0] = id0 >= 0 ? (uint32_t)id0 : ~0u;
+        cand_d[i0] = __float_as_uint(d0);
+      }
+      if (i1 < C0) {
+        cand_id[i1] = id1 >= 0 ? (uint32_t)id1 : ~0u;
+        cand_d[i1] = __float_as_uint(d1);
+      }
+    }
+  }
+  __syncthreads();
+  uint64_t b[SL];
+#pragma unroll
+  for (int s = 0; s < SL; s++) {
+    const int i = s * kWave + lane;
+    uint64_t key = kPadKey;
+    if (i < C0) {
+      const uint32_t id = cand_id[i];
+      if (id != ~0u) key = ((uint64_t)cand_d[i] << 32) | (uint64_t)id;
+    }
+    b[s] = key;
+  }
+  __syncthreads();  // the fetch table is overwritten by the rows below
+  wave_sort_asc_full<SL>(b);
+  // dedupe (equal ids are adjacent: equal distance) and compact into LDS
+  int C = 0;
+  uint32_t prev = 0xffffffffu;
+  bool prev_valid = false;
+#pragma unroll
+  for (int s = 0; s < SL; s++) {
+    const uint32_t id = (uint32_t)b[s];
+    uint32_t pid = (uint32_t)__shfl_up((int)id, 1);
+    bool pvalid = __shfl_up((int)(b[s] != kPadKey), 1) != 0;
+    if (lane == 0) {
+      pid = prev;
+      pvalid = prev_valid;
+    }
+    const bool keep = b[s] != kPadKey && !(pvalid && pid == id);
+    const uint64_t km = __ballot(keep);
+    const int pos = C + __popcll(km & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
+    if (keep && pos < a.cmax) m.keys[pos] = b[s];
+    C += __popcll(km);
+    prev = (uint32_t)__shfl((int)id, kWave - 1);
+    prev_valid = __shfl((int)(b[s] != kPadKey), kWave - 1) != 0;
+  }
+  C = min(C, a.cmax);
+  __syncthreads();
+
+  int out_n = 0;
+  if (C <= L.R) {
+    for (int i = lane; i < C; i += kWave) cnb[1 + i] = (uint32_t)m.keys[i];
+    out_n = C;
+  } else {
+    // stage the candidate rows (and their norms) in LDS, fetched as above
+    for (int r0 = 0; r0 < C; r0 += 2 * rpr) {
+      const int i0 = r0 + sub, i1 = r0 + rpr + sub;
+      const int64_t id0 = i0 < C ? (int64_t)(uint32_t)m.keys[i0] : center;
+      const int64_t id1 = i1 < C ? (int64_t)(uint32_t)m.keys[i1] : center;
+      const uint32_t* x0 = reinterpret_cast<const uint32_t*>(node_rec(L, id0));
+      const uint32_t* x1 = reinterpret_cast<const uint32_t*>(node_rec(L, id1));
+      AccT n0 = 0, n1 = 0;
+      for (int k0 = 0; k0 < kk; k0 += 4) {
+        uint32_t v0[4], v1[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const int w = p + G * (k0 + t);
+          const bool ok = k0 + t < kk && w < ds4;
+          v0[t] = ok ? x0[w] : 0u;
+          v1[t] = ok ? x1[w] : 0u;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const int w = p + G * (k0 + t);
+          if (k0 + t < kk && w < w4) {
+            if (i0 < C) m.vecs[i0 * S + w] = v0[t];
+            if (i1 < C) m.vecs[i1 * S + w] = v1[t];
+          }
+          n0 = Acc::norm_add(n0, v0[t]);
+          n1 = Acc::norm_add(n1, v1[t]);
+        }
+      }
+      if constexpr (sizeof(T) != 4) {
+        n0 = group_sum(n0, G);
+        n1 = group_sum(n1, G);
+        if (p == 0) {
+          if (i0 < C) m.norms[i0] = n0;
+          if (i1 < C) m.norms[i1] = n1;
+        }
+      }
+    }
+    __syncthreads();
+    uint32_t alive = 0;
+#pragma unroll
+    for (int s = 0; s < SL; s++)
+      if (s * kWave + lane < C) alive |= 1u << s;
+    const int q4 = w4 / 4;
+    for (int i = 0; i < C && out_n < L.R; i++) {
+      const uint32_t owner = (uint32_t)__shfl((int)alive, i & (kWave - 1));
+      if (!((owner >> (i >> 6)) & 1u)) continue;
+      if (lane == 0) m.outl[out_n] = (uint32_t)m.keys[i];
+      out_n++;
+      const uint32_t* vi = m.vecs + i * S;
+      const int32_t ni = sizeof(T) == 4 ? 0 : m.norms[i];
+#pragma unroll
+      for (int s = 0; s < SL; s++) {
+        const int j = s * kWave + lane;
+        if (j > i && j < C && ((alive >> s) & 1u)) {
+          const float dij = lds_row_dist<T>(vi, m.vecs + j * S, q4, ni, sizeof(T) == 4 ? 0 : m.norms[j]);
+          const float dpj = __uint_as_float((uint32_t)(m.keys[j] >> 32));
+          if (a.alpha * dij <= dpj) alive &= ~(1u << s);
+        }
+      }
+    }
+    __syncthreads();
+    for (int i = lane; i < out_n; i += kWave) cnb[1 + i] = m.outl[i];
+  }
+  if (lane == 0) {
+    cnb[0] = (uint32_t)out_n;
+    a.pcnt[center] = 0;
+  }
+  __syncthreads();
+}
+
+// One wave per centre: forward prunes (mode 0: the nodes expanded by the
+// centre's build search, then its current list and pending edges), reverse
+// prunes of marked segments (mode 1: current list, pending edges, then the
+// segment's incoming sources) and the flush of pending edges (mode 2: list and
+// pending).  The sort width follows the candidate count.
 template <class T>
 __global__ __launch_bounds__(64) void prune_kernel(PruneArgs a) {
   extern __shared__ __align__(16) char smem[];
   const GLayout& L = a.L;
   const int lane = lane_id();
   const int ds4 = (int)(L.data_size / 4);
-  uint64_t* keys = reinterpret_cast<uint64_t*>(smem);
-  int32_t* norms = reinterpret_cast<int32_t*>(keys + a.cmax);
-  uint32_t* cvec = reinterpret_cast<uint32_t*>(norms + a.cmax + 1);
-  uint32_t* vecs = cvec + a.ds4p;
+  const PruneLds pl = prune_lds_plan(a.cmax, a.stride, L.R);
+  PruneSmem m;
+  m.keys = reinterpret_cast<uint64_t*>(smem);
+  m.norms = reinterpret_cast<int32_t*>(smem + pl.norms_off);
+  m.cvec = reinterpret_cast<uint32_t*>(smem + pl.cvec_off);
+  m.vecs = reinterpret_cast<uint32_t*>(smem + pl.vecs_off);
+  m.outl = reinterpret_cast<uint32_t*>(smem + pl.outl_off);
   for (int64_t ci = blockIdx.x; ci < a.num_centers; ci += gridDim.x) {
     int64_t center;
     int64_t seg_begin = 0, seg_end = 0;
-    if (a.mode == 0) {
+    if (a.mode != 1) {
       center = a.centers[ci];
     } else {
-      seg_begin = a.heads[ci];
+      seg_begin = a.heads[a.marks[ci]];
       center = (int64_t)(a.pairs[seg_begin] >> 32);
-      // segment end: first position whose target differs
-      // pairs are sorted by target, so the segment is the run of lanes
-      // whose target matches: advance by whole waves, then to the first miss
+      // pairs are sorted by target, so the segment is the run of pairs whose
+      // target matches: advance by whole waves, then to the first miss
       seg_end = seg_begin;
       while (true) {
-        const int64_t p = seg_end + lane;
-        const bool same = p < a.num_pairs && (int64_t)(a.pairs[p] >> 32) == center;
-        const uint64_t m = __ballot(same);
-        if (m == ~0ull) {
+        const int64_t q = seg_end + lane;
+        const bool same = q < a.num_pairs && (int64_t)(a.pairs[q] >> 32) == center;
+        const uint64_t mk = __ballot(same);
+        if (mk == ~0ull) {
           seg_end += kWave;
           continue;
         }
-        seg_end += __ffsll((long long)~m) - 1;
+        seg_end += __ffsll((long long)~mk) - 1;
         break;
       }
     }
     uint32_t* crec = reinterpret_cast<uint32_t*>(node_rec(L, center));
-    for (int w = lane; w < ds4; w += kWave) cvec[w] = crec[w];
-    __syncthreads();
-    const int32_t cnorm = vec_norm<T>(cvec, ds4);
-    uint32_t* cnb = crec + ds4;
+    for (int w = lane; w < a.stride; w += kWave) m.cvec[w] = w < ds4 ? crec[w] : 0u;
+    const uint32_t* cnb = crec + ds4;
     const int cdeg = (int)cnb[0];
-
-    // candidates: forward = recorded expansions + current list;
-    //             reverse = current list + incoming sources (capped)
-    uint64_t b[kSlots];
-#pragma unroll
-    for (int s = 0; s < kSlots; s++) {
-      const int i = s * kWave + lane;
-      int64_t id = -1;
-      if (a.mode == 0) {
-        const int nrec = min(a.hops[ci], a.rec_cap);
-        if (i < nrec) id = a.rec_ids[ci * a.rec_cap + i];
-        else if (i - nrec < cdeg) id = cnb[1 + (i - nrec)];
-      } else {
-        const int64_t nsrc = min<int64_t>(seg_end - seg_begin, kMaxCand - L.R);
-        if (i < cdeg) id = cnb[1 + i];
-        else if (i - cdeg < nsrc) id = (int64_t)(uint32_t)a.pairs[seg_begin + (i - cdeg)];
-      }
-      uint64_t key = kPadKey;
-      if (id >= 0 && id != center) {
-        const uint32_t* rv = reinterpret_cast<const uint32_t*>(node_rec(L, id));
-        float d;
-        if constexpr (sizeof(T) == 4) {
-          float acc = 0.f;
-          for (int w = 0; w < ds4; w++) {
-            const float df = __uint_as_float(cvec[w]) - __uint_as_float(rv[w]);
-            acc = __fmaf_rn(df, df, acc);
-          }
-          d = acc;
-        } else {
-          d = vec_dist<T>(cvec, rv, ds4, cnorm, vec_norm<T>(rv, ds4));
-        }
-        key = ((uint64_t)__float_as_uint(d) << 32) | (uint64_t)(uint32_t)id;
-      }
-      b[s] = key;
-    }
-    wave_sort_asc_full<kSlots>(b);
-    // dedupe (equal ids are adjacent: equal distance) and compact into LDS
-    int C = 0;
-    uint32_t prev = 0xffffffffu;
-    bool prev_valid = false;
-#pragma unroll
-    for (int s = 0; s < kSlots; s++) {
-      const uint32_t id = (uint32_t)b[s];
-      uint32_t pid = (uint32_t)__shfl_up((int)id, 1);
-      bool pvalid = __shfl_up((int)(b[s] != kPadKey), 1) != 0;
-      if (lane == 0) {
-        pid = prev;
-        pvalid = prev_valid;
-      }
-      const bool keep = b[s] != kPadKey && !(pvalid && pid == id);
-      const uint64_t km = __ballot(keep);
-      const int pos = C + __popcll(km & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
-      if (keep && pos < a.cmax) keys[pos] = b[s];
-      C += __popcll(km);
-      prev = (uint32_t)__shfl((int)id, kWave - 1);
-      prev_valid = __shfl((int)(b[s] != kPadKey), kWave - 1) != 0;
-    }
-    C = min(C, a.cmax);
+    const int pc = a.pcnt[center];
+    const uint32_t* pend = a.pend + center * a.P;
+    // candidate i: [lead candidates][current list][pending][trailing sources]
+    int lead = 0, tail = 0;
+    if (a.mode == 0) lead = min(a.hops[ci], a.rec_cap);
+    if (a.mode == 1) tail = (int)min<int64_t>(seg_end - seg_begin, kMaxCand - L.R - a.P);
+    const int C0 = min(lead + cdeg + pc + tail, kMaxCand);
+    auto cand = [&](int i) -> int64_t {
+      int64_t id;
+      if (i < lead) id = (int64_t)a.rec_ids[ci * a.rec_cap + i];
+      else if (i < lead + cdeg) id = (int64_t)cnb[1 + (i - lead)];
+      else if (i < lead + cdeg + pc) id = (int64_t)pend[i - lead - cdeg];
+      else id = (int64_t)(uint32_t)a.pairs[seg_begin + (i - lead - cdeg - pc)];
+      return id == center ? -1 : id;
+    };
     __syncthreads();
-
-    int out_n = 0;
-    if (C <= L.R) {
-      for (int i = lane; i < C; i += kWave) cnb[1 + i] = (uint32_t)keys[i];
-      out_n = C;
-    } else {
-      // stage candidate vectors (padded rows: conflict-free column reads)
-      for (int i = lane; i < C; i += kWave) {
-        const uint32_t* rv = reinterpret_cast<const uint32_t*>(node_rec(L, (int64_t)(uint32_t)keys[i]));
-        for (int w = 0; w < ds4; w++) vecs[i * a.ds4p + w] = rv[w];
-        norms[i] = vec_norm<T>(vecs + i * a.ds4p, ds4);
-      }
-      __syncthreads();
-      uint32_t alive = 0;
-#pragma unroll
-      for (int s = 0; s < kSlots; s++)
-        if (s * kWave + lane < C) alive |= 1u << s;
-      uint32_t* outl = reinterpret_cast<uint32_t*>(vecs + C * a.ds4p);
-      for (int i = 0; i < C && out_n < L.R; i++) {
-        const uint32_t owner = (uint32_t)__shfl((int)alive, i & (kWave - 1));
-        if (!((owner >> (i >> 6)) & 1u)) continue;
-        if (lane == 0) outl[out_n] = (uint32_t)keys[i];
-        out_n++;
-        const uint32_t* vi = vecs + i * a.ds4p;
-        const int32_t ni = norms[i];
-#pragma unroll
-        for (int s = 0; s < kSlots; s++) {
-          const int j = s * kWave + lane;
-          if (j > i && j < C && ((alive >> s) & 1u)) {
-            const float dij = vec_dist<T>(vi, vecs + j * a.ds4p, ds4, ni, norms[j]);
-            const float dpj = __uint_as_float((uint32_t)(keys[j] >> 32));
-            if (a.alpha * dij <= dpj) alive &= ~(1u << s);
-          }
-        }
-      }
-      __syncthreads();
-      for (int i = lane; i < out_n; i += kWave) cnb[1 + i] = outl[i];
-    }
-    if (lane == 0) cnb[0] = (uint32_t)out_n;
-    __syncthreads();
+    if (C0 <= 2 * kWave) prune_one<T, 2>(a, m, center, C0, cand);
+    else if (C0 <= 4 * kWave) prune_one<T, 4>(a, m, center, C0, cand);
+    else prune_one<T, kSlots>(a, m, center, C0, cand);
   }
+}
+
+// Reverse edges of a batch, one wave per target (a run of sorted pairs):
+// sources already among the target's list or pending edges are dropped; the
+// rest are appended to the list while it has room, then to the pending edges
+// (up to P, DiskANN's graph slack: a list may hold 1.3 R before it is pruned);
+// a target whose new edges fit neither is marked for a reverse prune.
+__global__ __launch_bounds__(64) void reverse_insert_kernel(GLayout L, const uint64_t* __restrict__ pairs,
+                                                            const int32_t* __restrict__ heads, int64_t nheads,
+                                                            int64_t npairs, uint32_t* __restrict__ pend,
+                                                            int32_t* __restrict__ pcnt, int P,
+                                                            int32_t* __restrict__ marks,
+                                                            unsigned int* __restrict__ nmarks) {
+  const int lane = lane_id();
+  for (int64_t hi = blockIdx.x; hi < nheads; hi += gridDim.x) {
+    const int64_t b = heads[hi];
+    const uint32_t t = (uint32_t)(pairs[b] >> 32);
+    uint32_t* nb = reinterpret_cast<uint32_t*>(node_rec(L, t) + L.data_size);
+    const int cdeg = (int)nb[0];
+    const int pc = pcnt[t];
+    const uint32_t mine = lane < cdeg ? nb[1 + lane] : ~0u;
+    const uint32_t pmine = lane < pc ? pend[(int64_t)t * P + lane] : ~0u;
+    // new sources, counted over the whole run, 64 pairs at a time
+    auto fresh = [&](int64_t q, uint32_t& src) -> bool {
+      if (q >= npairs || (uint32_t)(pairs[q] >> 32) != t) return false;
+      src = (uint32_t)pairs[q];
+      bool dup = false;
+      for (int k = 0; k < cdeg; k++) dup |= src == (uint32_t)__builtin_amdgcn_readlane((int)mine, k);
+      for (int k = 0; k < pc; k++) dup |= src == (uint32_t)__builtin_amdgcn_readlane((int)pmine, k);
+      return !dup;
+    };
+    int u = 0;
+    int64_t q0 = b;
+    while (true) {
+      uint32_t src = 0;
+      const bool in_run = q0 + lane < npairs && (uint32_t)(pairs[q0 + lane] >> 32) == t;
+      const bool f = in_run && fresh(q0 + lane, src);
+      u += __popcll(__ballot(f));
+      if (__ballot(in_run) != ~0ull) break;
+      q0 += kWave;
+    }
+    const int room = L.R - cdeg;
+    if (u > room + (P - pc)) {
+      if (lane == 0) marks[atomicAdd(nmarks, 1u)] = (int32_t)hi;
+      continue;
+    }
+    if (u == 0) continue;
+    int placed = 0;
+    q0 = b;
+    while (true) {
+      uint32_t src = 0;
+      const bool in_run = q0 + lane < npairs && (uint32_t)(pairs[q0 + lane] >> 32) == t;
+      const bool f = in_run && fresh(q0 + lane, src);
+      const uint64_t fm = __ballot(f);
+      if (f) {
+        const int r = placed + __popcll(fm & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
+        if (r < room) nb[1 + cdeg + r] = src;
+        else pend[(int64_t)t * P + pc + (r - room)] = src;
+      }
+      placed += __popcll(fm);
+      if (__ballot(in_run) != ~0ull) break;
+      q0 += kWave;
+    }
+    if (lane == 0) {
+      const int to_list = min(u, room);
+      nb[0] = (uint32_t)(cdeg + to_list);
+      pcnt[t] = pc + (u - to_list);
+    }
+  }
+}
+
+// Nodes with pending edges, for the flush at the end of a pass.
+__global__ void pending_nodes_kernel(const int32_t* __restrict__ pcnt, int64_t n, int32_t* __restrict__ out,
+                                     unsigned int* __restrict__ count) {
+  for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < n; v += (int64_t)gridDim.x * blockDim.x)
+    if (pcnt[v] > 0) out[atomicAdd(count, 1u)] = (int32_t)v;
 }
 
 // Reverse-edge pairs (target << 32 | source) of every new list of the batch.
@@ -744,18 +1013,43 @@ qv_index* build_gpu_t(const T* d_base, int dtype, int64_t n, int dim, const qv_b
   HIP_OK(hipMalloc(&d_sorted.p, sizeof(uint64_t) * (size_t)(max_batch * prm.R)));
   HIP_OK(hipMalloc(&d_heads.p, sizeof(int32_t) * (size_t)(max_batch * prm.R)));
   HIP_OK(hipMalloc(&d_cnt.p, 64));
+  // graph slack (DiskANN's GRAPH_SLACK_FACTOR 1.3): up to P reverse edges per
+  // node wait beside its record's R slots until a prune folds them in
+  const int P = (int)std::ceil(0.3 * prm.R);
+  DevBuf d_pend, d_pcnt, d_marks, d_flush;
+  HIP_OK(hipMalloc(&d_pend.p, sizeof(uint32_t) * (size_t)n * (size_t)P));
+  HIP_OK(hipMalloc(&d_pcnt.p, sizeof(int32_t) * (size_t)n));
+  HIP_OK(hipMemsetAsync(d_pcnt.p, 0, sizeof(int32_t) * (size_t)n, st));
+  HIP_OK(hipMalloc(&d_marks.p, sizeof(int32_t) * (size_t)(max_batch * prm.R)));
+  HIP_OK(hipMalloc(&d_flush.p, sizeof(int32_t) * (size_t)n));
   size_t tmp_bytes = 0;
   HIP_OK(rocprim::radix_sort_keys(nullptr, tmp_bytes, d_pairs.as<uint64_t>(), d_sorted.as<uint64_t>(),
                                   (size_t)(max_batch * prm.R), 0, 64, st));
   HIP_OK(hipMalloc(&d_tmp.p, tmp_bytes));
 
+  // Prune wave geometry: rows of `stride` dwords (16-byte pieces, an odd
+  // number of them, so 16 lanes reading 16 different rows hit distinct banks),
+  // G lanes per cooperative row fetch, and the largest candidate capacity
+  // that keeps 4 waves per CU (2 for long rows).
   const int ds4 = (int)(lay.data_size / 4);
-  const int ds4p = ds4 + 1;
-  const size_t per_cand = 8 + 4 + 4 * (size_t)ds4p;
-  int cmax = (int)std::min<size_t>(256, ((size_t)(96 * 1024) / per_cand) / 64 * 64);
-  cmax = std::max(cmax, 64);
-  const size_t prune_lds = (size_t)cmax * 8 + 4 * (size_t)(cmax + 1) + 4 * (size_t)ds4p +
-                           4 * (size_t)cmax * ds4p + 4 * (size_t)prm.R;
+  int stride4 = (ds4 + 3) / 4;
+  if (stride4 % 2 == 0) stride4++;
+  const int stride = 4 * stride4;
+  int fetch_lanes = 4;
+  while (fetch_lanes < 64 && fetch_lanes * 4 < ds4) fetch_lanes *= 2;
+  int lds_cu = 0;
+  HIP_OK(hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, device));
+  auto waves_at = [&](int c) {
+    const int bytes = (prune_lds_plan(c, stride, prm.R).total + 1023) & ~1023;
+    return lds_cu / bytes;
+  };
+  int cmax = 256;
+  while (cmax > 192 && waves_at(cmax) < 4) cmax -= 8;
+  if (waves_at(cmax) < 4) {
+    cmax = 256;
+    while (cmax > 64 && waves_at(cmax) < 2) cmax -= 8;
+  }
+  const size_t prune_lds = (size_t)prune_lds_plan(cmax, stride, prm.R).total;
   HIP_OK(hipFuncSetAttribute(reinterpret_cast<const void*>(prune_kernel<T>),
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)prune_lds));
 
@@ -787,9 +1081,13 @@ qv_index* build_gpu_t(const T* d_base, int dtype, int64_t n, int dim, const qv_b
       pa.rec_ids = d_rec.as<int32_t>();
       pa.hops = d_hops.as<int32_t>();
       pa.rec_cap = rec_cap;
+      pa.pend = d_pend.as<uint32_t>();
+      pa.pcnt = d_pcnt.as<int32_t>();
+      pa.P = P;
       pa.alpha = alpha;
       pa.cmax = cmax;
-      pa.ds4p = ds4p;
+      pa.stride = stride;
+      pa.G = fetch_lanes;
       hipLaunchKernelGGL(prune_kernel<T>, dim3((unsigned)std::min<int64_t>(nb, 65536)), dim3(64), prune_lds, st, pa);
       HIP_OK(hipGetLastError());
 
@@ -805,24 +1103,37 @@ qv_index* build_gpu_t(const T* d_base, int dtype, int64_t n, int dim, const qv_b
       HIP_OK(hipStreamSynchronize(st));
       if (nvalid > 0) {
         unsigned int* d_nh = reinterpret_cast<unsigned int*>(d_cnt.as<char>() + 32);
-        HIP_OK(hipMemsetAsync(d_nh, 0, 4, st));
+        unsigned int* d_nm = reinterpret_cast<unsigned int*>(d_cnt.as<char>() + 40);
+        HIP_OK(hipMemsetAsync(d_nh, 0, 16, st));
         hipLaunchKernelGGL(heads_kernel, dim3((unsigned)grid_of((int64_t)nvalid, 256)), dim3(256), 0, st,
                            d_sorted.as<uint64_t>(), (int64_t)nvalid, d_heads.as<int32_t>(), d_nh);
         HIP_OK(hipGetLastError());
         unsigned int nheads = 0;
         HIP_OK(hipMemcpyAsync(&nheads, d_nh, 4, hipMemcpyDeviceToHost, st));
         HIP_OK(hipStreamSynchronize(st));
-        PruneArgs ra = pa;
-        ra.mode = 1;
-        ra.centers = nullptr;
-        ra.num_centers = nheads;
-        ra.pairs = d_sorted.as<uint64_t>();
-        ra.heads = d_heads.as<int32_t>();
-        ra.num_pairs = (int64_t)nvalid;
-        hipLaunchKernelGGL(prune_kernel<T>, dim3((unsigned)std::min<unsigned>(nheads, 65536u)), dim3(64), prune_lds,
-                           st, ra);
+        // append reverse edges where the list or its slack has room; mark the rest
+        hipLaunchKernelGGL(reverse_insert_kernel, dim3((unsigned)std::min<unsigned>(nheads, 65536u)), dim3(64), 0,
+                           st, G, d_sorted.as<uint64_t>(), d_heads.as<int32_t>(), (int64_t)nheads,
+                           (int64_t)nvalid, d_pend.as<uint32_t>(), d_pcnt.as<int32_t>(), P,
+                           d_marks.as<int32_t>(), d_nm);
         HIP_OK(hipGetLastError());
+        unsigned int nmarks = 0;
+        HIP_OK(hipMemcpyAsync(&nmarks, d_nm, 4, hipMemcpyDeviceToHost, st));
         HIP_OK(hipStreamSynchronize(st));
+        if (nmarks > 0) {
+          PruneArgs ra = pa;
+          ra.mode = 1;
+          ra.centers = nullptr;
+          ra.num_centers = nmarks;
+          ra.pairs = d_sorted.as<uint64_t>();
+          ra.heads = d_heads.as<int32_t>();
+          ra.marks = d_marks.as<int32_t>();
+          ra.num_pairs = (int64_t)nvalid;
+          hipLaunchKernelGGL(prune_kernel<T>, dim3((unsigned)std::min<unsigned>(nmarks, 65536u)), dim3(64),
+                             prune_lds, st, ra);
+          HIP_OK(hipGetLastError());
+          HIP_OK(hipStreamSynchronize(st));
+        }
       }
       done += nb;
       bsz = std::min<int64_t>(bsz * 2, max_batch);  // capped: no overflow on long builds
@@ -832,6 +1143,34 @@ qv_index* build_gpu_t(const T* d_base, int dtype, int64_t n, int dim, const qv_b
                      (long long)done, (long long)n);
         std::fflush(stderr);
       }
+    }
+    // end of the pass: fold every node's pending edges into its list (DiskANN's
+    // final prune of lists longer than R)
+    unsigned int* d_nf = reinterpret_cast<unsigned int*>(d_cnt.as<char>() + 48);
+    HIP_OK(hipMemsetAsync(d_nf, 0, 4, st));
+    hipLaunchKernelGGL(pending_nodes_kernel, dim3((unsigned)grid_of(n, 256)), dim3(256), 0, st,
+                       d_pcnt.as<int32_t>(), n, d_flush.as<int32_t>(), d_nf);
+    HIP_OK(hipGetLastError());
+    unsigned int nflush = 0;
+    HIP_OK(hipMemcpyAsync(&nflush, d_nf, 4, hipMemcpyDeviceToHost, st));
+    HIP_OK(hipStreamSynchronize(st));
+    if (nflush > 0) {
+      PruneArgs fa{};
+      fa.L = G;
+      fa.mode = 2;
+      fa.centers = d_flush.as<int32_t>();
+      fa.num_centers = nflush;
+      fa.pend = d_pend.as<uint32_t>();
+      fa.pcnt = d_pcnt.as<int32_t>();
+      fa.P = P;
+      fa.alpha = alpha;
+      fa.cmax = cmax;
+      fa.stride = stride;
+      fa.G = fetch_lanes;
+      hipLaunchKernelGGL(prune_kernel<T>, dim3((unsigned)std::min<unsigned>(nflush, 65536u)), dim3(64), prune_lds,
+                         st, fa);
+      HIP_OK(hipGetLastError());
+      HIP_OK(hipStreamSynchronize(st));
     }
   }
   (void)t_start;
