@@ -773,6 +773,137 @@ __global__ void gt_final_kernel(const uint64_t* __restrict__ part, int64_t nq, i
   }
 }
 
+// Ground truth for 8-bit data with integer dot products: each lane owns one
+// query (its elements packed four to a register, zero past dim <= 128), tiles
+// of kGtTile consecutive base rows are staged in LDS with coalesced loads
+// (rows of kGtStride words: nine 16-byte pieces, an odd count, so the row-per-
+// thread norm pass is conflict-free) and every lane compares its query with
+// each staged row: d = |q|^2 + |x|^2 - 2 q.x, exact in int32 and in fp32
+// (< 2^24), so keys (d, id) -- and the top-k with ties to the smaller id --
+// equal the floating-point kernel's.
+constexpr int kGtTile = 256;
+constexpr int kGtWords = 32;
+constexpr int kGtStride = 36;
+constexpr int kGtMaxK = 16;
+
+template <class T>
+__device__ __forceinline__ uint32_t dot4(uint32_t a, uint32_t b, uint32_t acc) {
+  if constexpr (std::is_signed<T>::value)
+    return (uint32_t)__builtin_amdgcn_sdot4((int)a, (int)b, (int)acc, false);
+  else
+    return __builtin_amdgcn_udot4(a, b, acc, false);
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void gt_int_kernel(const T* __restrict__ base, int64_t n, int dim,
+                                                     const float* __restrict__ queries, int64_t nq, int k,
+                                                     int64_t slice, int S, uint64_t* __restrict__ part) {
+  __shared__ __align__(16) uint32_t rows[kGtTile * kGtStride];
+  __shared__ int32_t norms[kGtTile];
+  const int tid = threadIdx.x;
+  const int64_t qi = (int64_t)blockIdx.x * 256 + tid;
+  const int s = blockIdx.y;
+  const int d4 = dim / 4;
+  uint32_t qw[kGtWords];
+#pragma unroll
+  for (int w = 0; w < kGtWords; w++) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int j = 4 * w + e;
+      const int v = qi < nq && j < dim ? (int)queries[qi * dim + j] : 0;
+      packed |= ((uint32_t)v & 0xffu) << (8 * e);
+    }
+    qw[w] = packed;
+  }
+  uint32_t qn = 0;
+#pragma unroll
+  for (int w = 0; w < kGtWords; w++) qn = dot4<T>(qw[w], qw[w], qn);
+  for (int i = tid; i < kGtTile * kGtStride; i += 256) rows[i] = 0u;  // pads stay zero
+  uint64_t tk[kGtMaxK];
+#pragma unroll
+  for (int i = 0; i < kGtMaxK; i++) tk[i] = kPadKey;
+  uint64_t thr = kPadKey;
+  const int64_t r0 = (int64_t)s * slice, r1 = min(n, r0 + slice);
+  __syncthreads();
+  for (int64_t t0 = r0; t0 < r1; t0 += kGtTile) {
+    const int here = (int)min<int64_t>(kGtTile, r1 - t0);
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(base + t0 * dim);
+    if ((d4 & 3) == 0) {
+      const int pr = d4 / 4;  // 16-byte pieces per row
+      const uint4* s4 = reinterpret_cast<const uint4*>(src);
+      for (int u = tid; u < here * pr; u += 256) {
+        const int r = u / pr, c = u - r * pr;
+        *reinterpret_cast<uint4*>(rows + r * kGtStride + 4 * c) = s4[u];
+      }
+    } else {
+      const uint32_t* s1 = reinterpret_cast<const uint32_t*>(src);
+      for (int u = tid; u < here * d4; u += 256) {
+        const int r = u / d4, c = u - r * d4;
+        rows[r * kGtStride + c] = s1[u];
+      }
+    }
+    __syncthreads();
+    if (tid < here) {
+      const uint4* rp = reinterpret_cast<const uint4*>(rows + tid * kGtStride);
+      uint32_t nn = 0;
+#pragma unroll
+      for (int pc = 0; pc < kGtWords / 4; pc++) {
+        const uint4 x = rp[pc];
+        nn = dot4<T>(x.x, x.x, nn);
+        nn = dot4<T>(x.y, x.y, nn);
+        nn = dot4<T>(x.z, x.z, nn);
+        nn = dot4<T>(x.w, x.w, nn);
+      }
+      norms[tid] = (int32_t)nn;
+    }
+    __syncthreads();
+    for (int r = 0; r < here; r++) {
+      const uint4* rp = reinterpret_cast<const uint4*>(rows + r * kGtStride);
+      uint32_t acc = 0;
+#pragma unroll
+      for (int pc = 0; pc < kGtWords / 4; pc++) {
+        const uint4 x = rp[pc];
+        acc = dot4<T>(qw[4 * pc + 0], x.x, acc);
+        acc = dot4<T>(qw[4 * pc + 1], x.y, acc);
+        acc = dot4<T>(qw[4 * pc + 2], x.z, acc);
+        acc = dot4<T>(qw[4 * pc + 3], x.w, acc);
+      }
+      const int32_t d = (int32_t)qn + norms[r] - 2 * (int32_t)acc;
+      const uint64_t key = ((uint64_t)__float_as_uint((float)d) << 32) | (uint64_t)(t0 + r);
+      if (key < thr) {
+#pragma unroll
+        for (int i = kGtMaxK - 1; i > 0; i--) {
+          const uint64_t lo = tk[i - 1], cur = tk[i];
+          tk[i] = key < lo ? lo : (key < cur ? key : cur);
+        }
+        tk[0] = key < tk[0] ? key : tk[0];
+        uint64_t t = tk[0];
+#pragma unroll
+        for (int i = 1; i < kGtMaxK; i++) t = i == k - 1 ? tk[i] : t;
+        thr = t;
+      }
+    }
+    __syncthreads();
+  }
+  if (qi < nq) {
+#pragma unroll
+    for (int i = 0; i < kGtMaxK; i++)
+      if (i < k) part[(qi * S + s) * k + i] = tk[i];
+  }
+}
+
+// Sets *bad when a query element is not an integer of the element type's range
+// (then the 8-bit kernel does not apply).
+template <class T>
+__global__ void gt_query_check(const float* __restrict__ q, int64_t count, int32_t* __restrict__ bad) {
+  const float lo = std::is_signed<T>::value ? -128.f : 0.f, hi = std::is_signed<T>::value ? 127.f : 255.f;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = q[i];
+    if (!(v >= lo && v <= hi && v == rintf(v))) *bad = 1;
+  }
+}
+
 int grid_of(int64_t work, int block) {
   return (int)std::max<int64_t>(1, std::min<int64_t>((work + block - 1) / block, 1 << 20));
 }
@@ -780,6 +911,37 @@ int grid_of(int64_t work, int block) {
 template <class T>
 void ground_truth_t(const T* d_base, int64_t n, int dim, const float* d_q, int64_t nq, int k, int32_t* d_ids,
                     float* d_dists, hipStream_t st) {
+  if constexpr (sizeof(T) == 1) {
+    if (dim <= 4 * kGtWords && dim % 4 == 0 && k <= kGtMaxK) {
+      int32_t* d_bad = nullptr;
+      HIP_OK(hipMallocAsync(reinterpret_cast<void**>(&d_bad), sizeof(int32_t), st));
+      HIP_OK(hipMemsetAsync(d_bad, 0, sizeof(int32_t), st));
+      hipLaunchKernelGGL(gt_query_check<T>, dim3((unsigned)grid_of(nq * dim, 256)), dim3(256), 0, st, d_q, nq * dim,
+                         d_bad);
+      HIP_OK(hipGetLastError());
+      int32_t bad = 0;
+      HIP_OK(hipMemcpyAsync(&bad, d_bad, sizeof(bad), hipMemcpyDeviceToHost, st));
+      HIP_OK(hipStreamSynchronize(st));
+      HIP_OK(hipFreeAsync(d_bad, st));
+      if (!bad) {
+        const int64_t groups = (nq + 255) / 256;
+        const int64_t tiles = (n + kGtTile - 1) / kGtTile;
+        const int S = (int)std::max<int64_t>(1, std::min<int64_t>({256, tiles, (2048 + groups - 1) / groups}));
+        const int64_t slice = (tiles + S - 1) / S * kGtTile;
+        uint64_t* part = nullptr;
+        HIP_OK(hipMallocAsync(reinterpret_cast<void**>(&part), sizeof(uint64_t) * (size_t)(nq * S * k), st));
+        hipLaunchKernelGGL(gt_int_kernel<T>, dim3((unsigned)groups, (unsigned)S), dim3(256), 0, st, d_base, n, dim,
+                           d_q, nq, k, slice, S, part);
+        HIP_OK(hipGetLastError());
+        hipLaunchKernelGGL(gt_final_kernel, dim3((unsigned)std::min<int64_t>(nq, 65536)), dim3(64), 0, st, part, nq,
+                           S, k, d_ids, d_dists);
+        HIP_OK(hipGetLastError());
+        HIP_OK(hipFreeAsync(part, st));
+        HIP_OK(hipStreamSynchronize(st));
+        return;
+      }
+    }
+  }
   const int S = (int)std::max<int64_t>(1, std::min<int64_t>(64, 4096 / std::max<int64_t>(1, (nq + kGtQ - 1) / kGtQ)));
   const int64_t slice = (n + S - 1) / S;
   uint64_t* part = nullptr;
