@@ -2,12 +2,16 @@
 """Benchmark: QPS at Recall@10 >= 0.90 and P99 latency of the HBM-resident
 Quiver query path on one MI355X, plus the PQ-ADC gather bandwidth.
 
-Workload (default): 10M uint8 vectors of dimension 128 from the seeded
-Gaussian mixture (8192 centres uniform in [32, 224], sigma 20, clipped), a
+Workload (default): 100M uint8 vectors of dimension 128 from the seeded
+Gaussian mixture (65536 centres uniform in [32, 224], sigma 20, clipped), a
 Vamana graph R=64 / L=100 / alpha=1.2 and PQ 32x256 built on the GPU, 10k
 queries from the same mixture, top-10.  Setup (data, build, ground truth, the
 ef/early-exit sweep) is untimed; a step is one search of all queries with the
-queries resident in HBM.  Prints one JSON line.
+queries resident in HBM.  Beside it: the same steps with the queries and
+results in host memory (transfers inside each step), the latency mode
+(open-loop batches of 1, 16 and 256 queries at Recall@10 0.90 and 0.95), the
+PQ-ADC microbenchmark and the CPU oracle on the same index.  Prints one JSON
+line.
 """
 from __future__ import annotations
 
@@ -49,7 +53,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="mid-10M-u8", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="large-100M-u8", choices=sorted(WORKLOADS))
     ap.add_argument("--n", type=int, default=0, help="override the number of base vectors")
     ap.add_argument("--target-recall", type=float, default=0.90)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -59,8 +63,8 @@ def main() -> int:
     ap.add_argument("--ef", type=int, default=0, help="time this ef_search and skip the sweep")
     ap.add_argument("--policy", default="none", choices=("none", "gpruning"),
                     help="early-exit policy used with --ef")
-    ap.add_argument("--latency-batches", default="",
-                    help="comma-separated batch sizes for the latency leg (e.g. 1,16,256); empty: off")
+    ap.add_argument("--latency-batches", default="1,16,256",
+                    help="comma-separated batch sizes for the latency leg; empty: off")
     ap.add_argument("--adc-only", action="store_true",
                     help="run only the ADC microbenchmark leg (prints its JSON object)")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -136,6 +140,8 @@ def main() -> int:
     _lib.check(L.qv_ground_truth(d_base.ptr, dtype_code, n, dim, d_q.ptr, nq, 10, d_gi.ptr, d_gd.ptr, 0))
     gt = d_gi.download(np.int32, (nq, 10))
     log(f"ground truth: {time.time() - t:.1f}s")
+    if args.nav_sample <= 0:
+        d_base.close()  # only the nav-graph leg reads the base rows again
 
     if args.graph_placement == "host":
         _lib.check(L.qv_index_place_graph(h, _lib.QV_GRAPH_HOST))
@@ -234,11 +240,36 @@ def main() -> int:
     elapsed = t1 - t0
     recall = recall_of()
     timed_ids = d_ids.download(np.int32, (nq, 10))  # the later legs reuse d_ids
+    timed_dists = d_dists.download(np.float32, (nq, 10))
     qps = args.steps * nq / elapsed
     p99 = float(np.median([r.lat_p99_ms for r in reps]))
     p50 = float(np.median([r.lat_p50_ms for r in reps]))
     last = reps[-1]
     log(f"timed: ef={ef} {pname} steps={args.steps} qps={qps:.0f} recall={recall:.4f} p50={p50:.3f} p99={p99:.3f}")
+
+    # the same steps with the queries and results in host memory: the query
+    # upload and the result download fall inside each step, as in the
+    # reference's timing (src/quiver/search.cu:869, 1121-1129)
+    host_steps = max(1, min(args.steps, 10))
+    h_ids = np.empty((nq, 10), np.int32)
+    h_dists = np.empty((nq, 10), np.float32)
+    ho = _lib.default_search_opts()
+    ho.early_exit = policy
+    ho.pipe_width = 1
+    ho.kernel = _lib.KERNEL_NAMES[args.search_kernel]
+    ho.admission = _lib.QV_ADMIT_STREAMING
+    _lib.check(L.qv_search(h, qf.ctypes.data, nq, dim, 10, ef, C.byref(ho), h_ids.ctypes.data,
+                           h_dists.ctypes.data, None, None))
+    t0h = time.perf_counter()
+    for _ in range(host_steps):
+        _lib.check(L.qv_search(h, qf.ctypes.data, nq, dim, 10, ef, C.byref(ho), h_ids.ctypes.data,
+                               h_dists.ctypes.data, None, None))
+    host_s = time.perf_counter() - t0h
+    host_buffers = {"value": round(host_steps * nq / host_s, 1), "unit": "queries/s", "steps": host_steps,
+                    "ms_per_step": round(host_s / host_steps * 1e3, 3),
+                    "same_results": bool(np.array_equal(h_ids, timed_ids) and np.array_equal(h_dists, timed_dists)),
+                    "note": "queries uploaded from and results copied to host memory inside each step"}
+    log(f"host buffers: {host_buffers['value']:.0f} queries/s ({host_buffers['ms_per_step']} ms per step)")
 
     # with a nav graph: the same steps from the medoid, to price the nav search
     medoid_entry = None
@@ -260,7 +291,9 @@ def main() -> int:
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic(args.workload, ef, pname, kname, log),
                 "kernel": kname, "kernel_ms": round(kernel_ms, 3),
-                "bytes_per_launch": int(alg_bytes), "hops_per_launch": int(last.total_hops),
+                "bytes_per_launch": int(alg_bytes),
+                "bytes_per_launch_without_lut": int(alg_bytes - nq * info.num_chunks * 256 * 4),
+                "hops_per_launch": int(last.total_hops),
                 "evals_per_launch": int(last.total_evals)}
 
     result = {
@@ -277,6 +310,7 @@ def main() -> int:
                    "build_s": round(build_s, 1),
                    **({"medoid_entry": medoid_entry} if medoid_entry else {})},
         "roofline": roofline,
+        "host_buffers": host_buffers,
         "sweep": sweep,
     }
 
@@ -315,7 +349,7 @@ def main() -> int:
 
     # ---- CPU baseline: the oracle (CPU restatement) on a bounded sample -------
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_leg(_lib, L, h, info, qf, ef, policy, pname, timed_ids, nq,
+        result["cpu_baseline"] = cpu_leg(_lib, L, h, info, qf, ef, policy, pname, timed_ids, timed_dists, nq,
                                          args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
@@ -446,7 +480,7 @@ def adc_leg(_lib, L, ncodes: int, log) -> dict:
             "frac_of_stream_read": round(gbs / stream_gbs, 4)}
 
 
-def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, gpu_ids_all, nq, seconds: float) -> dict:
+def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, gpu_ids_all, gpu_dists_all, nq, seconds: float) -> dict:
     sys.path.insert(0, str(ROOT / "oracle"))
     import qv_oracle as O
 
@@ -468,17 +502,17 @@ def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, gpu_ids_all, nq, seconds: f
     sample = int(max(threads * 8, min(nq, seconds / max(per_q, 1e-9))))
     secs = np.zeros(sample, np.float64)
     t = time.time()
-    ids, _, _, _ = O.search(host, qf[:sample], 10, ef, early_exit=early, threads=threads, seconds=secs)
+    ids, dists, _, _ = O.search(host, qf[:sample], 10, ef, early_exit=early, threads=threads, seconds=secs)
     el = time.time() - t
-    gpu_ids = gpu_ids_all[:sample]
-    same = bool(np.array_equal(ids, gpu_ids))
+    same = bool(np.array_equal(ids, gpu_ids_all[:sample]))
+    same_d = bool(np.array_equal(dists, gpu_dists_all[:sample]))
     return {"value": round(sample / el, 1), "unit": "queries/s", "cores": threads, "kind": "port",
             "sample": f"first {sample} of the {nq} queries, same index, ef={ef}, {pname}, "
                       f"{el:.1f}s wall on {threads} threads (OpenMP over queries)",
             "p50_ms": round(float(np.percentile(secs, 50)) * 1e3, 3),
             "p99_ms": round(float(np.percentile(secs, 99)) * 1e3, 3),
             "label": "CPU restatement of the reference beam search (DiskANN unavailable offline)",
-            "ids_identical_to_gpu": same}
+            "ids_identical_to_gpu": same, "dists_identical_to_gpu": same_d}
 
 
 if __name__ == "__main__":
