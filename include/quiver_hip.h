@@ -93,6 +93,32 @@ int qv_index_open(const char* index_dir, const char* data_type,
                   const char* memory_backend, const char* memory_index_file,
                   int device, qv_index** out);
 
+/* A handle from an index the caller already holds in host memory -- what
+ * quiver::run_persistent_search (src/quiver/search.cuh:45-66) receives from
+ * its caller instead of file names: the shared::Layout (layout.hpp:7-19; of
+ * `layout` the fields num_data, num_dims, max_m0, enter_point, data_size,
+ * node_size, num_pages, nodes_per_page and data_type are read), the page
+ * image of its IndexLoader (num_pages x 4096 bytes, page k = page k + 1 of the
+ * disk index, as MemLoaderSync::load_heap holds it, mem_loader.cpp:28-44, and
+ * as submit_direct hands pages out, :104-117) and the host tables of its
+ * PQSearch (PQSearchData, pq_search.hpp:13-29: centroid [dim], pivots
+ * [256][dim], chunk_id [dim] non-decreasing -- chunks are contiguous
+ * dimension ranges -- and compressed_data [num_data][num_chunks]).  The same
+ * checks as qv_index_open; everything is copied to HBM of `device`, nothing of
+ * the caller's is kept. */
+int qv_index_from_memory(const qv_index_info* layout, const uint8_t* pages,
+                         const float* centroid, const float* pivots,
+                         const int32_t* chunk_id, int32_t num_chunks,
+                         const uint8_t* codes, int device, qv_index** out);
+
+/* Sets (or replaces) the navigation graph of a handle from the host arrays of
+ * a shared::NavGraph (nav_graph.hpp): data [num_node][dim] elements of the
+ * index type, graph [num_node][max_m] (-1 after a node's neighbours), mapping
+ * [num_node] base ids, start; max_m <= 32 (nav_graph.cu:58). */
+int qv_index_set_nav(qv_index* index, const void* data, const int32_t* graph,
+                     const int32_t* mapping, int64_t num_node, int32_t max_m,
+                     int32_t start);
+
 /* Where the page image (vectors + adjacency, the bulk of an index) lives. */
 #define QV_GRAPH_HBM 0  /* device memory (default) */
 #define QV_GRAPH_HOST 1 /* pinned host memory the kernel reads over the host link,
@@ -157,6 +183,20 @@ typedef struct {
   double timeout_s;          /* 0: no limit */
   int32_t skip_nav;          /* --skip-nav: medoid entry even with a nav graph loaded */
   int32_t kernel;            /* QV_KERNEL_AUTO / QV_KERNEL_LUT / QV_KERNEL_SHARED_PIVOTS */
+  /* Per-step recall (--per-step-recall; PerStepRecallOptions, src/quiver/
+   * search.cuh:17-28, applied as kernel_q1.cuh:354-364, 662-667): when
+   * step_recall_gt is not NULL, query i stops after the first step at which
+   * ceil(threshold x topk) of its top-k ids appear in ground-truth row
+   * i % count.  Host memory, also with device_buffers: gt [count][width]
+   * int32 (width 1..256, >= topk), outputs step [nq] (-1 if never reached) and
+   * hits [nq] (may be NULL).  Pipe width 1 and queries_per_block 1 only, as
+   * in the reference (search.cu:492-505). */
+  const int32_t* step_recall_gt;
+  int32_t step_recall_gt_width;
+  int32_t step_recall_gt_count;
+  float step_recall_threshold;  /* (0, 1]; --recall-threshold, 0.9 by default */
+  int32_t* step_recall_step;
+  int32_t* step_recall_hits;
 } qv_search_opts;
 
 /* shared::RunReport (src/shared/common/run_report.hpp:32-56) for one search. */

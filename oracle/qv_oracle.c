@@ -441,15 +441,46 @@ int64_t qvo_nav_entry(const qvo_nav* nav, const float* q, int64_t fallback) {
 /* node fetch served instantly (graph resident in memory), so every issued   */
 /* lane is ready on the next pipe iteration.                                  */
 /* ------------------------------------------------------------------------ */
+static int search_one_impl(const qvo_index* ix, const float* q, const qvo_search_params* p,
+                           int32_t* out_ids, float* out_dists, int32_t* out_found,
+                           int32_t* out_hops, int32_t* trace, int trace_cap,
+                           const int32_t* sr_row, int32_t* sr_step, int32_t* sr_hits);
+
 int qvo_search_one(const qvo_index* ix, const float* q, const qvo_search_params* p,
                    int32_t* out_ids, float* out_dists, int32_t* out_found,
                    int32_t* out_hops) {
-  return qvo_search_trace(ix, q, p, out_ids, out_dists, out_found, out_hops, NULL, 0);
+  return search_one_impl(ix, q, p, out_ids, out_dists, out_found, out_hops, NULL, 0, NULL, NULL, NULL);
 }
 
 int qvo_search_trace(const qvo_index* ix, const float* q, const qvo_search_params* p,
                      int32_t* out_ids, float* out_dists, int32_t* out_found,
                      int32_t* out_hops, int32_t* trace, int trace_cap) {
+  const int32_t* row = p->sr_gt ? p->sr_gt : NULL;  /* one query: ground-truth row 0 */
+  return search_one_impl(ix, q, p, out_ids, out_dists, out_found, out_hops, trace, trace_cap, row,
+                         row ? p->sr_step : NULL, row ? p->sr_hits : NULL);
+}
+
+/* count_topk_gt_hits: kernel_helpers.cuh:520-535 -- top-k entries (padding
+ * -1 skipped, a repeated id counted each time) found in the ground-truth row. */
+static int topk_gt_hits(const int32_t* nns, int topk, const int32_t* gt, int width) {
+  int hits = 0;
+  for (int i = 0; i < topk; i++) {
+    if (nns[i] < 0) continue;
+    for (int j = 0; j < width; j++) {
+      if (nns[i] == gt[j]) {
+        hits++;
+        break;
+      }
+    }
+  }
+  return hits;
+}
+
+static int search_one_impl(const qvo_index* ix, const float* q, const qvo_search_params* p,
+                           int32_t* out_ids, float* out_dists, int32_t* out_found,
+                           int32_t* out_hops, int32_t* trace, int trace_cap,
+                           const int32_t* sr_row, int32_t* sr_step, int32_t* sr_hits) {
+  if (sr_row && p->pipe_width != 1) return QVO_EINVAL;
   if (p->topk <= 0 || p->ef_search <= 0 || p->pipe_width < 1 || p->pipe_width > 16)
     return QVO_EINVAL;
   const int W = p->pipe_width;
@@ -485,6 +516,7 @@ int qvo_search_trace(const qvo_index* ix, const float* q, const qvo_search_param
   gprune g = {0, 0, INFINITY, INFINITY};
   int step = 0;
   int stop = 0;
+  int sr_reached = 0, sr_at = -1, sr_h = 0;
   int32_t lane_req[16];
   int32_t lane_node[16];
   int lane_ready[16];
@@ -501,6 +533,16 @@ int qvo_search_trace(const qvo_index* ix, const float* q, const qvo_search_param
   if (gpruning_step(p, &s, &g, step)) {
     stop = 1;
     lane_req[0] = -1;
+  }
+  if (sr_row && !stop) {
+    const int h = topk_gt_hits(s.nns, p->topk, sr_row, p->sr_width);
+    if (h >= p->sr_required) {
+      sr_reached = 1;
+      sr_at = step;
+      sr_h = h;
+      stop = 1;
+      lane_req[0] = -1;
+    }
   }
   for (int w = 1; w < W; w++) lane_req[w] = select_next_no_compact(&s);
   for (int w = 0; w < W; w++) {
@@ -527,6 +569,16 @@ int qvo_search_trace(const qvo_index* ix, const float* q, const qvo_search_param
         stop = 1;
         lane_req[w] = -1;
       }
+      if (sr_row && !stop) {
+        const int h = topk_gt_hits(s.nns, p->topk, sr_row, p->sr_width);
+        if (h >= p->sr_required) {
+          sr_reached = 1;
+          sr_at = step;
+          sr_h = h;
+          stop = 1;
+          lane_req[w] = -1;
+        }
+      }
     }
     if (stop) break;
     /* phase 1: idle lanes that were not served this iteration (:622-630) */
@@ -550,6 +602,10 @@ done:
     }
     if (out_found) *out_found = s.fc;
     if (out_hops) *out_hops = step;
+    if (sr_row) {
+      if (sr_step) *sr_step = sr_reached ? sr_at : -1;
+      if (sr_hits) *sr_hits = sr_reached ? sr_h : topk_gt_hits(s.nns, p->topk, sr_row, p->sr_width);
+    }
   }
   free(s.nid); free(s.ndist); free(s.tmp_id); free(s.tmp_dist);
   free(s.mv_id); free(s.mv_dist); free(s.mv_pos); free(s.written);
@@ -579,9 +635,12 @@ int qvo_search_timed(const qvo_index* ix, const float* queries, int64_t nq,
 #endif
   for (int64_t i = 0; i < nq; i++) {
     const double t0 = seconds ? wall_seconds() : 0.0;
-    int rc = qvo_search_one(ix, queries + i * (int64_t)ix->dim, p,
-                            ids + i * p->topk, dists + i * p->topk,
-                            found ? found + i : NULL, hops ? hops + i : NULL);
+    const int32_t* sr_row = p->sr_gt ? p->sr_gt + (i % p->sr_count) * (int64_t)p->sr_width : NULL;
+    int rc = search_one_impl(ix, queries + i * (int64_t)ix->dim, p,
+                             ids + i * p->topk, dists + i * p->topk,
+                             found ? found + i : NULL, hops ? hops + i : NULL, NULL, 0, sr_row,
+                             sr_row && p->sr_step ? p->sr_step + i : NULL,
+                             sr_row && p->sr_hits ? p->sr_hits + i : NULL);
     if (seconds) seconds[i] = wall_seconds() - t0;
     if (rc != QVO_OK) {
 #ifdef _OPENMP

@@ -88,6 +88,19 @@ typedef struct {
   int gpruning_warmup;     /* reference CLI default 10 */
   int gpruning_patience;   /* reference CLI default 8 */
   const qvo_nav* nav;      /* entry from the nav search when not NULL, else the medoid */
+  /* per-step recall (kernel_q1.cuh:354-364, 662-667; search.cu:100-102): when
+   * sr_gt is not NULL, query i checks after each step how many of its top-k
+   * ids appear in ground-truth row i % sr_count (sr_width ids) and stops once
+   * that count reaches sr_required; sr_step[i] receives that step (-1 when
+   * never reached) and sr_hits[i] the count then (else the final count).
+   * Pipe width 1 only (search.cu:493-496).  sr_step/sr_hits are used by the
+   * batch calls (qvo_search, qvo_search_timed), indexed by query. */
+  const int32_t* sr_gt;
+  int sr_width;
+  int sr_count;
+  int sr_required;
+  int32_t* sr_step;
+  int32_t* sr_hits;
 } qvo_search_params;
 
 /* Entry node of raw query q from the nav graph (base id).  `fallback` is

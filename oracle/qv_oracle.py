@@ -52,6 +52,12 @@ class SearchParams(C.Structure):
         ("gpruning_warmup", C.c_int),
         ("gpruning_patience", C.c_int),
         ("nav", C.c_void_p),
+        ("sr_gt", C.c_void_p),
+        ("sr_width", C.c_int),
+        ("sr_count", C.c_int),
+        ("sr_required", C.c_int),
+        ("sr_step", C.c_void_p),
+        ("sr_hits", C.c_void_p),
     ]
 
 
@@ -264,12 +270,22 @@ def nav_entry(nav: HostNav, q: np.ndarray, fallback: int = -1) -> int:
     return int(load().qvo_nav_entry(C.byref(cs), _ptr(qq), fallback))
 
 
+def required_hits(threshold: float, topk: int) -> int:
+    """Hits a query needs to stop under per-step recall (search.cu:100-102)."""
+    import math
+    return max(1, min(topk, int(math.ceil(np.float32(threshold) * np.float32(topk) - np.float32(1e-6)))))
+
+
 def search(ix: HostIndex, queries: np.ndarray, topk: int, ef: int, *, pipe_width: int = 1,
            early_exit: int = EXIT_GPRUNING, warmup: int = 10, patience: int = 8, threads: int = 0,
-           nav: HostNav | None = None, seconds: np.ndarray | None = None):
+           nav: HostNav | None = None, seconds: np.ndarray | None = None,
+           step_recall: tuple[np.ndarray, int] | None = None):
     """Oracle search: returns (ids int32 [n,k], dists float32 [n,k], found, hops).
     With `nav`, each query starts from its nav-graph entry instead of the medoid.
-    With `seconds` (float64 [n]), each query's wall time is written there."""
+    With `seconds` (float64 [n]), each query's wall time is written there.
+    With `step_recall` = (ground truth int32 [count, width], required hits),
+    each query stops once that many of its top-k ids are in its ground-truth
+    row, and (step, hits) arrays are returned after the four above."""
     lib = load()
     q = np.ascontiguousarray(queries, dtype=np.float32)
     n = q.shape[0]
@@ -280,6 +296,13 @@ def search(ix: HostIndex, queries: np.ndarray, topk: int, ef: int, *, pipe_width
     ns = nav.c_struct() if nav is not None else None
     p = SearchParams(topk, ef, pipe_width, early_exit, warmup, patience,
                      C.cast(C.pointer(ns), C.c_void_p) if ns is not None else None)
+    if step_recall is not None:
+        sr_gt = np.ascontiguousarray(step_recall[0], np.int32)
+        sr_step = np.empty(n, np.int32)
+        sr_hits = np.empty(n, np.int32)
+        p.sr_gt, p.sr_width, p.sr_count = sr_gt.ctypes.data, sr_gt.shape[1], sr_gt.shape[0]
+        p.sr_required = int(step_recall[1])
+        p.sr_step, p.sr_hits = sr_step.ctypes.data, sr_hits.ctypes.data
     cs = ix.c_struct()
     if seconds is not None:
         if seconds.dtype != np.float64 or seconds.shape != (n,) or not seconds.flags.c_contiguous:
@@ -291,13 +314,17 @@ def search(ix: HostIndex, queries: np.ndarray, topk: int, ef: int, *, pipe_width
                             _ptr(found), _ptr(hops))
     if rc != 0:
         raise RuntimeError(f"oracle search failed with status {rc}")
+    if step_recall is not None:
+        return ids, dists, found, hops, sr_step, sr_hits
     return ids, dists, found, hops
 
 
 def search_trace(ix: HostIndex, query: np.ndarray, topk: int, ef: int, *, pipe_width: int = 1,
-                 early_exit: int = EXIT_NONE, warmup: int = 10, patience: int = 8, cap: int = 4096):
+                 early_exit: int = EXIT_NONE, warmup: int = 10, patience: int = 8, cap: int = 4096,
+                 step_recall: tuple[np.ndarray, int] | None = None):
     """One query; returns (ids, dists, found, hops, expanded) where expanded[s]
-    is the node expanded at step s + 1 (the entry first)."""
+    is the node expanded at step s + 1 (the entry first).  With `step_recall`
+    = (ground-truth row int32 [width], required hits), (step, hits) follow."""
     lib = load()
     q = np.ascontiguousarray(query, dtype=np.float32).reshape(-1)
     ids = np.empty(topk, np.int32)
@@ -306,13 +333,22 @@ def search_trace(ix: HostIndex, query: np.ndarray, topk: int, ef: int, *, pipe_w
     hops = np.empty(1, np.int32)
     trace = np.full(cap, -1, np.int32)
     p = SearchParams(topk, ef, pipe_width, early_exit, warmup, patience, None)
+    if step_recall is not None:
+        sr_gt = np.ascontiguousarray(step_recall[0], np.int32).reshape(1, -1)
+        sr_out = np.full(2, -7, np.int32)
+        p.sr_gt, p.sr_width, p.sr_count = sr_gt.ctypes.data, sr_gt.shape[1], 1
+        p.sr_required = int(step_recall[1])
+        p.sr_step, p.sr_hits = sr_out.ctypes.data, sr_out.ctypes.data + 4
     cs = ix.c_struct()
     rc = lib.qvo_search_trace(C.byref(cs), _ptr(q), C.byref(p), _ptr(ids), _ptr(dists), _ptr(found),
                               _ptr(hops), _ptr(trace), cap)
     if rc != 0:
         raise RuntimeError(f"oracle search failed with status {rc}")
     h = int(hops[0])
-    return ids, dists, int(found[0]), h, [int(v) for v in trace[:min(h, cap)]]
+    out = (ids, dists, int(found[0]), h, [int(v) for v in trace[:min(h, cap)]])
+    if step_recall is not None:
+        return out + (int(sr_out[0]), int(sr_out[1]))
+    return out
 
 
 def lut(dim: int, centroid: np.ndarray, pivots_t: np.ndarray, chunk_id: np.ndarray,

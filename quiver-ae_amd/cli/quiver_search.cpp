@@ -1,6 +1,7 @@
 // quiver_search -- command-line front end with the reference's flags, stdout
 // report and result files (bin/quiver_search.cu:58-320, bin/common/*.hpp),
 // running the memory (heap) backend through libquiver_hip's C ABI.
+#include <algorithm>
 #include <cerrno>
 #include <cmath>
 #include <cstdint>
@@ -33,7 +34,8 @@ const char* kUsage =
     "  [--graph-placement hbm|host] [--search-kernel auto|lut|shared-pivots]\n"
     "  [--num-blocks 756] [--num-blocks-list L] [--pipe-width 2] [--queries-per-block 1]\n"
     "  [--poll-threads 6] [--runners-per-ssd 1] [--early-exit-policy gpruning|none]\n"
-    "  [--result-prefix P] [--final-recall-csv F] [--skip-nav] [--help]\n";
+    "  [--result-prefix P] [--final-recall-csv F] [--skip-nav] [--help]\n"
+    "  [--per-step-recall [--recall-threshold 0.9] [--step-recall-csv quiver_step_recall.csv]]\n";
 
 bool parse_int(const std::string& s, int& out) {
   char* end = nullptr;
@@ -104,6 +106,41 @@ int query_hits(const int32_t* res, const int32_t* gt, int k) {
 }
 
 }  // namespace
+
+// write_step_recall_csv (src/quiver/search.cu:100-153): one row per query and
+// the reached / step-percentile summary lines.
+bool write_step_recall(const std::string& path, const std::vector<int32_t>& steps,
+                       const std::vector<int32_t>& hits, int topk, float threshold) {
+  std::ofstream out(path);
+  if (!out.is_open()) {
+    std::cerr << "Failed to open step recall CSV " << path << std::endl;
+    return false;
+  }
+  out << "query_id,step,hits,recall,reached\n";
+  std::vector<int32_t> reached;
+  for (size_t q = 0; q < steps.size(); q++) {
+    const bool ok = steps[q] >= 0;
+    if (ok) reached.push_back(steps[q]);
+    out << q << "," << steps[q] << "," << hits[q] << "," << std::fixed << std::setprecision(6)
+        << (double)hits[q] / (double)topk << "," << (ok ? 1 : 0) << "\n";
+  }
+  out.close();
+  std::sort(reached.begin(), reached.end());
+  const int required = std::max(1, std::min(topk, (int)std::ceil(threshold * (float)topk - 1e-6f)));
+  std::cout << "[Quiver] Step recall CSV: " << path << "\n"
+            << "[Quiver] Step recall reached=" << reached.size() << " unreached=" << steps.size() - reached.size()
+            << " threshold=" << threshold << " required_hits=" << required << std::endl;
+  if (!reached.empty()) {
+    auto pct = [&](double p) {
+      size_t i = (size_t)((double)reached.size() * p / 100.0);
+      if (i >= reached.size()) i = reached.size() - 1;
+      return (double)reached[i];
+    };
+    std::cout << "[Quiver] Step recall steps p50=" << pct(50) << " p90=" << pct(90) << " p99=" << pct(99)
+              << " max=" << reached.back() << std::endl;
+  }
+  return true;
+}
 
 int main(int argc, char** argv) {
   std::map<std::string, Flag> f;
@@ -189,9 +226,38 @@ int main(int argc, char** argv) {
     std::cerr << "invalid --early-exit-policy: " << policy << " (expected gpruning or none)" << std::endl;
     return 1;
   }
-  if (f["--per-step-recall"].used) {
-    std::cerr << "--per-step-recall is not supported by this binary" << std::endl;
-    return 1;
+  // --per-step-recall (bin/quiver_search.cu:219-233): the ground truth stops
+  // each query once its top-k reaches the threshold
+  const bool step_recall = f["--per-step-recall"].used;
+  float recall_threshold = 0.9f;
+  const std::string step_csv = f["--step-recall-csv"].used ? f["--step-recall-csv"].value : "quiver_step_recall.csv";
+  std::vector<int32_t> step_gt;
+  int32_t step_gt_n = 0, step_gt_w = 0;
+  if (f["--recall-threshold"].used) {
+    char* end = nullptr;
+    recall_threshold = std::strtof(f["--recall-threshold"].value.c_str(), &end);
+    if (end == f["--recall-threshold"].value.c_str() || *end != 0) {
+      std::cerr << "invalid float for --recall-threshold: " << f["--recall-threshold"].value << "\n" << kUsage;
+      return 1;
+    }
+  }
+  if (step_recall) {
+    if (!f["--ground-truth"].used) {
+      std::cerr << "--per-step-recall requires --ground-truth" << std::endl;
+      return 1;
+    }
+    if (pipe_w != 1 || qpb != 1) {
+      std::cerr << "--per-step-recall currently requires pipe_width=1 and queries_per_block=1" << std::endl;
+      return 1;
+    }
+    try {
+      step_gt = read_bin<int32_t>(f["--ground-truth"].value, step_gt_n, step_gt_w);
+    } catch (const std::exception& e) {
+      std::cerr << e.what() << std::endl;
+      return 1;
+    }
+    std::cout << "[Quiver] per-step recall enabled: threshold=" << recall_threshold << " csv=" << step_csv
+              << " gt_count=" << step_gt_n << " gt_width=" << step_gt_w << std::endl;
   }
   std::vector<int> nb_list{num_blocks};
   if (f["--num-blocks-list"].used) {
@@ -275,6 +341,17 @@ int main(int argc, char** argv) {
     o.kernel = kernel;
     if (const char* e = std::getenv("QUIVER_PREFEED")) o.prefeed = std::atoi(e);
     if (const char* e = std::getenv("QUIVER_ADMIT_MIN_BATCH")) o.admit_min_batch = std::max(1, std::atoi(e));
+    std::vector<int32_t> sr_step, sr_hits;
+    if (step_recall) {
+      sr_step.resize((size_t)nq);
+      sr_hits.resize((size_t)nq);
+      o.step_recall_gt = step_gt.data();
+      o.step_recall_gt_width = step_gt_w;
+      o.step_recall_gt_count = step_gt_n;
+      o.step_recall_threshold = recall_threshold;
+      o.step_recall_step = sr_step.data();
+      o.step_recall_hits = sr_hits.data();
+    }
     qv_search_report rep;
     if (qv_search(ix, queries.data(), nq, dim, topk, ef, &o, ids.data(), dists.data(), found.data(), &rep) != QV_OK) {
       std::cerr << qv_last_error() << std::endl;
@@ -282,6 +359,10 @@ int main(int argc, char** argv) {
       return 1;
     }
     qv_last_hops(ix, hops.data(), nq);
+    if (step_recall && !write_step_recall(step_csv, sr_step, sr_hits, topk, recall_threshold)) {
+      qv_index_close(ix);
+      return 1;
+    }
     std::cout << "[Quiver] search_kernel="
               << (rep.kernel == QV_KERNEL_SHARED_PIVOTS ? "shared-pivots" : "lut") << std::endl;
     // format_run_report (src/shared/common/run_report.hpp:96-140)

@@ -95,6 +95,8 @@ std::string find_nav_dir(const std::string& index_dir);
 // nav_index.data and map.txt of dir; validated against the base (ids, dims).
 void read_nav(const std::string& dir, int data_type, int64_t base_n, int64_t dims, NavGraphHost& nav);
 void write_nav(const std::string& dir, int data_type, const NavGraphHost& nav);
+// The checks read_nav applies to its files, for a graph given in memory.
+void check_nav(const NavGraphHost& nav, int64_t base_n, int64_t dims, int data_type);
 
 // typed .bin with int32 (n, d) header (bin/common/data_io.hpp:29-51, 116-140)
 template <class T>

@@ -318,6 +318,22 @@ void read_nav(const std::string& dir, int data_type, int64_t base_n, int64_t dim
   }
 }
 
+void check_nav(const NavGraphHost& nav, int64_t base_n, int64_t dims, int data_type) {
+  if (nav.num_node <= 0) fail(QV_EINDEX, "nav graph has no nodes");
+  if (nav.dims != dims)
+    fail(QV_EINDEX, "nav graph has " + std::to_string(nav.dims) + " dims, the index " + std::to_string(dims));
+  if (nav.max_m < 1 || nav.max_m > 32) fail(QV_EINDEX, "nav graph max degree must be in [1, 32]");  // nav_graph.cu:58
+  if (nav.start < 0 || nav.start >= nav.num_node) fail(QV_EINDEX, "nav start out of range");
+  if (nav.data.size() != (size_t)nav.num_node * (size_t)dims * (size_t)elem_size(data_type))
+    fail(QV_EINDEX, "nav data size does not match num_node x dims");
+  if (nav.mapping.size() != (size_t)nav.num_node || nav.graph.size() != (size_t)nav.num_node * nav.max_m)
+    fail(QV_EINDEX, "nav map or graph size does not match num_node");
+  for (int32_t x : nav.mapping)
+    if (x < 0 || x >= base_n) fail(QV_EINDEX, "nav map entry out of range: " + std::to_string(x));
+  for (int32_t v : nav.graph)
+    if (v < -1 || v >= nav.num_node) fail(QV_EINDEX, "nav neighbour id out of range");
+}
+
 void write_nav(const std::string& dir, int data_type, const NavGraphHost& nav) {
   fs::create_directories(dir);
   {

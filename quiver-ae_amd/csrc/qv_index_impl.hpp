@@ -79,6 +79,8 @@ void release_index(qv_index* ix);
 
 // Loads the nav graph of dir (nav_index, nav_index.data, map.txt) to the device.
 void load_nav(qv_index* ix, const std::string& dir);
+// Checks a nav graph held in host memory and moves it to the handle's device.
+void upload_nav(qv_index* ix, const NavGraphHost& nav);
 
 // Checks degree <= R, neighbour ids < n and duplicate-free lists on the device;
 // throws QV_EINDEX on the first violation.

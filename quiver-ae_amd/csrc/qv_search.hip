@@ -102,6 +102,15 @@ struct SearchArgs {
   // <=> v in the beam), bits_words 32-bit words per slot, zero between queries
   uint32_t* bits;
   int64_t bits_words;
+  // per-step recall (pipe width 1): query q stops once sr_required of its
+  // top-k ids appear in ground-truth row q % sr_count (sr_width <= 256 ids);
+  // sr_gt null: off
+  const int32_t* sr_gt;
+  int32_t sr_width;
+  int32_t sr_count;
+  int32_t sr_required;
+  int32_t* sr_step;                // [nq] step at which it was reached, -1 if never
+  int32_t* sr_hits;                // [nq] hits then (else at the end)
 };
 
 enum : int32_t { kErrSpinTimeout = 1 };
@@ -581,6 +590,25 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       return gpr && step >= a.warmup && a.patience > 0 && g.no_improve >= a.patience;
     };
 
+    // count_topk_gt_hits (kernel_helpers.cuh:520-535): top-k entries (a
+    // repeated id counted each time, -1 padding skipped) found anywhere in the
+    // query's ground-truth row, read four ids per lane.
+    const bool sr = a.sr_gt != nullptr;
+    int sr_at = -1, sr_h = 0;
+    auto sr_hits = [&]() -> int {
+      const int32_t* row = a.sr_gt + (int64_t)(qid % a.sr_count) * a.sr_width;
+      int32_t g[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) g[t] = lane + kWave * t < a.sr_width ? row[lane + kWave * t] : -1;
+      int hits = 0;
+      for (int i = 0; i < a.topk; i++) {
+        const int32_t id = read_lane_i32(Qy.ti, i);
+        if (id < 0) continue;
+        hits += __ballot(g[0] == id || g[1] == id || g[2] == id || g[3] == id) != 0 ? 1 : 0;
+      }
+      return hits;
+    };
+
     auto log_hop = [&](int32_t v) {
       if (a.rec_ids && lane == 0 && step < a.rec_cap) {
         a.rec_ids[(int64_t)qid * a.rec_cap + step] = v;
@@ -607,6 +635,16 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
         if (check()) {
           stop = true;
           break;
+        }
+        // per-step recall, after the early-exit test (kernel_q1.cuh:354-364)
+        if (sr) {
+          const int h = sr_hits();
+          if (h >= a.sr_required) {
+            sr_at = step;
+            sr_h = h;
+            stop = true;
+            break;
+          }
         }
         if (nx < 0) break;
         v = nx;
@@ -659,7 +697,14 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     }
 
   finish:
-    // ---- finish (kernel_q1.cuh:684-704)
+    // ---- finish (kernel_q1.cuh:662-704)
+    if (sr) {
+      if (sr_at < 0) sr_h = sr_hits();
+      if (lane == 0) {
+        a.sr_step[qid] = sr_at;
+        a.sr_hits[qid] = sr_h;
+      }
+    }
     Qy.clear_bits(lane);
     if (lane < a.topk) {
       a.out_ids[(int64_t)qid * a.topk + lane] = Qy.ti;
@@ -1133,10 +1178,91 @@ qv_index* open_index(const std::string& index_dir, const std::string& dtype_s,
   return ix.release();
 }
 
+// A handle from an index the caller already holds in host memory: the
+// Layout, the heap image of the pages (page k = page k + 1 of the disk index,
+// MemLoaderSync::load_heap, mem_loader.cpp:28-44) and PQSearchData's host
+// tables (pq_search.hpp:13-29; chunk_id per dimension, contiguous chunks).
+// Checked as open_index checks files; everything is copied to HBM.
+qv_index* index_from_memory(const qv_index_info& li, const uint8_t* pages, const float* centroid,
+                            const float* pivots, const int32_t* chunk_id, int num_chunks, const uint8_t* codes,
+                            int device) {
+  if (!pages || !centroid || !pivots || !chunk_id || !codes) fail(QV_EINVAL, "null argument");
+  Layout lay;
+  lay.data_type = li.data_type;
+  if (lay.data_type != QV_UINT8 && lay.data_type != QV_FLOAT && lay.data_type != QV_INT8)
+    fail(QV_EINVAL, "data type must be QV_UINT8, QV_FLOAT or QV_INT8");
+  lay.num_data = li.num_data;
+  lay.num_dims = li.num_dims;
+  lay.max_m0 = li.max_m0;
+  lay.enter_point = li.enter_point;
+  lay.data_size = li.data_size;
+  lay.node_size = li.node_size;
+  lay.num_pages = li.num_pages;
+  lay.nodes_per_page = li.nodes_per_page;
+  if (lay.num_data <= 0 || lay.num_data > INT32_MAX) fail(QV_EUNSUPPORTED, "num_data must be in [1, 2^31-1]");
+  if (lay.num_dims <= 0 || lay.data_size != lay.num_dims * elem_size(lay.data_type))
+    fail(QV_EINDEX, "data_size must be num_dims x the element size");
+  if (lay.max_m0 > kMaxDegree || lay.max_m0 < 1)
+    fail(QV_EUNSUPPORTED, "max degree " + std::to_string(lay.max_m0) + " outside [1, 64]");
+  if (lay.node_size != lay.data_size + 4 + 4 * lay.max_m0)
+    fail(QV_EINDEX, "node_size must be data_size + 4 + 4 max_m0");
+  if ((lay.data_size & 3) || (lay.node_size & 3)) fail(QV_EUNSUPPORTED, "node records must be 4-byte aligned");
+  if (lay.nodes_per_page != kPageSize / lay.node_size || lay.nodes_per_page < 1)
+    fail(QV_EINDEX, "nodes_per_page must be 4096 / node_size");
+  if (lay.num_pages < (lay.num_data + lay.nodes_per_page - 1) / lay.nodes_per_page)
+    fail(QV_EINDEX, "num_pages too small for num_data records");
+  if (lay.enter_point < 0 || lay.enter_point >= lay.num_data) fail(QV_EINDEX, "enter_point out of range");
+  const int dim = (int)lay.num_dims;
+  if (num_chunks < 1 || num_chunks > dim) fail(QV_EINVAL, "num_chunks must be in [1, dim]");
+  PQTables pq;
+  pq.dim = dim;
+  pq.num_chunks = num_chunks;
+  pq.num_pts = lay.num_data;
+  pq.centroid.assign(centroid, centroid + dim);
+  pq.pivots.assign(pivots, pivots + (size_t)kNumPivots * dim);
+  pq.pivots_t.assign((size_t)dim * kNumPivots, 0.f);
+  for (int c = 0; c < kNumPivots; c++)
+    for (int j = 0; j < dim; j++) pq.pivots_t[(size_t)j * kNumPivots + c] = pq.pivots[(size_t)c * dim + j];
+  pq.chunk_id.assign(chunk_id, chunk_id + dim);
+  pq.chunk_offsets.assign((size_t)num_chunks + 1, 0);
+  for (int j = 0; j < dim; j++) {
+    const int m = chunk_id[j];
+    if (m < 0 || m >= num_chunks || (j > 0 && m < chunk_id[j - 1]))
+      fail(QV_EINDEX, "chunk_id must be non-decreasing in [0, num_chunks): PQ chunks are contiguous");
+    pq.chunk_offsets[(size_t)m + 1]++;
+  }
+  for (int m = 0; m < num_chunks; m++) pq.chunk_offsets[(size_t)m + 1] += pq.chunk_offsets[(size_t)m];
+
+  int ndev = 0;
+  HIP_OK(hipGetDeviceCount(&ndev));
+  if (device < 0 || device >= ndev) fail(QV_EINVAL, "device " + std::to_string(device) + " not present");
+  HIP_OK(hipSetDevice(device));
+  const size_t page_bytes = (size_t)(lay.num_pages * kPageSize);
+  const size_t code_bytes = (size_t)lay.num_data * (size_t)num_chunks;
+  uint8_t* d_pages = nullptr;
+  uint8_t* d_codes = nullptr;
+  HIP_OK(hipMalloc(&d_pages, page_bytes));
+  std::unique_ptr<uint8_t, void (*)(uint8_t*)> pg(d_pages, [](uint8_t* p) { (void)hipFree(p); });
+  HIP_OK(hipMalloc(&d_codes, std::max<size_t>(code_bytes, 64)));
+  std::unique_ptr<uint8_t, void (*)(uint8_t*)> cg(d_codes, [](uint8_t* p) { (void)hipFree(p); });
+  HIP_OK(hipMemcpy(d_pages, pages, page_bytes, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(d_codes, codes, code_bytes, hipMemcpyHostToDevice));
+  pg.release();
+  cg.release();
+  return make_index(device, lay, pq, d_pages, d_codes, true, false);
+}
+
 // NavGraph::init + copy_to_dev (nav_graph.cu:12-73) into this handle's device.
 void load_nav(qv_index* ix, const std::string& dir) {
   NavGraphHost nav;
   read_nav(dir, ix->lay.data_type, ix->lay.num_data, ix->lay.num_dims, nav);
+  upload_nav(ix, nav);
+}
+
+// A nav graph already in host memory (checked like read_nav's files) to the
+// handle's device, replacing any previous one.
+void upload_nav(qv_index* ix, const NavGraphHost& nav) {
+  check_nav(nav, ix->lay.num_data, ix->lay.num_dims, ix->lay.data_type);
   HIP_OK(hipSetDevice(ix->device));
   uint8_t* dd = nullptr;
   int32_t *dg = nullptr, *dm = nullptr;
@@ -1384,6 +1510,20 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   if (o.early_exit != QV_EXIT_NONE && o.early_exit != QV_EXIT_GPRUNING)
     fail(QV_EINVAL, "early exit policy must be none or gpruning");
   if (o.num_blocks < 0) fail(QV_EINVAL, "--num-blocks must be positive");
+  const bool step_recall = o.step_recall_gt != nullptr;
+  if (step_recall) {  // search.cu:492-505
+    if (o.queries_per_block != 1 || o.pipe_width != 1)
+      fail(QV_EINVAL, "Per-step recall currently supports only queries_per_block=1 and pipe_width=1");
+    if (o.step_recall_gt_count < 1 || o.step_recall_gt_width < 1)
+      fail(QV_EINVAL, "per-step recall needs a non-empty ground truth");
+    if (topk > o.step_recall_gt_width)
+      fail(QV_EINVAL, "Per-step recall topk=" + std::to_string(topk) + " exceeds ground truth width=" +
+                          std::to_string(o.step_recall_gt_width));
+    if (!(o.step_recall_threshold > 0.0f && o.step_recall_threshold <= 1.0f))
+      fail(QV_EINVAL, "Per-step recall threshold must be in (0, 1], got " + std::to_string(o.step_recall_threshold));
+    if (o.step_recall_gt_width > 4 * kWave)
+      fail(QV_EUNSUPPORTED, "per-step recall ground truth wider than 256 ids");
+  }
 
   HIP_OK(hipSetDevice(ix->device));
   ensure_scratch(ix, nq, topk);
@@ -1461,6 +1601,27 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   a.rec_ids = nullptr;
   a.rec_dists = nullptr;
   a.rec_cap = 0;
+  // per-step recall: ground truth and per-query outputs on the device for this call
+  struct DevFree {
+    void operator()(void* p) const { (void)hipFree(p); }
+  };
+  std::unique_ptr<int32_t, DevFree> sr_gt, sr_out;
+  if (step_recall) {
+    const size_t gt_elems = (size_t)o.step_recall_gt_count * (size_t)o.step_recall_gt_width;
+    int32_t* p = nullptr;
+    HIP_OK(hipMalloc(&p, sizeof(int32_t) * gt_elems));
+    sr_gt.reset(p);
+    HIP_OK(hipMemcpy(p, o.step_recall_gt, sizeof(int32_t) * gt_elems, hipMemcpyHostToDevice));
+    HIP_OK(hipMalloc(&p, sizeof(int32_t) * 2 * (size_t)nq));
+    sr_out.reset(p);
+    a.sr_gt = sr_gt.get();
+    a.sr_width = o.step_recall_gt_width;
+    a.sr_count = o.step_recall_gt_count;
+    // required_hits_for_threshold (search.cu:100-102), in the reference's float arithmetic
+    a.sr_required = std::max(1, std::min(topk, (int)std::ceil(o.step_recall_threshold * (float)topk - 1e-6f)));
+    a.sr_step = sr_out.get();
+    a.sr_hits = sr_out.get() + nq;
+  }
 
   using clock = std::chrono::steady_clock;
   if (use_bits) ix->bits_dirty = true;  // until every admitted query is seen to finish
@@ -1565,6 +1726,12 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     fail(QV_ETIMEDOUT, buf);
   }
   ix->last_hops.assign(st_hops, st_hops + nq);
+  if (step_recall) {
+    if (o.step_recall_step)
+      HIP_OK(hipMemcpy(o.step_recall_step, a.sr_step, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost));
+    if (o.step_recall_hits)
+      HIP_OK(hipMemcpy(o.step_recall_hits, a.sr_hits, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost));
+  }
   if (!streaming) {
     // every query admitted at launch: latency = its completion tick - the first start tick
     std::vector<uint64_t> ts((size_t)nq), te((size_t)nq);
@@ -1669,6 +1836,7 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
     fail(QV_EINVAL, "early exit policy must be none or gpruning");
   if (o.num_blocks < 0) fail(QV_EINVAL, "--num-blocks must be positive");
   if (o.timeout_s != 0.0) fail(QV_EINVAL, "qv_search_noalloc has no deadline (timeout_s must be 0)");
+  if (o.step_recall_gt) fail(QV_EINVAL, "qv_search_noalloc does not take per-step recall");
   if (!d_queries || !d_ids || !d_dists) fail(QV_EINVAL, "null argument");
 
   std::lock_guard<std::mutex> dlk(g_noalloc_mu);  // one device array: calls on one GPU are serialised here
@@ -1795,6 +1963,8 @@ void qv_search_opts_default(qv_search_opts* o) {
   o->timeout_s = 0.0;
   o->skip_nav = 0;
   o->kernel = QV_KERNEL_AUTO;
+  o->step_recall_gt = nullptr;
+  o->step_recall_threshold = 0.9f;
 }
 
 int qv_index_open(const char* index_dir, const char* data_type, const char* memory_backend,
@@ -1847,6 +2017,36 @@ int qv_index_place_graph(qv_index* ix, int32_t graph_placement) {
     ix->d_pages = p;
     ix->pages_in_host = to_host;
     ix->device_bytes += to_host ? -(int64_t)bytes : (int64_t)bytes;
+  });
+}
+
+int qv_index_from_memory(const qv_index_info* layout, const uint8_t* pages, const float* centroid,
+                         const float* pivots, const int32_t* chunk_id, int32_t num_chunks, const uint8_t* codes,
+                         int device, qv_index** out) {
+  return qv::guard([&] {
+    if (!layout || !out) qv::fail(QV_EINVAL, "null argument");
+    *out = nullptr;
+    *out = qv::index_from_memory(*layout, pages, centroid, pivots, chunk_id, num_chunks, codes, device);
+  });
+}
+
+int qv_index_set_nav(qv_index* ix, const void* data, const int32_t* graph, const int32_t* mapping,
+                     int64_t num_node, int32_t max_m, int32_t start) {
+  return qv::guard([&] {
+    if (!ix || !data || !graph || !mapping) qv::fail(QV_EINVAL, "null argument");
+    if (num_node <= 0 || num_node > INT32_MAX) qv::fail(QV_EINVAL, "num_node out of range");
+    if (max_m < 1 || max_m > 32) qv::fail(QV_EINDEX, "nav graph max degree must be in [1, 32]");
+    std::lock_guard<std::mutex> lk(ix->mu);
+    qv::NavGraphHost nav;
+    nav.num_node = (int32_t)num_node;
+    nav.dims = (int32_t)ix->lay.num_dims;
+    nav.max_m = max_m;
+    nav.start = start;
+    const size_t bytes = (size_t)num_node * (size_t)ix->lay.data_size;
+    nav.data.assign(static_cast<const uint8_t*>(data), static_cast<const uint8_t*>(data) + bytes);
+    nav.graph.assign(graph, graph + (size_t)num_node * (size_t)max_m);
+    nav.mapping.assign(mapping, mapping + num_node);
+    qv::upload_nav(ix, nav);
   });
 }
 

@@ -81,6 +81,12 @@ class SearchOpts(C.Structure):
         ("timeout_s", C.c_double),
         ("skip_nav", C.c_int32),
         ("kernel", C.c_int32),
+        ("step_recall_gt", C.c_void_p),
+        ("step_recall_gt_width", C.c_int32),
+        ("step_recall_gt_count", C.c_int32),
+        ("step_recall_threshold", C.c_float),
+        ("step_recall_step", C.c_void_p),
+        ("step_recall_hits", C.c_void_p),
     ]
 
 
@@ -144,6 +150,8 @@ SIGNATURES = {
     "qv_index_open": (_I32, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int, C.POINTER(_P)]),
     "qv_index_open_ex": (_I32, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int, _I32, C.POINTER(_P)]),
     "qv_index_place_graph": (_I32, [_P, _I32]),
+    "qv_index_from_memory": (_I32, [C.POINTER(IndexInfo), _P, _P, _P, _P, _I32, _P, C.c_int, C.POINTER(_P)]),
+    "qv_index_set_nav": (_I32, [_P, _P, _P, _P, _I64, _I32, _I32]),
     "qv_index_get_info": (_I32, [_P, C.POINTER(IndexInfo)]),
     "qv_index_load_nav": (_I32, [_P, C.c_char_p]),
     "qv_build_nav": (_I32, [_P, _P, _I64, _I32, _I32, C.POINTER(BuildParams), C.c_char_p]),

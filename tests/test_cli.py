@@ -43,6 +43,19 @@ def test_validation(tmp_path, flags, msg):
     assert r.returncode == 1 and msg in r.stderr
 
 
+@pytest.mark.parametrize("flags,msg", [
+    (["--per-step-recall"], "--per-step-recall requires --ground-truth"),
+    (["--per-step-recall", "--ground-truth", "gt.ibin"],
+     "--per-step-recall currently requires pipe_width=1 and queries_per_block=1"),
+    (["--per-step-recall", "--ground-truth", "gt.ibin", "--pipe-width", "1", "--queries-per-block", "2"],
+     "--per-step-recall currently requires pipe_width=1 and queries_per_block=1"),
+    (["--recall-threshold", "high"], "invalid float for --recall-threshold"),
+])
+def test_step_recall_validation(tmp_path, flags, msg):
+    r = run("--index-dir", tmp_path, "--query", "q.u8bin", "--data-type", "uint8", *flags)
+    assert r.returncode == 1 and msg in r.stderr
+
+
 def test_spdk_requires_spdk_build(tmp_path):
     ssd = tmp_path / "ssds.txt"
     ssd.write_text("0000:01:00.0\n")
@@ -86,3 +99,36 @@ def test_cli_search_report_and_results(small_u8_index, tmp_path, kernel, want):
     line = [s for s in r.stdout.splitlines() if s.startswith("Recall @ 10:")][0]
     assert abs(float(line.split(":")[1]) - O.recall(oids, ix["gt"][:100], 10)) < 1e-6
     assert (tmp_path / "r.csv").read_text().startswith("query_id,gt_query_id,hits,recall")
+
+
+@pytest.mark.gpu
+def test_cli_per_step_recall_matches_oracle(small_u8_index, tmp_path):
+    """--per-step-recall: the step CSV and summary lines (search.cu:112-153)
+    against the oracle's per-step recall on the same queries."""
+    import qv_oracle as O
+
+    ix = small_u8_index
+    q = ix["queries"][:120]
+    qf = tmp_path / "q.u8bin"
+    qf.write_bytes(struct.pack("<ii", *q.shape) + q.tobytes())
+    gt = np.ascontiguousarray(ix["gt"][:120], np.int32)
+    gf = tmp_path / "gt.ibin"
+    gf.write_bytes(struct.pack("<ii", *gt.shape) + gt.tobytes())
+    csv = tmp_path / "steps.csv"
+    print("[gpu] CLI --per-step-recall", flush=True)
+    r = run("--index-dir", ix["dir"], "--query", qf, "--data-type", "uint8", "--ef-search", "96",
+            "--repeat", "1", "--pipe-width", "1", "--ground-truth", gf, "--early-exit-policy", "none",
+            "--per-step-recall", "--recall-threshold", "0.8", "--step-recall-csv", csv)
+    assert r.returncode == 0, r.stderr
+    host = O.HostIndex.from_files(ix["dir"], "uint8")
+    _, _, _, _, step, hits = O.search(host, q.astype(np.float32), 10, 96, early_exit=O.EXIT_NONE,
+                                      step_recall=(gt, O.required_hits(0.8, 10)))
+    rows = [line.split(",") for line in csv.read_text().splitlines()]
+    assert rows[0] == ["query_id", "step", "hits", "recall", "reached"]
+    got = np.array([[int(x[1]), int(x[2]), int(x[4])] for x in rows[1:]])
+    np.testing.assert_array_equal(got[:, 0], step)
+    np.testing.assert_array_equal(got[:, 1], hits)
+    np.testing.assert_array_equal(got[:, 2], (step >= 0).astype(int))
+    reached = int((step >= 0).sum())
+    assert f"[Quiver] Step recall reached={reached} unreached={120 - reached} threshold=0.8 required_hits=8" in r.stdout
+    assert "[Quiver] per-step recall enabled: threshold=0.8" in r.stdout

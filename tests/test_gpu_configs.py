@@ -175,3 +175,38 @@ def test_deadline_gives_up_then_next_search_is_exact(c1):
         rc, got = _search(c1, c1["q"][:NQ], 128, "none", "lut")
         assert rc == 0
         _same(got, _oracle(c1, 128, "none"), f"LUT kernel after a {kernel} give-up")
+
+
+@pytest.mark.parametrize("threshold", [0.8, 1.0])
+def test_c1_step_recall_matches_oracle(c1, threshold):
+    """Per-step recall on the benchmark shape: each query stops once
+    ceil(threshold k) of its top-10 ids are in its ground-truth row; steps,
+    hits, ids and hop counts equal the oracle's."""
+    lib, L = c1["lib"], c1["L"]
+    n = 1000
+    _say(f"[gpu] C1 per-step recall threshold={threshold}")
+    gt = np.ascontiguousarray(c1["gt"][:n], np.int32)
+    for kernel in ("lut", "shared-pivots"):
+        o = lib.default_search_opts()
+        o.early_exit = lib.QV_EXIT_NONE
+        o.kernel = KERNEL[kernel]
+        step = np.empty(n, np.int32)
+        hits = np.empty(n, np.int32)
+        o.step_recall_gt, o.step_recall_gt_width, o.step_recall_gt_count = gt.ctypes.data, K, n
+        o.step_recall_threshold = threshold
+        o.step_recall_step, o.step_recall_hits = step.ctypes.data, hits.ctypes.data
+        q = np.ascontiguousarray(c1["q"][:n], np.float32)
+        ids = np.empty((n, K), np.int32)
+        dists = np.empty((n, K), np.float32)
+        found = np.empty(n, np.int32)
+        lib.check(L.qv_search(c1["h"], q.ctypes.data, n, DIM, K, 128, C.byref(o), ids.ctypes.data,
+                              dists.ctypes.data, found.ctypes.data, None))
+        hops = np.empty(n, np.int32)
+        lib.check(L.qv_last_hops(c1["h"], hops.ctypes.data, n))
+        oids, odists, ofound, ohops, ostep, ohits = O.search(
+            c1["host"], c1["q"][:n], K, 128, early_exit=O.EXIT_NONE,
+            step_recall=(gt, O.required_hits(threshold, K)))
+        _same((ids, dists, found, hops), (oids, odists, ofound, ohops), f"step recall {kernel}")
+        np.testing.assert_array_equal(step, ostep)
+        np.testing.assert_array_equal(hits, ohits)
+        assert 0 < (step >= 0).sum() < n  # both outcomes occur

@@ -29,11 +29,19 @@ def _open(lib, tmp_path, name, xs, adj, entry):
     return h
 
 
-def _run(lib, h, x, k, ef, width, policy, warmup=10, patience=8):
+def _run(lib, h, x, k, ef, width, policy, warmup=10, patience=8, sr=None):
+    """One query at position x; sr = (ground-truth row, threshold) turns on
+    per-step recall and appends (step, hits) to the result."""
     o = lib.default_search_opts()
     o.pipe_width = width
     o.early_exit = lib.QV_EXIT_GPRUNING if policy == "gpruning" else lib.QV_EXIT_NONE
     o.gpruning_warmup, o.gpruning_patience = warmup, patience
+    if sr is not None:
+        gt = np.ascontiguousarray(np.array(sr[0], np.int32).reshape(1, -1))
+        sr_out = np.full(2, -7, np.int32)
+        o.step_recall_gt, o.step_recall_gt_width, o.step_recall_gt_count = gt.ctypes.data, gt.shape[1], 1
+        o.step_recall_threshold = sr[1]
+        o.step_recall_step, o.step_recall_hits = sr_out.ctypes.data, sr_out.ctypes.data + 4
     q = np.full((1, 4), x, np.float32)
     ids = np.empty((1, k), np.int32)
     dists = np.empty((1, k), np.float32)
@@ -42,7 +50,8 @@ def _run(lib, h, x, k, ef, width, policy, warmup=10, patience=8):
                                    dists.ctypes.data, found.ctypes.data, None))
     hops = np.empty(1, np.int32)
     lib.check(lib.load().qv_last_hops(h, hops.ctypes.data, 1))
-    return list(ids[0]), list(dists[0]), int(found[0]), int(hops[0])
+    out = (list(ids[0]), list(dists[0]), int(found[0]), int(hops[0]))
+    return out + (int(sr_out[0]), int(sr_out[1])) if sr is not None else out
 
 
 @pytest.fixture(scope="module")
@@ -66,6 +75,14 @@ def test_line_gpruning_known_answers(lib, tmp_path):
             assert _run(lib, h, 30, 1, 64, 1, "gpruning", warmup, patience)[3] == stop, (warmup, patience)
         assert _run(lib, h, 30, 3, 64, 1, "gpruning", 2, 4) == ([5, 4, 6], [0.0, 144.0, 144.0], 3, 11)
         assert _run(lib, h, 0, 3, 64, 1, "gpruning", 0, 1) == ([0, 0, 1], [0.0, 0.0, 144.0], 3, 4)
+        # per-step recall (k = 3: thresholds 0.3 / 0.6 / 0.9 need 1 / 2 / 3 hits)
+        row_a, row_b = [20, 19, 21, 18, 22], [20, 21, 22]
+        for row, t, step, hits, hops in ((row_a, 0.3, 19, 1, 19), (row_a, 0.6, 20, 2, 20), (row_a, 0.9, 21, 3, 21),
+                                         (row_b, 0.3, 21, 1, 21), (row_b, 0.6, 22, 2, 22), (row_b, 1.0, -1, 2, 41)):
+            got = _run(lib, h, 120, 3, 64, 1, "none", sr=(row, t))
+            assert (got[3], got[4], got[5]) == (hops, step, hits), (row, t)
+        got = _run(lib, h, 120, 3, 64, 1, "gpruning", 10, 8, sr=(row_b, 1.0))
+        assert (got[3], got[4], got[5]) == (30, -1, 2)
     finally:
         lib.load().qv_index_close(h)
 

@@ -182,3 +182,50 @@ def test_pipe_lanes_with_gpruning(branch, width, order, ids, dists):
     assert got_order == order
     assert hops == len(order)
     assert list(got_ids) == ids and list(got_dists) == dists
+
+
+# ---- per-step recall (kernel_q1.cuh:354-364, 662-667) ---------------------------
+# q at node 20 (x = 120), k = 3, no early exit: step s <= 21 expands node s - 1,
+# so the top-3 after step s is {s-1, s-2, s-3}; step 22 expands 21 (144), which
+# ties 19 and enters: [20, 19, 21].  Hits count top-3 ids found anywhere in the
+# ground-truth row:
+#   row A = [20, 19, 21, 18, 22]: step 19 {18, 17, 16} -> 1, step 20 -> 2, step 21 -> 3
+#   row B = [20, 21, 22]:         step 21 -> 1, step 22 -> 2, never 3 (19 stays in the top-3)
+ROW_A = [20, 19, 21, 18, 22]
+ROW_B = [20, 21, 22]
+
+
+@pytest.mark.parametrize("row,required,step,hits,hops", [
+    (ROW_A, 1, 19, 1, 19), (ROW_A, 2, 20, 2, 20), (ROW_A, 3, 21, 3, 21),
+    (ROW_B, 1, 21, 1, 21), (ROW_B, 2, 22, 2, 22), (ROW_B, 3, -1, 2, 41),
+])
+def test_step_recall_stop(line40, row, required, step, hits, hops):
+    out = O.search_trace(line40, _q(120), 3, 64, early_exit=O.EXIT_NONE,
+                         step_recall=(np.array(row, np.int32), required))
+    assert out[3] == hops
+    assert out[5:] == (step, hits)
+
+
+def test_step_recall_after_gpruning(line40):
+    # gpruning (warmup 10, patience 8, k = 3): the last improvement is step 22
+    # (the 3rd distance, 576 -> 144), steps 23..30 count 1..8, so the query
+    # stops at step 30, before row B's 3 hits are ever reached: step -1 and the
+    # final hit count 2
+    out = O.search_trace(line40, _q(120), 3, 64, early_exit=O.EXIT_GPRUNING, warmup=10, patience=8,
+                         step_recall=(np.array(ROW_B, np.int32), 3))
+    assert out[3] == 30 and out[5:] == (-1, 2)
+
+
+def test_step_recall_batch_rows_and_width_one_only(line40):
+    # query i takes ground-truth row i % count
+    q = np.stack([_q(120), _q(120), _q(120)])
+    gt = np.array([ROW_A, ROW_B[:2] + [-1, -1, -1]], np.int32)
+    ids, _, _, hops, step, hits = O.search(line40, q, 3, 64, early_exit=O.EXIT_NONE, step_recall=(gt, 2))
+    assert list(step) == [20, 22, 20] and list(hits) == [2, 2, 2] and list(hops) == [20, 22, 20]
+    with pytest.raises(RuntimeError):
+        O.search(line40, q, 3, 64, pipe_width=2, early_exit=O.EXIT_NONE, step_recall=(gt, 2))
+
+
+def test_required_hits_known_values():
+    # search.cu:100-102 at the CLI's default threshold and k = 10
+    assert [O.required_hits(t, 10) for t in (0.9, 0.95, 1.0, 0.1, 0.01, 0.5)] == [9, 10, 10, 1, 1, 5]
