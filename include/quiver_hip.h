@@ -43,6 +43,11 @@ extern "C" {
 #define QV_ADMIT_STREAMING 0 /* window of num_blocks*Q + prefeed queries, as
                                 run_persistent_search (src/quiver/search.cu:827-1051) */
 #define QV_ADMIT_BATCH 1     /* every query admitted when the clock starts */
+#define QV_ADMIT_STATIC 2    /* sequential batches of num_blocks*Q queries, each
+                                admitted when the previous one has completed;
+                                a query's latency is its batch's wall time, as
+                                run_static_batch_search (src/quiver/search.cuh:
+                                68-95, search.cu:1703-1796) */
 
 /* Search kernel variants (no counterpart in the reference, whose one kernel
  * keeps a per-query LUT in shared memory).  Both give identical results. */

@@ -35,7 +35,8 @@ const char* kUsage =
     "  [--num-blocks 756] [--num-blocks-list L] [--pipe-width 2] [--queries-per-block 1]\n"
     "  [--poll-threads 6] [--runners-per-ssd 1] [--early-exit-policy gpruning|none]\n"
     "  [--result-prefix P] [--final-recall-csv F] [--skip-nav] [--help]\n"
-    "  [--per-step-recall [--recall-threshold 0.9] [--step-recall-csv quiver_step_recall.csv]]\n";
+    "  [--per-step-recall [--recall-threshold 0.9] [--step-recall-csv quiver_step_recall.csv]]\n"
+    "  [--static-batches]\n";
 
 bool parse_int(const std::string& s, int& out) {
   char* end = nullptr;
@@ -152,7 +153,7 @@ int main(int argc, char** argv) {
                                "--runners-per-ssd", "--num-blocks-list", "--recall-threshold",
                                "--step-recall-csv", "--final-recall-csv", "--result-prefix",
                                "--early-exit-policy", "--graph-placement", "--search-kernel"};
-  const char* bool_flags[] = {"--skip-nav", "--per-step-recall", "--help"};
+  const char* bool_flags[] = {"--skip-nav", "--per-step-recall", "--static-batches", "--help"};
   for (auto* s : value_flags) f[s] = Flag{};
   for (auto* s : bool_flags) f[s] = Flag{"", false, true};
   f["--topk"].value = "10";
@@ -339,6 +340,13 @@ int main(int argc, char** argv) {
     o.gpruning_patience = 8;
     o.skip_nav = f["--skip-nav"].used ? 1 : 0;
     o.kernel = kernel;
+    if (f["--static-batches"].used) {  // run_static_batch_search (search.cu:1703-1796)
+      o.admission = QV_ADMIT_STATIC;
+      const int64_t stride = (int64_t)nb * qpb;
+      std::cout << "[Quiver] StaticBatch: " << (nq + stride - 1) / stride << " batches of " << nb
+                << " blocks x Q=" << qpb << " = " << stride << " queries per batch, total " << nq << " queries"
+                << std::endl;
+    }
     if (const char* e = std::getenv("QUIVER_PREFEED")) o.prefeed = std::atoi(e);
     if (const char* e = std::getenv("QUIVER_ADMIT_MIN_BATCH")) o.admit_min_batch = std::max(1, std::atoi(e));
     std::vector<int32_t> sr_step, sr_hits;

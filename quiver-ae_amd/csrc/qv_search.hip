@@ -1543,7 +1543,10 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   const LaunchShape ls = shape_launch(lp, launched, ix->num_cus);
   const int grid = ls.grid;
   const int num_blocks = grid * ls.waves;  // query slots (waves) launched
-  const int max_inflight = (int)std::min<int64_t>(nq, slots + std::max(0, o.prefeed));
+  if (o.admission != QV_ADMIT_STREAMING && o.admission != QV_ADMIT_BATCH && o.admission != QV_ADMIT_STATIC)
+    fail(QV_EINVAL, "admission must be QV_ADMIT_STREAMING, QV_ADMIT_BATCH or QV_ADMIT_STATIC");
+  const int max_inflight = (int)std::min<int64_t>(
+      nq, o.admission == QV_ADMIT_STATIC ? slots : slots + std::max(0, o.prefeed));
   const bool use_bits = lp.variant == QV_KERNEL_LUT;
   if (use_bits) ensure_bits(ix, num_blocks);
 
@@ -1559,7 +1562,12 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
 
   HIP_OK(hipMemsetAsync(ix->d_counters, 0, 64, ix->stream));
   HIP_OK(hipStreamSynchronize(ix->stream));
-  const bool streaming = o.admission == QV_ADMIT_STREAMING;
+  // Static batches (StaticDispatch, search.cu:1703-1796): sequential batches of
+  // num_blocks x queries_per_block queries, each admitted once the previous
+  // one has completed; served by the same persistent launch, the host gating
+  // admission, instead of one launch per batch.
+  const bool static_batches = o.admission == QV_ADMIT_STATIC;
+  const bool streaming = o.admission == QV_ADMIT_STREAMING || static_batches;  // the host feeds tickets
   volatile int32_t* feed = ix->h_ctrl;
   volatile int32_t* term = ix->h_ctrl + 1;
   *feed = streaming ? 0 : (int32_t)nq;
@@ -1641,7 +1649,15 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     // admitted-but-unfinished queries; stamp each completion from the ring.
     std::vector<clock::time_point> admit((size_t)nq);
     lat_ms.assign((size_t)nq, 0.0);
-    int64_t fed = max_inflight;
+    const int64_t stride = static_batches ? std::min<int64_t>(nq, slots) : 0;
+    int64_t fed = static_batches ? stride : max_inflight;
+    int64_t batch_begin = 0;  // static batches: the batch in flight is [batch_begin, fed)
+    auto batch_t = t0;
+    // a static batch's queries all take its wall time as their latency (search.cu:1783-1788)
+    auto close_batch = [&](clock::time_point now) {
+      const double ms = std::chrono::duration<double, std::milli>(now - batch_t).count();
+      for (int64_t i = batch_begin; i < fed; i++) lat_ms[(size_t)i] = ms;
+    };
     for (int64_t i = 0; i < fed; i++) admit[(size_t)i] = t0;
     __atomic_store_n(ix->h_ctrl, (int32_t)fed, __ATOMIC_RELEASE);
     int64_t done = 0;
@@ -1657,7 +1673,17 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
         progressed = true;
       }
       const int64_t target = std::min<int64_t>(nq, done + max_inflight);
-      if (target > fed && (target - fed >= min_batch || target == nq || fed - done == 0)) {
+      if (static_batches) {
+        if (done == fed && fed < nq) {
+          const auto now = clock::now();
+          close_batch(now);
+          batch_begin = fed;
+          fed = std::min<int64_t>(nq, fed + stride);
+          batch_t = now;
+          for (int64_t i = batch_begin; i < fed; i++) admit[(size_t)i] = now;
+          __atomic_store_n(ix->h_ctrl, (int32_t)fed, __ATOMIC_RELEASE);
+        }
+      } else if (target > fed && (target - fed >= min_batch || target == nq || fed - done == 0)) {
         const auto now = clock::now();
         for (int64_t i = fed; i < target; i++) admit[(size_t)i] = now;
         fed = target;
@@ -1682,6 +1708,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
         }
       }
     }
+    if (static_batches && done == nq) close_batch(clock::now());
   }
   // Wait for the kernel, honouring the deadline.
   while (true) {

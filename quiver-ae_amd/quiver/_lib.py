@@ -30,6 +30,7 @@ QV_EXIT_NONE = 0
 QV_EXIT_GPRUNING = 2
 QV_ADMIT_STREAMING = 0
 QV_ADMIT_BATCH = 1
+QV_ADMIT_STATIC = 2
 QV_GRAPH_HBM = 0
 QV_GRAPH_HOST = 1
 QV_STREAM_READ_BLOCKS = 4096

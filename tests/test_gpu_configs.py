@@ -210,3 +210,36 @@ def test_c1_step_recall_matches_oracle(c1, threshold):
         np.testing.assert_array_equal(step, ostep)
         np.testing.assert_array_equal(hits, ohits)
         assert 0 < (step >= 0).sum() < n  # both outcomes occur
+
+
+@pytest.mark.parametrize("kernel", ["lut", "shared-pivots"])
+def test_c1_static_batches(c1, kernel):
+    """Static dispatch (run_static_batch_search, search.cu:1703-1796): batches
+    of num_blocks queries, each admitted when the previous has completed, every
+    query of a batch taking the batch's wall time as its latency; answers equal
+    the oracle's."""
+    lib, L = c1["lib"], c1["L"]
+    n, blocks = 1000, 64
+    _say(f"[gpu] C1 static batches kernel={kernel}")
+    o = lib.default_search_opts()
+    o.early_exit = lib.QV_EXIT_NONE
+    o.kernel = KERNEL[kernel]
+    o.num_blocks = blocks
+    o.admission = lib.QV_ADMIT_STATIC
+    q = np.ascontiguousarray(c1["q"][:n], np.float32)
+    ids = np.empty((n, K), np.int32)
+    dists = np.empty((n, K), np.float32)
+    found = np.empty(n, np.int32)
+    rep = lib.SearchReport()
+    lib.check(L.qv_search(c1["h"], q.ctypes.data, n, DIM, K, 128, C.byref(o), ids.ctypes.data,
+                          dists.ctypes.data, found.ctypes.data, C.byref(rep)))
+    hops = np.empty(n, np.int32)
+    lib.check(L.qv_last_hops(c1["h"], hops.ctypes.data, n))
+    _same((ids, dists, found, hops), _oracle(c1, 128, "none", n=n), f"static {kernel}")
+    assert rep.max_inflight == blocks
+    lat = np.empty(n, np.float64)
+    lib.check(L.qv_last_latencies(c1["h"], lat.ctypes.data, n))
+    batches = [lat[b:b + blocks] for b in range(0, n, blocks)]
+    assert len(batches) == 16
+    for bl in batches:
+        assert bl.min() == bl.max() > 0  # one wall time per batch
