@@ -458,6 +458,31 @@ def adc_leg(_lib, L, ncodes: int, log) -> dict:
     gms = float(np.median(gt[1:]))
     fold.close()
     log(f"gather alone: {gms:.3f} ms, {evals / gms / 1e6:.1f} G rows/s; ADC at {gms / ms:.1%} of that rate")
+    # the same number of uniformly random rows of 32, 64, 128 and 256 bytes from
+    # the same table: a rate that does not fall with the width means the gather
+    # pays per row, not per byte
+    fold = _lib.DeviceBuffer(evals * 16 // 256 * 4 + 4096)
+    widths = {}
+    for wb, sh in ((32, 0), (64, 1), (128, 2), (256, 3)):
+        ts = []
+        for _ in range(3):
+            wms = C.c_float()
+            _lib.check(L.qv_gather_rows_bench(codes.ptr, ncodes * M, wb, ids.ptr, evals, sh, fold.ptr, 0,
+                                              C.byref(wms)))
+            ts.append(wms.value)
+        wms = float(np.median(ts[1:]))
+        widths[wb] = {"ms": round(wms, 4), "rows_per_s": round(evals / (wms * 1e-3), 1),
+                      "gb_per_s": round(evals * wb / (wms * 1e-3) / 1e9, 1)}
+        log(f"random {wb:3d}-byte rows: {wms:.3f} ms, {evals / wms / 1e6:.1f} G rows/s, "
+            f"{evals * wb / wms / 1e6:.0f} GB/s")
+    fold.close()
+    rate32 = widths[32]["rows_per_s"]
+    # the widest row read at (within 15 % of) the 32-byte row rate: what one
+    # random 32-byte row occupies of the memory system
+    same_cost = max(wb for wb in widths if widths[wb]["rows_per_s"] >= 0.85 * rate32)
+    phys = evals * (same_cost + 4) + nq * M * 256 * 4
+    phys_gbs = phys / (ms * 1e-3) / 1e9
+    random_peak = max(v["gb_per_s"] for v in widths.values())
     # the whole code table read sequentially: the measured streaming-read peak
     fold = _lib.DeviceBuffer(_lib.QV_STREAM_READ_BLOCKS * 4)
     st = []
@@ -477,7 +502,12 @@ def adc_leg(_lib, L, ncodes: int, log) -> dict:
             "gather_alone_ms": round(gms, 4), "gather_alone_rows_per_s": round(evals / (gms * 1e-3), 1),
             "frac_of_gather_alone": round(gms / ms, 4),
             "stream_read_gbs": round(stream_gbs, 1),
-            "frac_of_stream_read": round(gbs / stream_gbs, 4)}
+            "frac_of_stream_read": round(gbs / stream_gbs, 4),
+            "random_row_widths": widths, "same_cost_row_bytes": same_cost,
+            "physical_bytes_per_launch": int(phys), "physical_gbs": round(phys_gbs, 1),
+            "physical_frac": round(phys_gbs / HBM_PEAK_GBS, 4),
+            "random_read_peak_gbs": random_peak,
+            "physical_frac_of_random_read_peak": round(phys_gbs / random_peak, 4)}
 
 
 def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, gpu_ids_all, gpu_dists_all, nq, seconds: float) -> dict:

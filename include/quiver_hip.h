@@ -323,6 +323,18 @@ int qv_adc_bench(const float* d_luts, int32_t num_chunks, const uint8_t* d_codes
 int qv_gather_bench(const uint8_t* d_rows, int64_t num_rows, const int32_t* d_ids,
                     int64_t n, uint32_t* d_fold, int device, float* elapsed_ms);
 
+/* The gather for rows of row_bytes (32, 64, 128 or 256) over one table of
+ * table_bytes (16-byte aligned): row i is d_table + (d_ids[i] >> id_shift) *
+ * row_bytes, clamped into the table; XOR-folded into d_fold[ceil(n *
+ * row_bytes / 16 / 256)].  With one id array and shifts 0, 1, 2, 3 the same
+ * number of uniformly random rows of 32 to 256 bytes are read from the same
+ * table, which tells a per-row cost from a per-byte one (no reference
+ * counterpart; a measurement aid).  elapsed_ms (may be NULL) receives the
+ * kernel time. */
+int qv_gather_rows_bench(const uint8_t* d_table, int64_t table_bytes, int32_t row_bytes,
+                         const int32_t* d_ids, int64_t n, int32_t id_shift, uint32_t* d_fold,
+                         int device, float* elapsed_ms);
+
 /* Sequential read of nbytes (a multiple of 16, 16-byte aligned) from d_src,
  * XOR-folded into d_fold[min(QV_STREAM_READ_BLOCKS, ceil(nbytes / 4096))] (no
  * reference counterpart; a measurement aid): the device's streaming read

@@ -262,6 +262,30 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint8_t* __restrict__
   if (threadIdx.x == 0) fold[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
 }
 
+// The same gather for rows of ROW bytes (ROW / 16 lanes per row, one 16-byte
+// piece each): row = id >> shift, clamped to the table, so one id array
+// addresses uniformly random rows of any width over one table.  Comparing
+// widths at the same row count separates a per-row cost from a per-byte one.
+template <int ROW>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint8_t* __restrict__ rows, int64_t last_row,
+                                                          const int32_t* __restrict__ ids, int64_t n, int shift,
+                                                          uint32_t* __restrict__ fold) {
+  constexpr int kLanes = ROW / 16;
+  __shared__ uint32_t part[4];
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t i = t / kLanes;
+  uint32_t x = 0;
+  if (i < n) {
+    const int64_t row = min((int64_t)(max(ids[i], 0) >> shift), last_row);
+    const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rows + row * ROW) + (t % kLanes));
+    x = a[0] ^ a[1] ^ a[2] ^ a[3];
+  }
+  for (int off = 32; off > 0; off >>= 1) x ^= (uint32_t)__shfl_xor((int)x, off);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) fold[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
+}
+
 // Streaming read of nwords 16-byte words (grid-stride, four loads in flight
 // per thread), XOR-folded into one word per workgroup: the device's sequential
 // read bandwidth, the measured counterpart of the nominal HBM peak.
@@ -425,6 +449,42 @@ int qv_gather_bench(const uint8_t* d_rows, int64_t num_rows, const int32_t* d_id
     HIP_OK(hipEventCreate(&e1));
     HIP_OK(hipEventRecord(e0, 0));
     hipLaunchKernelGGL(gather_kernel, dim3((unsigned)blocks), dim3(256), 0, 0, d_rows, num_rows - 1, d_ids, n, d_fold);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipEventRecord(e1, 0));
+    HIP_OK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (elapsed_ms) *elapsed_ms = ms;
+  });
+}
+
+int qv_gather_rows_bench(const uint8_t* d_table, int64_t table_bytes, int32_t row_bytes, const int32_t* d_ids,
+                         int64_t n, int32_t id_shift, uint32_t* d_fold, int device, float* elapsed_ms) {
+  return qv::guard([&] {
+    if (!d_table || !d_ids || !d_fold || n <= 0 || n > ((int64_t)1 << 34) || id_shift < 0 || id_shift > 30)
+      qv::fail(QV_EINVAL, "bad argument");
+    if (row_bytes != 32 && row_bytes != 64 && row_bytes != 128 && row_bytes != 256)
+      qv::fail(QV_EINVAL, "row_bytes must be 32, 64, 128 or 256");
+    if ((reinterpret_cast<uintptr_t>(d_table) & 15) != 0) qv::fail(QV_EINVAL, "table must be 16-byte aligned");
+    const int64_t num_rows = table_bytes / row_bytes;
+    if (num_rows < 1) qv::fail(QV_EINVAL, "table smaller than one row");
+    HIP_OK(hipSetDevice(device));
+    const int64_t blocks = (n * (row_bytes / 16) + 255) / 256;
+    if (blocks > INT32_MAX) qv::fail(QV_EINVAL, "too many rows");
+    hipEvent_t e0, e1;
+    HIP_OK(hipEventCreate(&e0));
+    HIP_OK(hipEventCreate(&e1));
+    HIP_OK(hipEventRecord(e0, 0));
+    auto launch = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, 0, d_table, num_rows - 1, d_ids, n, id_shift,
+                         d_fold);
+    };
+    if (row_bytes == 32) launch(gather_rows_kernel<32>);
+    else if (row_bytes == 64) launch(gather_rows_kernel<64>);
+    else if (row_bytes == 128) launch(gather_rows_kernel<128>);
+    else launch(gather_rows_kernel<256>);
     HIP_OK(hipGetLastError());
     HIP_OK(hipEventRecord(e1, 0));
     HIP_OK(hipEventSynchronize(e1));

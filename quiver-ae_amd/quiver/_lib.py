@@ -172,6 +172,7 @@ SIGNATURES = {
                             C.POINTER(C.c_float)]),
     "qv_gather_bench": (_I32, [_P, _I64, _P, _I64, _P, C.c_int, C.POINTER(C.c_float)]),
     "qv_stream_read_bench": (_I32, [_P, _I64, _P, C.c_int, C.POINTER(C.c_float)]),
+    "qv_gather_rows_bench": (_I32, [_P, _I64, _I32, _P, _I64, _I32, _P, C.c_int, C.POINTER(C.c_float)]),
     "qv_fill_uniform_bytes": (_I32, [_P, _I64, C.c_uint64, C.c_int]),
     "qv_fill_uniform_ids": (_I32, [_P, _I64, _I64, C.c_uint64, C.c_int]),
     "qv_build_params_default": (None, [C.POINTER(BuildParams)]),
