@@ -221,42 +221,183 @@ __device__ __forceinline__ float adc_sum(const CodeRow<MC>& cr, const float* __r
   return dist;
 }
 
+typedef float qv_float4 __attribute__((ext_vector_type(4)));
+
+// LDS reads of one group of four chunks (M0 .. M0 + 3, whose codes are the
+// bytes of the code word w) for adc_recompute<MC, 4>, in one block so that
+// the group costs one LDS round trip: per chunk, an SDWA shift (the source
+// operand selects the byte) makes the address 8 c of the pivot entry, whose
+// two halves one ds_read2st64_b64 reads at 4096 m and 4096 m + 2048 (offsets
+// 8 m and 8 m + 4 in 512-byte units) from the pivot table at LDS address 0;
+// the query chunks are broadcast reads at qa + 16 m.  The block ends with
+// its own wait, since the compiler does not count these reads.  dep is not
+// read: it orders the block after the previous group's arithmetic, so a
+// group's operands are the only ones held at a time.
+template <int M0>
+__device__ __forceinline__ void adc_group_reads(uint32_t w, uint32_t qa, float dep, qv_float4 (&pc)[4],
+                                                qv_float4 (&qq)[4]) {
+  static_assert(M0 % 4 == 0 && M0 + 3 < 32, "read2st64 offsets cover 32 chunks");
+  uint32_t a0, a1, a2, a3;
+  asm volatile(
+      "v_lshlrev_b32_sdwa %[a0], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0\n\t"
+      "v_lshlrev_b32_sdwa %[a1], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1\n\t"
+      "v_lshlrev_b32_sdwa %[a2], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2\n\t"
+      "v_lshlrev_b32_sdwa %[a3], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3\n\t"
+      "ds_read2st64_b64 %[p0], %[a0] offset0:%[o0] offset1:%[o0h]\n\t"
+      "ds_read2st64_b64 %[p1], %[a1] offset0:%[o1] offset1:%[o1h]\n\t"
+      "ds_read2st64_b64 %[p2], %[a2] offset0:%[o2] offset1:%[o2h]\n\t"
+      "ds_read2st64_b64 %[p3], %[a3] offset0:%[o3] offset1:%[o3h]\n\t"
+      "ds_read_b128 %[q0], %[qa] offset:%[qo0]\n\t"
+      "ds_read_b128 %[q1], %[qa] offset:%[qo1]\n\t"
+      "ds_read_b128 %[q2], %[qa] offset:%[qo2]\n\t"
+      "ds_read_b128 %[q3], %[qa] offset:%[qo3]\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : [a0] "=&v"(a0), [a1] "=&v"(a1), [a2] "=&v"(a2), [a3] "=&v"(a3), [p0] "=&v"(pc[0]), [p1] "=&v"(pc[1]),
+        [p2] "=&v"(pc[2]), [p3] "=&v"(pc[3]), [q0] "=&v"(qq[0]), [q1] "=&v"(qq[1]), [q2] "=&v"(qq[2]),
+        [q3] "=&v"(qq[3])
+      : [w] "v"(w), [qa] "v"(qa), [dep] "v"(dep), [o0] "i"(8 * M0), [o0h] "i"(8 * M0 + 4),
+        [o1] "i"(8 * M0 + 8), [o1h] "i"(8 * M0 + 12), [o2] "i"(8 * M0 + 16), [o2h] "i"(8 * M0 + 20),
+        [o3] "i"(8 * M0 + 24), [o3h] "i"(8 * M0 + 28), [qo0] "i"(16 * M0), [qo1] "i"(16 * M0 + 16),
+        [qo2] "i"(16 * M0 + 32), [qo3] "i"(16 * M0 + 48));
+}
+
+// Groups G .. MC/4 - 1 of adc_recompute<MC, 4>: dist += LUT[m][c_m] in chunk
+// order, each LUT entry the LUT build's fused chain from acc = 0.
+template <int G, int MC>
+__device__ __forceinline__ float adc_groups(const uint32_t* w, uint32_t qa, float dist) {
+  if constexpr (4 * G >= MC) {
+    return dist;
+  } else {
+    qv_float4 pc[4], qq[4];
+    adc_group_reads<4 * G>(w[G], qa, dist, pc, qq);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float acc = 0.f;
+      float d = qq[j].x - pc[j].x;
+      acc = __fmaf_rn(d, d, acc);
+      d = qq[j].y - pc[j].y;
+      acc = __fmaf_rn(d, d, acc);
+      d = qq[j].z - pc[j].z;
+      acc = __fmaf_rn(d, d, acc);
+      d = qq[j].w - pc[j].w;
+      acc = __fmaf_rn(d, d, acc);
+      dist += acc;
+    }
+    return adc_groups<G + 1, MC>(w, qa, dist);
+  }
+}
+
+typedef float qv_float2 __attribute__((ext_vector_type(2)));
+
+// The same for adc_recompute<MC, 2> (M0 + 3 < 48): the pivot entry of chunk m
+// (8 bytes at 2048 m + 8 c) is one ds_read_b64 from the address 8 c when its
+// offset fits the instruction's 16 bits (m < 32), else one ds_read2st64_b64
+// reading it twice (offsets 4 m in 512-byte units); the query chunks are two
+// broadcast reads of 16 bytes at qa + 8 m.
+template <int M0>
+__device__ __forceinline__ void adc_group_reads2(uint32_t w, uint32_t qa, float dep, qv_float2 (&pc)[4],
+                                                 qv_float4 (&qq)[2]) {
+  static_assert(M0 % 4 == 0 && M0 + 3 < 48, "chunks of two dimensions, M <= 48");
+  uint32_t a0, a1, a2, a3;
+  if constexpr (M0 < 32) {
+    asm volatile(
+        "v_lshlrev_b32_sdwa %[a0], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0\n\t"
+        "v_lshlrev_b32_sdwa %[a1], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1\n\t"
+        "v_lshlrev_b32_sdwa %[a2], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2\n\t"
+        "v_lshlrev_b32_sdwa %[a3], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3\n\t"
+        "ds_read_b64 %[p0], %[a0] offset:%[o0]\n\t"
+        "ds_read_b64 %[p1], %[a1] offset:%[o1]\n\t"
+        "ds_read_b64 %[p2], %[a2] offset:%[o2]\n\t"
+        "ds_read_b64 %[p3], %[a3] offset:%[o3]\n\t"
+        "ds_read_b128 %[q0], %[qa] offset:%[qo0]\n\t"
+        "ds_read_b128 %[q1], %[qa] offset:%[qo1]\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : [a0] "=&v"(a0), [a1] "=&v"(a1), [a2] "=&v"(a2), [a3] "=&v"(a3), [p0] "=&v"(pc[0]), [p1] "=&v"(pc[1]),
+          [p2] "=&v"(pc[2]), [p3] "=&v"(pc[3]), [q0] "=&v"(qq[0]), [q1] "=&v"(qq[1])
+        : [w] "v"(w), [qa] "v"(qa), [dep] "v"(dep), [o0] "i"(2048 * M0), [o1] "i"(2048 * (M0 + 1)),
+          [o2] "i"(2048 * (M0 + 2)), [o3] "i"(2048 * (M0 + 3)), [qo0] "i"(8 * M0), [qo1] "i"(8 * M0 + 16));
+  } else {
+    qv_float4 t0, t1, t2, t3;
+    asm volatile(
+        "v_lshlrev_b32_sdwa %[a0], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0\n\t"
+        "v_lshlrev_b32_sdwa %[a1], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1\n\t"
+        "v_lshlrev_b32_sdwa %[a2], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2\n\t"
+        "v_lshlrev_b32_sdwa %[a3], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3\n\t"
+        "ds_read2st64_b64 %[p0], %[a0] offset0:%[o0] offset1:%[o0]\n\t"
+        "ds_read2st64_b64 %[p1], %[a1] offset0:%[o1] offset1:%[o1]\n\t"
+        "ds_read2st64_b64 %[p2], %[a2] offset0:%[o2] offset1:%[o2]\n\t"
+        "ds_read2st64_b64 %[p3], %[a3] offset0:%[o3] offset1:%[o3]\n\t"
+        "ds_read_b128 %[q0], %[qa] offset:%[qo0]\n\t"
+        "ds_read_b128 %[q1], %[qa] offset:%[qo1]\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : [a0] "=&v"(a0), [a1] "=&v"(a1), [a2] "=&v"(a2), [a3] "=&v"(a3), [p0] "=&v"(t0), [p1] "=&v"(t1),
+          [p2] "=&v"(t2), [p3] "=&v"(t3), [q0] "=&v"(qq[0]), [q1] "=&v"(qq[1])
+        : [w] "v"(w), [qa] "v"(qa), [dep] "v"(dep), [o0] "i"(4 * M0), [o1] "i"(4 * (M0 + 1)),
+          [o2] "i"(4 * (M0 + 2)), [o3] "i"(4 * (M0 + 3)), [qo0] "i"(8 * M0), [qo1] "i"(8 * M0 + 16));
+    pc[0] = t0.xy;
+    pc[1] = t1.xy;
+    pc[2] = t2.xy;
+    pc[3] = t3.xy;
+  }
+}
+
+// Groups G .. MC/4 - 1 of adc_recompute<MC, 2>.
+template <int G, int MC>
+__device__ __forceinline__ float adc_groups2(const uint32_t* w, uint32_t qa, float dist) {
+  if constexpr (4 * G >= MC) {
+    return dist;
+  } else {
+    qv_float2 pc[4];
+    qv_float4 qq[2];
+    adc_group_reads2<4 * G>(w[G], qa, dist, pc, qq);
+    const float q[8] = {qq[0].x, qq[0].y, qq[0].z, qq[0].w, qq[1].x, qq[1].y, qq[1].z, qq[1].w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float acc = 0.f;
+      float d = q[2 * j] - pc[j].x;
+      acc = __fmaf_rn(d, d, acc);
+      d = q[2 * j + 1] - pc[j].y;
+      acc = __fmaf_rn(d, d, acc);
+      dist += acc;
+    }
+    return adc_groups2<G + 1, MC>(w, qa, dist);
+  }
+}
+
+// LDS float index of pivot dimension i for code c in the shared pivot table
+// of adc_recompute<MC, SC>:
+//  SC = 4: chunk m owns bytes [4096 m, 4096 (m + 1)); dims 0-1 of code c at
+//          4096 m + 8 c, dims 2-3 at 4096 m + 2048 + 8 c (adc_group_reads);
+//  SC = 2: entry (m, c) at float (m * 256 + c) * 2 (adc_group_reads2).
+template <int SC>
+__host__ __device__ __forceinline__ int piv_index(int i, int c) {
+  const int m = i / SC, j = i % SC;
+  if constexpr (SC == 4)
+    return m * 1024 + (j >> 1) * 512 + c * 2 + (j & 1);
+  else
+    return (m * 256 + c) * SC + j;
+}
+
 // The same ADC with every LUT entry recomputed from the pivots instead of
 // read from a per-query table: LUT[m][c] is the fused chain
 // acc = fma(q'_i - P[c][i], q'_i - P[c][i], acc) over the SC dims i of chunk m
 // from acc = 0 (the LUT build's own order), then dist += LUT[m][c] in chunk
-// order, so the result is the table ADC's bit for bit.  piv holds P
-// chunk-major, entry (m, c) at float (m * 256 + c) * SC (LDS, shared by the
-// waves of a workgroup); qv holds q' (LDS, read as broadcasts).
+// order, so the result is the table ADC's bit for bit.  piv holds P as
+// piv_index<SC> places it (LDS at address 0, shared by the waves of a
+// workgroup); qv holds q' (LDS, read as broadcasts).
 template <int MC, int SC>
 __device__ __forceinline__ float adc_recompute(const CodeRow<MC>& cr, const float* __restrict__ qv,
                                                const float* __restrict__ piv) {
+  // the pivot table sits at LDS address 0 (piv), the query at qv
+  (void)piv;
   float dist = 0.f;
-#pragma unroll
-  for (int m = 0; m < MC; m++) {
-    const uint32_t c = (cr.w[m >> 2] >> ((m & 3) * 8)) & 0xffu;
-    float acc = 0.f;
-    if constexpr (SC == 4) {
-      const float4 pc = reinterpret_cast<const float4*>(piv)[m * kPivots + c];
-      const float4 qq = *reinterpret_cast<const float4*>(qv + m * 4);
-      float d = qq.x - pc.x;
-      acc = __fmaf_rn(d, d, acc);
-      d = qq.y - pc.y;
-      acc = __fmaf_rn(d, d, acc);
-      d = qq.z - pc.z;
-      acc = __fmaf_rn(d, d, acc);
-      d = qq.w - pc.w;
-      acc = __fmaf_rn(d, d, acc);
-    } else {
-      static_assert(SC == 2, "chunks of 2 or 4 dimensions");
-      const float2 pc = reinterpret_cast<const float2*>(piv)[m * kPivots + c];
-      const float2 qq = *reinterpret_cast<const float2*>(qv + m * 2);
-      float d = qq.x - pc.x;
-      acc = __fmaf_rn(d, d, acc);
-      d = qq.y - pc.y;
-      acc = __fmaf_rn(d, d, acc);
-    }
-    dist += acc;
+  if constexpr (SC == 4) {
+    static_assert(MC % 4 == 0, "chunks in groups of four");
+    dist = adc_groups<0, MC>(cr.w, (uint32_t)(uintptr_t)qv, dist);
+  } else {
+    static_assert(SC == 2, "chunks of 2 or 4 dimensions");
+    static_assert(MC % 4 == 0, "chunks in groups of four");
+    dist = adc_groups2<0, MC>(cr.w, (uint32_t)(uintptr_t)qv, dist);
   }
   return dist;
 }
@@ -329,6 +470,18 @@ __device__ __forceinline__ void load_vec_pre(const uint8_t* __restrict__ rec, in
   for (int k = 0; k < kVecPre; k++) x[k] = elem_raw<T>(rec, min((lane & 31) + 32 * k, dim - 1));
 }
 
+// load_vec_pre for a dim KD known at compile time (a multiple of 32 up to
+// 32 kVecPre): element (lane & 31) + 32 k for each k with 32 k < KD, at the
+// lane's loop-invariant byte offset off = (lane & 31) sizeof(T) plus an
+// immediate, so a request costs no address arithmetic.
+template <class T, int KD>
+__device__ __forceinline__ void load_vec_pre_fixed(const uint8_t* __restrict__ rec, uint32_t off,
+                                                   uint32_t (&x)[kVecPre]) {
+  static_assert(KD % 32 == 0 && KD <= 32 * kVecPre, "whole 32-element rows");
+#pragma unroll
+  for (int k = 0; k < kVecPre; k++) x[k] = 32 * k < KD ? elem_raw<T>(rec + off, 32 * k) : 0u;
+}
+
 // Query elements lane + 32k (k < kVecPre) of the first 32 lanes, kept in
 // registers for the whole query (0 past dim).
 __device__ __forceinline__ void load_query_pre(const float* __restrict__ qu_lds, int dim, int lane,
@@ -359,6 +512,32 @@ __device__ __forceinline__ float exact_l2_pre(const uint32_t (&x)[kVecPre], cons
   if (lo) {
     for (int i = lane + 32 * kVecPre; i < dim; i += 32) {
       const float diff = qu_lds[i] - elem_to_float<T>(rec, i);
+      val = __fmaf_rn(diff, diff, val);
+    }
+  }
+  val += __uint_as_float(xor_lane32<16>(__float_as_uint(val), lane));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x108, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x104, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x102, 0xF, 0xF, false));
+  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x101, 0xF, 0xF, false));
+  return read_lane_f32(val, 0);
+}
+
+// exact_l2_pre for a dim KD known at compile time (a multiple of 32 up to
+// 32 kVecPre): lanes < 32 accumulate the same chain as exact_l2_pre without
+// its per-element tests (terms past KD would add fma(0, 0, val) = val), and
+// lanes >= 32 compute values that no step of the reduction carries into
+// lanes < 32 (the swizzle stays inside 32-lane halves, the row shifts inside
+// 16-lane rows), so lane 0 ends with the same sum bit for bit.
+template <class T, int KD>
+__device__ __forceinline__ float exact_l2_pre_fixed(const uint32_t (&x)[kVecPre], const float (&qv)[kVecPre],
+                                                    int lane) {
+  static_assert(KD % 32 == 0 && KD <= 32 * kVecPre, "whole 32-element rows");
+  float val = 0.f;
+#pragma unroll
+  for (int k = 0; k < kVecPre; k++) {
+    if (32 * k < KD) {
+      const float diff = qv[k] - raw_to_float<T>(x[k]);
       val = __fmaf_rn(diff, diff, val);
     }
   }

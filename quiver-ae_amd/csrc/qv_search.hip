@@ -192,6 +192,11 @@ struct Query {
   // dependent LDS binary search after the ADC but no memory traffic, which
   // pays when 8 to 16 queries per CU compete for the device's random accesses.
   static constexpr bool kBits = SC == 0;
+  // The shared-pivot kernels serve dim = MC SC only (uniform chunks).
+  static constexpr int kD = SC > 0 ? MC * SC : 0;
+  // Loop-invariant byte offsets of this lane's loads inside a record: its
+  // neighbour slot (past the degree word) and its first vector element.
+  uint32_t off_nbr, off_x;
 
   // smem: this query's LDS area; slot: this wave's bitmap index.
   __device__ Query(const SearchArgs& args, char* smem, const float* pivots_lds, int64_t slot)
@@ -206,6 +211,9 @@ struct Query {
     qu = reinterpret_cast<float*>(smem + pl.qu_off);
     beam = reinterpret_cast<uint64_t*>(smem + pl.beam_off);
     bits = kBits ? a.bits + slot * a.bits_words : nullptr;
+    const int lane = lane_id();
+    off_nbr = 4u * (uint32_t)(1 + min(lane, a.max_m - 1));  // lanes >= max_m are masked by the degree
+    off_x = (uint32_t)(lane & 31) * (uint32_t)sizeof(T);
   }
 
   __device__ __forceinline__ const uint8_t* record(int32_t v) const {
@@ -219,18 +227,25 @@ struct Query {
   // loads are used, so waits on LDS traffic never wait for these.
   __device__ __forceinline__ void fetch(int32_t v, int lane, NodeRec& nr) const {
     const uint8_t* rec = record(v);
-    const uint32_t* rec32 = reinterpret_cast<const uint32_t*>(rec + a.data_size);
-    int z = 0;
+    const uint8_t* nb = rec + a.data_size;
+    uint32_t z = 0;
     asm volatile("" : "+v"(z));  // per-lane address: a vector load of the degree
-    nr.deg = (int)rec32[z];
-    nr.nbr = rec32[1 + min(lane, a.max_m - 1)];  // lanes >= max_m are masked by the degree
-    load_vec_pre<T>(rec, a.dim, lane, nr.xv);
+    nr.deg = *reinterpret_cast<const int*>(nb + z);
+    nr.nbr = *reinterpret_cast<const uint32_t*>(nb + off_nbr);
+    if constexpr (kD > 0)
+      load_vec_pre_fixed<T, kD>(rec, off_x, nr.xv);
+    else
+      load_vec_pre<T>(rec, a.dim, lane, nr.xv);
   }
 
   // Exact distance of v and the top-k insert (the reference's second warp).
   __device__ __forceinline__ void exact_and_topk(int32_t v, const uint32_t (&xv)[kVecPre], const uint8_t* rec,
                                                  int lane) {
-    const float e = exact_l2_pre<T>(xv, quv, rec, qu, a.dim, lane);
+    float e;
+    if constexpr (kD > 0)
+      e = exact_l2_pre_fixed<T, kD>(xv, quv, lane);
+    else
+      e = exact_l2_pre<T>(xv, quv, rec, qu, a.dim, lane);
     last_e = e;
     const float dlast = read_lane_f32(td, a.topk - 1);
     if (fc < a.topk || e < dlast) topk_insert(td, ti, fc, a.topk, e, v);
@@ -240,8 +255,16 @@ struct Query {
   // followed by persistent_visit_select_dualwarp (kernel_helpers.cuh:422-489).
   // nr holds v's record (fetch); with PF the selected next node's record is
   // requested into nr as soon as it is known.  Returns the next node or -1.
+  //
+  // With PF, cr carries code rows from one hop to the next: when `have`, cr
+  // holds (or is loading) v's neighbours' rows, requested by the previous hop.
+  // A hop that guesses its successor (the beam's first unvisited entry, spec)
+  // requests that node's record at its start and, once the ADC no longer
+  // needs cr, that node's code rows, so the next hop's rows are in flight
+  // through this hop's merge; `have` is set when the guess was the node
+  // selected.  Only loads move: every result is the same.
   template <bool PF>
-  __device__ __forceinline__ int32_t hop(int32_t v, NodeRec& nr) {
+  __device__ __forceinline__ int32_t hop(int32_t v, NodeRec& nr, CodeRow<MC>& cr, bool& have) {
     const int lane = opaque_lane();
     const int deg = read_lane_i32(nr.deg, 0);
     evals += deg;
@@ -250,7 +273,7 @@ struct Query {
     uint32_t xv[kVecPre];
 #pragma unroll
     for (int k = 0; k < kVecPre; k++) xv[k] = nr.xv[k];
-    const uint8_t* rec = a.dim > 32 * kVecPre ? record(v) : nullptr;
+    const uint8_t* rec = kD == 0 && a.dim > 32 * kVecPre ? record(v) : nullptr;
     // With PF, the next node is most often the beam's first unvisited entry
     // (whenever no new candidate beats it), so its record is requested right
     // after this hop's code rows, and the merge only requests another record
@@ -272,8 +295,7 @@ struct Query {
     // a neighbour read code row 0 and discard the sum.
     float d;
     if constexpr (MC > 0 && MC % 16 == 0) {
-      CodeRow<MC> cr;
-      adc_load<MC>(cr, a.codes, nbr);
+      if (!(PF && have)) adc_load<MC>(cr, a.codes, nbr);
       // Issued on every hop (v's own record when there is no unvisited entry
       // to guess), so every path reaches the ADC with the same loads in
       // flight and the compiler's wait for the code rows can leave the
@@ -284,6 +306,13 @@ struct Query {
         d = adc_recompute<MC, SC>(cr, qc, piv);
       else
         d = adc_sum<MC>(cr, lut);
+      // the guessed successor's code rows (lanes past its degree read row 0)
+      if constexpr (PF) {
+        if (spec) {
+          const int ndeg = read_lane_i32(nr.deg, 0);
+          adc_load<MC>(cr, a.codes, lane < ndeg ? nr.nbr : 0u);
+        }
+      }
     } else {
       if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
       d = adc_row<MC>(a.codes + (int64_t)nbr * a.num_chunks, lut, a.num_chunks);
@@ -291,7 +320,10 @@ struct Query {
     }
     const uint64_t nkey = has ? make_key(d, nbr, false) : sentinel_key(lane);
     const bool fresh = kBits ? has && !((bword >> (nbr & 31)) & 1u) : has;
-    return merge_select<PF>(nkey, fresh, lane, nr, spec);
+    bool hit = false;
+    const int32_t nx = merge_select<PF>(nkey, fresh, lane, nr, spec, hit);
+    if constexpr (PF) have = MC > 0 && MC % 16 == 0 && hit;
+    return nx;
   }
 
   // Without the bitmap, every LDS beam position from sz to cap holds kPadKey
@@ -314,9 +346,17 @@ struct Query {
       if (m) first = min(first, (__ffsll((long long)m) - 1) * Q + k);
     }
     u = first;
-    // (the LDS beam is current: written before the register copy was reloaded,
-    // or by mark_visited; one broadcast read instead of 2 Q lane reads)
-    bu = first < sz ? beam[first] : ~0ull;
+    // its key from the register copy: slot first % Q of lane first / Q
+    // (wave-uniform, so the next node's record address is scalar work)
+    if (first < sz) {
+      const int kk = first % Q;
+      uint64_t e = ck[0];
+#pragma unroll
+      for (int k = 1; k < Q; k++) e = kk == k ? ck[k] : e;
+      bu = read_lane_u64(e, first / Q);
+    } else {
+      bu = ~0ull;
+    }
   }
 
   // Marks the entry at position pos visited (LDS and registers).
@@ -349,8 +389,11 @@ struct Query {
   // requested (PF) before the rest of the merge, which then overlaps that load,
   // unless it is the first unvisited entry whose record the hop requested at
   // its start (spec).
+  // hit: (PF) the selected node is the guessed one, whose record the hop
+  // requested at its start.
   template <bool PF>
-  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool fresh, int lane, NodeRec& nr, bool spec) {
+  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool fresh, int lane, NodeRec& nr, bool spec,
+                                                  bool& hit) {
     const int ef = a.ef;
     // Candidates at or above the last entry of a full beam end beyond ef.
     const uint64_t last = sz >= ef ? beam[ef - 1] : ~0ull;
@@ -359,22 +402,33 @@ struct Query {
     bool valid = below;
     if constexpr (!kBits) {
       if (__ballot(below)) {
-        // r = #{beam entries e : e < (nkey & ~1)} by binary lifting over the
+        // r = #{beam entries e : e < (nkey & ~1)} by a 4-ary search over the
         // LDS beam: sorted, kPadKey from sz to its capacity cap (>= ef), so
         // a read clamped to cap - 1 sees either a key of the beam or kPadKey
         // (a below candidate is under the last key of a full beam, so even a
-        // full-capacity beam never lifts r past it).  Steps are uniform and
-        // cover 64 Q >= cap positions.
+        // full-capacity beam never lifts r past it).  A level of step s reads
+        // r + s - 1, r + 2 s - 1 and r + 3 s - 1 at once (one LDS round trip)
+        // and adds s per key below; steps 4^i from kTop cover 4 kTop - 1 >=
+        // 64 Q - 1 positions.  The last level (s = 1) also reads r + 3, so
+        // beam[r] for the membership test is one of its four keys.
         constexpr int kCap = Q * kWave;
-        constexpr int kTop = kCap >= 256 ? 256 : (kCap >= 128 ? 128 : 64);
+        constexpr int kTop = kCap <= 64 ? 16 : (kCap <= 256 ? 64 : 256);
         const int top = cap - 1;
         const uint64_t c0 = nkey & ~1ull;
 #pragma unroll
-        for (int step = kTop; step > 0; step >>= 1) {
-          const uint64_t e = beam[min(r + step - 1, top)];
-          r += e < c0 ? step : 0;
+        for (int step = kTop; step > 1; step >>= 2) {
+          const uint64_t e1 = beam[min(r + step - 1, top)];
+          const uint64_t e2 = beam[min(r + 2 * step - 1, top)];
+          const uint64_t e3 = beam[min(r + 3 * step - 1, top)];
+          r += ((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * step;
         }
-        const uint64_t at = beam[min(r, top)];
+        const uint64_t e0 = beam[min(r, top)];
+        const uint64_t e1 = beam[min(r + 1, top)];
+        const uint64_t e2 = beam[min(r + 2, top)];
+        const uint64_t e3 = beam[min(r + 3, top)];
+        const int n = (e0 < c0 ? 1 : 0) + (e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0);
+        r += n;
+        const uint64_t at = n == 0 ? e0 : (n == 1 ? e1 : (n == 2 ? e2 : e3));
         valid = below && (at >> 1) != (nkey >> 1);
       }
     }
@@ -402,7 +456,8 @@ struct Query {
     }
     if constexpr (PF) {
       // (the key test, not the position: a winning candidate lands at u too)
-      if (!(spec && selkey == bu)) fetch((int32_t)key_id(selkey), lane, nr);
+      hit = spec && selkey == bu;
+      if (!hit) fetch((int32_t)key_id(selkey), lane, nr);
     }
     if (vm == 0) {
       mark_visited(selpos, selkey, lane);
@@ -617,9 +672,11 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     };
 
     NodeRec nr;
+    CodeRow<MC> cr;
+    bool have = false;
     auto expand = [&](int32_t v) -> int32_t {
       Qy.fetch(v, lane, nr);
-      return Qy.template hop<false>(v, nr);
+      return Qy.template hop<false>(v, nr, cr, have);
     };
 
     if (a.pipe_w == 1) {
@@ -629,7 +686,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       Qy.fetch(entry, lane, nr);
       int32_t v = entry;
       while (true) {
-        const int32_t nx = Qy.template hop<true>(v, nr);
+        const int32_t nx = Qy.template hop<true>(v, nr, cr, have);
         log_hop(v);
         ++step;
         if (check()) {
@@ -741,10 +798,10 @@ template <class T, int Q, int MC, int SC>
 __global__ __launch_bounds__(1024) void search_kernel_sp(SearchArgs a) {
   extern __shared__ __align__(16) char smem[];
   float* piv = reinterpret_cast<float*>(smem);
-  // pivots_t is [dim][256]; dim i = m SC + j of code c goes to (m 256 + c) SC + j
+  // pivots_t is [dim][256]; dim i of code c goes where adc_recompute reads it
   for (int idx = threadIdx.x; idx < a.dim * kPivots; idx += blockDim.x) {
     const int i = idx >> 8, c = idx & (kPivots - 1);
-    piv[((i / SC) * kPivots + c) * SC + i % SC] = a.pivots_t[idx];
+    piv[piv_index<SC>(i, c)] = a.pivots_t[idx];
   }
   __syncthreads();
   const int w = threadIdx.x / kWave;
@@ -1331,8 +1388,14 @@ static int occupancy(int device, int lds_cu, KernelFn k, int waves, int lds) {
   const auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   const auto any = cache.lower_bound(std::make_tuple(device, f, INT32_MIN, INT32_MIN));
-  if (any == cache.end() || std::get<0>(any->first) != device || std::get<1>(any->first) != f)
+  if (any == cache.end() || std::get<0>(any->first) != device || std::get<1>(any->first) != f) {
     HIP_OK(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, std::max(lds_cu, 65536)));
+    // The shared-pivot ADC addresses the pivot table at LDS address 0: the
+    // search kernels keep all their LDS dynamic, so it starts there.
+    hipFuncAttributes fa{};
+    HIP_OK(hipFuncGetAttributes(&fa, f));
+    if (fa.sharedSizeBytes != 0) fail(QV_EHIP, "search kernel has static LDS; the pivot table must start at 0");
+  }
   int nb = 0;
   HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, kWave * waves, (size_t)lds));
   cache.emplace(key, nb);
