@@ -25,7 +25,7 @@ extern "C" {
 #define QV_EIO -2         /* file missing, short or malformed */
 #define QV_EHIP -3        /* HIP runtime error */
 #define QV_ETIMEDOUT -4   /* search exceeded qv_search_opts.timeout_s */
-#define QV_EUNSUPPORTED -5/* feature this library does not implement (SPDK, R > 64, ...) */
+#define QV_EUNSUPPORTED -5/* feature this library does not implement (SPDK, R > 128, ...) */
 #define QV_ENOMEM -6      /* host or device allocation failed */
 #define QV_EINDEX -7      /* index content invalid (ids out of range, ...) */
 

@@ -322,7 +322,7 @@ void build_index_cpu(const void* base, int dtype, int64_t n, int dim,
   qv_build_params prm = prm_in;
   if (prm.threads <= 0) prm.threads = omp_get_num_procs();
   if (n <= 1 || n > (int64_t)INT32_MAX) fail(QV_EINVAL, "n must be in [2, 2^31)");
-  if (prm.R <= 0 || prm.R > kMaxDegree) fail(QV_EINVAL, "R must be in [1, 64]");
+  if (prm.R <= 0 || prm.R > kMaxDegree) fail(QV_EINVAL, "R must be in [1, 128]");
   if (prm.L < prm.R) fail(QV_EINVAL, "L must be >= R");
   Base B{static_cast<const uint8_t*>(base), dtype, n, dim};
 

@@ -1352,7 +1352,7 @@ int qv_build_index_gpu(const void* d_base, int32_t data_type, int64_t n, int32_t
     qv_build_params p;
     qv_build_params_default(&p);
     if (params) p = *params;
-    if (p.R <= 0 || p.R > kMaxDegree) qv::fail(QV_EINVAL, "R must be in [1, 64]");
+    if (p.R <= 0 || p.R > kMaxBuildDegree) qv::fail(QV_EINVAL, "R must be in [1, 64]");
     if (p.L < p.R) qv::fail(QV_EINVAL, "L must be >= R");
     HIP_OK(hipSetDevice(device));
     if (data_type == QV_UINT8)

@@ -44,774 +44,16 @@
 using namespace qv;
 using namespace qv::dev;
 
+#include "qv_search_kernels.hpp"
+
+using namespace qv::sk;
+
 namespace {
-
-struct SearchArgs {
-  // index (HBM)
-  const uint8_t* pages;
-  const uint8_t* codes;
-  const float* centroid;
-  const float* pivots_t;
-  const int32_t* chunk_off;
-  int64_t num_points;
-  int64_t nodes_per_page;
-  uint64_t npp_magic;              // page = (v * npp_magic) >> npp_shift, exact for 0 <= v < 2^31
-  int32_t npp_shift;
-  int64_t node_size;
-  int64_t data_size;
-  int32_t dim;
-  int32_t num_chunks;
-  int32_t max_m;
-  int32_t medoid;
-  // queries / params
-  const float* queries;
-  int32_t nq;
-  int32_t topk;
-  int32_t ef;
-  int32_t pipe_w;
-  int32_t early_exit;
-  int32_t warmup;
-  int32_t patience;
-  // outputs (device)
-  int32_t* out_ids;
-  float* out_dists;
-  int32_t* out_found;
-  int32_t* out_hops;
-  int32_t* out_stopped;
-  int32_t* out_evals;              // neighbour distance evaluations per query
-  uint64_t* t_start;
-  uint64_t* t_end;
-  // dispatch
-  int32_t* counters;               // [0] next ticket, [1] done count, [2] error bits
-  const int32_t* feed_count;       // host-coherent, may be null (then nq)
-  const int32_t* terminate;        // host-coherent, may be null
-  int32_t* ring;                   // host-coherent completion ring, may be null
-  uint64_t spin_limit_ticks;       // watchdog on feed waits (100 MHz ticks)
-  // navigation graph for the per-query entry node (nav_data null: the medoid)
-  const uint8_t* nav_data;
-  const int32_t* nav_graph;
-  const int32_t* nav_map;
-  int64_t nav_nodes;
-  int32_t nav_max_m;
-  int32_t nav_start;
-  // optional record of expanded nodes (graph construction)
-  int32_t* rec_ids;
-  float* rec_dists;
-  int32_t rec_cap;
-  // per-slot beam membership bitmaps of the per-query-LUT kernel (bit v set
-  // <=> v in the beam), bits_words 32-bit words per slot, zero between queries
-  uint32_t* bits;
-  int64_t bits_words;
-  // per-step recall (pipe width 1): query q stops once sr_required of its
-  // top-k ids appear in ground-truth row q % sr_count (sr_width <= 256 ids);
-  // sr_gt null: off
-  const int32_t* sr_gt;
-  int32_t sr_width;
-  int32_t sr_count;
-  int32_t sr_required;
-  int32_t* sr_step;                // [nq] step at which it was reached, -1 if never
-  int32_t* sr_hits;                // [nq] hits then (else at the end)
-};
-
-enum : int32_t { kErrSpinTimeout = 1 };
-
-// Dynamic LDS carve-up of one query (one wave), shared by the kernel and its
-// launcher.  Q = beam positions per lane: the register beam holds Q * 64 >= ef
-// entries, the LDS beam cap of them (beam_cap).  With a per-query LUT (lut) the
-// table comes first; the shared-
-// pivot kernel has none, and when every query element the exact distance
-// needs fits the lanes' registers (dim <= 32 kVecPre) its beam overlays the
-// query copy qu, which is only read once, into those registers, before the
-// first hop.
-struct LdsPlan {
-  int lut_off, qc_off, qu_off, beam_off, total;
-};
-
-// LDS beam entries: Q * 64 with the per-query LUT (its table, not the beam,
-// limits the queries per CU); ef rounded up to 8 with shared pivots, where the
-// beam's LDS decides how many queries a CU holds.
-__host__ __device__ inline int beam_cap(int ef, int Q, bool lut) { return lut ? Q * kWave : (ef + 7) & ~7; }
-
-__host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool lut, int ef) {
-  LdsPlan p;
-  p.lut_off = 0;
-  p.qc_off = p.lut_off + (lut ? num_chunks * kPivots * 4 : 0);
-  const int dpad = (dim + 3) & ~3;
-  p.qu_off = p.qc_off + dpad * 4;
-  const bool overlay = !lut && dim <= 32 * kVecPre;
-  p.beam_off = overlay ? p.qu_off : (p.qu_off + dpad * 4 + 15) & ~15;
-  const int beam_bytes = beam_cap(ef, Q, lut) * 8;
-  p.total = p.beam_off + (overlay && dpad * 4 > beam_bytes ? dpad * 4 : beam_bytes);
-  return p;
-}
-
-// Shared-pivot kernel: the PQ pivots chunk-major, [chunk m][code c][SC dims]
-// (entry (m, c) at float (m * 256 + c) * SC), ahead of the per-wave query
-// areas.  The SC floats one LUT entry needs are one aligned vector read, and
-// lanes reading different codes of one chunk hit consecutive 4 SC-byte slots,
-// so rows need no padding against bank conflicts.
-__host__ __device__ inline int piv_bytes(int dim) { return kPivots * dim * 4; }
-
-// Registers holding the start of a node record (see Query::fetch).
-struct NodeRec {
-  int deg;
-  uint32_t nbr;
-  uint32_t xv[kVecPre];  // raw vector elements (load_vec_pre)
-};
-
-// SC = 0: per-query LUT in LDS; SC > 0: LUT entries recomputed from the
-// shared pivots (chunks of SC dimensions).
-template <class T, int Q, int MC, int SC>
-struct Query {
-  const SearchArgs& a;
-  float* lut;
-  const float* piv;  // shared pivots (SC > 0)
-  float* qc;
-  float* qu;
-  float quv[kVecPre];  // qu elements of this lane for the exact distance
-  uint64_t* beam;
-  uint32_t* bits;  // this slot's membership bitmap (SC == 0)
-  int sz;        // beam size (ctx.size)
-  int cap;       // LDS beam entries (beam_cap >= ef)
-  // The beam in registers, chunk-major (lane l holds positions [l Q, l Q + Q),
-  // kPadKey at and beyond sz), and its first unvisited entry u with key bu
-  // (INT32_MAX and ~0 when every entry is visited).  LDS holds the same beam
-  // for the scatter of each merge.
-  uint64_t ck[Q];
-  int u;
-  uint64_t bu;
-  float td;      // top-k entry of this lane
-  int32_t ti;
-  int fc;        // found count
-  int evals;     // ADC evaluations so far
-  float last_e;  // exact distance of the node expanded by the last hop
-
-  // Membership test: a bitmap in HBM (SC == 0), else the rank in the LDS
-  // beam.  The bitmap costs a random read per neighbour but nothing on the
-  // hop's critical path (the read overlaps the code rows); the rank costs a
-  // dependent LDS binary search after the ADC but no memory traffic, which
-  // pays when 8 to 16 queries per CU compete for the device's random accesses.
-  static constexpr bool kBits = SC == 0;
-  // The shared-pivot kernels serve dim = MC SC only (uniform chunks).
-  static constexpr int kD = SC > 0 ? MC * SC : 0;
-  // Loop-invariant byte offsets of this lane's loads inside a record: its
-  // neighbour slot (past the degree word) and its first vector element.
-  uint32_t off_nbr, off_x;
-
-  // smem: this query's LDS area; slot: this wave's bitmap index.
-  __device__ Query(const SearchArgs& args, char* smem, const float* pivots_lds, int64_t slot)
-      : a(args), piv(pivots_lds), sz(0), u(INT32_MAX), bu(~0ull), td(__int_as_float(0x7f800000)), ti(-1), fc(0),
-        evals(0) {
-#pragma unroll
-    for (int k = 0; k < Q; k++) ck[k] = kPadKey;
-    LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, SC == 0, a.ef);
-    cap = beam_cap(a.ef, Q, SC == 0);
-    lut = reinterpret_cast<float*>(smem + pl.lut_off);
-    qc = reinterpret_cast<float*>(smem + pl.qc_off);
-    qu = reinterpret_cast<float*>(smem + pl.qu_off);
-    beam = reinterpret_cast<uint64_t*>(smem + pl.beam_off);
-    bits = kBits ? a.bits + slot * a.bits_words : nullptr;
-    const int lane = lane_id();
-    off_nbr = 4u * (uint32_t)(1 + min(lane, a.max_m - 1));  // lanes >= max_m are masked by the degree
-    off_x = (uint32_t)(lane & 31) * (uint32_t)sizeof(T);
-  }
-
-  __device__ __forceinline__ const uint8_t* record(int32_t v) const {
-    const int64_t page = (int64_t)(((uint64_t)(uint32_t)v * a.npp_magic) >> a.npp_shift);
-    const int64_t slot = (int64_t)v - page * a.nodes_per_page;
-    return a.pages + page * 4096 + slot * a.node_size;
-  }
-
-  // Requests the parts of v's record a hop reads: degree, the max_m neighbour
-  // slots (inside the record) and the first vector elements.  Only vector
-  // loads are used, so waits on LDS traffic never wait for these.
-  __device__ __forceinline__ void fetch(int32_t v, int lane, NodeRec& nr) const {
-    const uint8_t* rec = record(v);
-    const uint8_t* nb = rec + a.data_size;
-    uint32_t z = 0;
-    asm volatile("" : "+v"(z));  // per-lane address: a vector load of the degree
-    nr.deg = *reinterpret_cast<const int*>(nb + z);
-    nr.nbr = *reinterpret_cast<const uint32_t*>(nb + off_nbr);
-    if constexpr (kD > 0)
-      load_vec_pre_fixed<T, kD>(rec, off_x, nr.xv);
-    else
-      load_vec_pre<T>(rec, a.dim, lane, nr.xv);
-  }
-
-  // Exact distance of v and the top-k insert (the reference's second warp).
-  __device__ __forceinline__ void exact_and_topk(int32_t v, const uint32_t (&xv)[kVecPre], const uint8_t* rec,
-                                                 int lane) {
-    float e;
-    if constexpr (kD > 0)
-      e = exact_l2_pre_fixed<T, kD>(xv, quv, lane);
-    else
-      e = exact_l2_pre<T>(xv, quv, rec, qu, a.dim, lane);
-    last_e = e;
-    const float dlast = read_lane_f32(td, a.topk - 1);
-    if (fc < a.topk || e < dlast) topk_insert(td, ti, fc, a.topk, e, v);
-  }
-
-  // One expansion of node v: persistent_merge_data (kernel_helpers.cuh:232-357)
-  // followed by persistent_visit_select_dualwarp (kernel_helpers.cuh:422-489).
-  // nr holds v's record (fetch); with PF the selected next node's record is
-  // requested into nr as soon as it is known.  Returns the next node or -1.
-  //
-  // With PF, cr carries code rows from one hop to the next: when `have`, cr
-  // holds (or is loading) v's neighbours' rows, requested by the previous hop.
-  // A hop that guesses its successor (the beam's first unvisited entry, spec)
-  // requests that node's record at its start and, once the ADC no longer
-  // needs cr, that node's code rows, so the next hop's rows are in flight
-  // through this hop's merge; `have` is set when the guess was the node
-  // selected.  Only loads move: every result is the same.
-  template <bool PF>
-  __device__ __forceinline__ int32_t hop(int32_t v, NodeRec& nr, CodeRow<MC>& cr, bool& have) {
-    const int lane = opaque_lane();
-    const int deg = read_lane_i32(nr.deg, 0);
-    evals += deg;
-    const bool has = lane < deg;
-    const uint32_t nbr = has ? nr.nbr : 0u;
-    uint32_t xv[kVecPre];
-#pragma unroll
-    for (int k = 0; k < kVecPre; k++) xv[k] = nr.xv[k];
-    const uint8_t* rec = kD == 0 && a.dim > 32 * kVecPre ? record(v) : nullptr;
-    // With PF, the next node is most often the beam's first unvisited entry
-    // (whenever no new candidate beats it), so its record is requested right
-    // after this hop's code rows, and the merge only requests another record
-    // when a candidate wins.
-    const bool spec = PF && u < sz;
-
-    // Beam membership of each neighbour from the bitmap.  The bitmap updates
-    // of the previous hop were issued before this hop's record arrived;
-    // waiting for every outstanding vector memory operation here (the record
-    // is complete by now) orders them before these reads, which bypass the
-    // vector L1.
-    uint32_t bword = 0;
-    if constexpr (kBits) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      bword = __hip_atomic_load(bits + (nbr >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // ADC gather-sum over the neighbour's code row (LUT in LDS); the code rows
-    // are in flight while the exact distance of v is computed.  Lanes without
-    // a neighbour read code row 0 and discard the sum.
-    float d;
-    if constexpr (MC > 0 && MC % 16 == 0) {
-      if (!(PF && have)) adc_load<MC>(cr, a.codes, nbr);
-      // Issued on every hop (v's own record when there is no unvisited entry
-      // to guess), so every path reaches the ADC with the same loads in
-      // flight and the compiler's wait for the code rows can leave the
-      // record outstanding.
-      if constexpr (PF) fetch(spec ? (int32_t)key_id(bu) : v, lane, nr);
-      exact_and_topk(v, xv, rec, lane);
-      if constexpr (SC > 0)
-        d = adc_recompute<MC, SC>(cr, qc, piv);
-      else
-        d = adc_sum<MC>(cr, lut);
-      // the guessed successor's code rows (lanes past its degree read row 0)
-      if constexpr (PF) {
-        if (spec) {
-          const int ndeg = read_lane_i32(nr.deg, 0);
-          adc_load<MC>(cr, a.codes, lane < ndeg ? nr.nbr : 0u);
-        }
-      }
-    } else {
-      if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
-      d = adc_row<MC>(a.codes + (int64_t)nbr * a.num_chunks, lut, a.num_chunks);
-      exact_and_topk(v, xv, rec, lane);
-    }
-    const uint64_t nkey = has ? make_key(d, nbr, false) : sentinel_key(lane);
-    const bool fresh = kBits ? has && !((bword >> (nbr & 31)) & 1u) : has;
-    bool hit = false;
-    const int32_t nx = merge_select<PF>(nkey, fresh, lane, nr, spec, hit);
-    if constexpr (PF) have = MC > 0 && MC % 16 == 0 && hit;
-    return nx;
-  }
-
-  // Without the bitmap, every LDS beam position from sz to cap holds kPadKey
-  // (above every key): set once per query; merges only write below the new
-  // sz, which never shrinks.  The rank search then needs no bounds test.
-  __device__ __forceinline__ void pad_beam(int lane) {
-    if constexpr (!kBits) {
-#pragma unroll
-      for (int k = 0; k < Q; k++)
-        if (k * kWave + lane < cap) beam[k * kWave + lane] = kPadKey;
-    }
-  }
-
-  // First unvisited entry of the beam from the register copy.
-  __device__ __forceinline__ void find_unvisited(int lane) {
-    int first = INT32_MAX;
-#pragma unroll
-    for (int k = 0; k < Q; k++) {
-      const uint64_t m = __ballot(lane * Q + k < sz && key_unvisited(ck[k]));
-      if (m) first = min(first, (__ffsll((long long)m) - 1) * Q + k);
-    }
-    u = first;
-    // its key from the register copy: slot first % Q of lane first / Q
-    // (wave-uniform, so the next node's record address is scalar work)
-    if (first < sz) {
-      const int kk = first % Q;
-      uint64_t e = ck[0];
-#pragma unroll
-      for (int k = 1; k < Q; k++) e = kk == k ? ck[k] : e;
-      bu = read_lane_u64(e, first / Q);
-    } else {
-      bu = ~0ull;
-    }
-  }
-
-  // Marks the entry at position pos visited (LDS and registers).
-  __device__ __forceinline__ void mark_visited(int pos, uint64_t key, int lane) {
-    if (lane == 0) beam[pos] = key & ~1ull;
-#pragma unroll
-    for (int k = 0; k < Q; k++) ck[k] &= lane * Q + k == pos ? ~1ull : ~0ull;
-  }
-
-  // persistent_merge_data's result after persistent_visit_select_dualwarp's
-  // compaction and truncation (kernel_helpers.cuh:288-357, 440-472), built by
-  // rank.  The reference places a candidate equal to a beam entry (same id,
-  // hence same distance) right after it (lower_bound + 1, :300-329) and the
-  // adjacent-id compaction then drops it; the min(sz + deg, 2 ef) cap (:350)
-  // only removes entries that sit at or beyond ef after compaction, since at
-  // most sz <= ef entries are compacted away.  So the new beam is the first ef
-  // entries of  beam  U  {candidates whose id is not in the beam}, in key
-  // order, and its first unvisited entry is taken and marked visited.
-  // fresh: lane holds a neighbour, not in the beam by the bitmap (kBits).
-  //
-  // Without the bitmap: a neighbour whose id is in the beam has that entry's
-  // key (the ADC of one code row against one query is one value), visited
-  // bit aside.  So the lower bound r of (c & ~1) in the sorted beam is both
-  // the candidate's rank and its membership test: c is in the beam iff
-  // beam[r] and c differ only in the visited bit.  Only neighbours below the
-  // end of a full beam need it.
-  //
-  // The selected node only depends on the smallest surviving candidate and
-  // the old first unvisited entry, so it is found first and its record is
-  // requested (PF) before the rest of the merge, which then overlaps that load,
-  // unless it is the first unvisited entry whose record the hop requested at
-  // its start (spec).
-  // hit: (PF) the selected node is the guessed one, whose record the hop
-  // requested at its start.
-  template <bool PF>
-  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool fresh, int lane, NodeRec& nr, bool spec,
-                                                  bool& hit) {
-    const int ef = a.ef;
-    // Candidates at or above the last entry of a full beam end beyond ef.
-    const uint64_t last = sz >= ef ? beam[ef - 1] : ~0ull;
-    const bool below = fresh && nkey < last;
-    int r = 0;  // rank in the beam (valid lanes)
-    bool valid = below;
-    if constexpr (!kBits) {
-      if (__ballot(below)) {
-        // r = #{beam entries e : e < (nkey & ~1)} by a 4-ary search over the
-        // LDS beam: sorted, kPadKey from sz to its capacity cap (>= ef), so
-        // a read clamped to cap - 1 sees either a key of the beam or kPadKey
-        // (a below candidate is under the last key of a full beam, so even a
-        // full-capacity beam never lifts r past it).  A level of step s reads
-        // r + s - 1, r + 2 s - 1 and r + 3 s - 1 at once (one LDS round trip)
-        // and adds s per key below; steps 4^i from kTop cover 4 kTop - 1 >=
-        // 64 Q - 1 positions.  The last level (s = 1) also reads r + 3, so
-        // beam[r] for the membership test is one of its four keys.
-        constexpr int kCap = Q * kWave;
-        constexpr int kTop = kCap <= 64 ? 16 : (kCap <= 256 ? 64 : 256);
-        const int top = cap - 1;
-        const uint64_t c0 = nkey & ~1ull;
-#pragma unroll
-        for (int step = kTop; step > 1; step >>= 2) {
-          const uint64_t e1 = beam[min(r + step - 1, top)];
-          const uint64_t e2 = beam[min(r + 2 * step - 1, top)];
-          const uint64_t e3 = beam[min(r + 3 * step - 1, top)];
-          r += ((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * step;
-        }
-        const uint64_t e0 = beam[min(r, top)];
-        const uint64_t e1 = beam[min(r + 1, top)];
-        const uint64_t e2 = beam[min(r + 2, top)];
-        const uint64_t e3 = beam[min(r + 3, top)];
-        const int n = (e0 < c0 ? 1 : 0) + (e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0);
-        r += n;
-        const uint64_t at = n == 0 ? e0 : (n == 1 ? e1 : (n == 2 ? e2 : e3));
-        valid = below && (at >> 1) != (nkey >> 1);
-      }
-    }
-    const uint64_t vm = __ballot(valid);
-
-    if (vm == 0 && u >= sz) return -1;
-    // Smallest surviving candidate and its rank in the beam (with the bitmap:
-    // entries below it by ballots against the register beam, visited bit
-    // ignored: e < c iff e < (c & ~1)).
-    int selpos = u;
-    uint64_t selkey = bu;
-    if (vm != 0) {
-      const uint64_t kv0 = wave_min_u64(valid ? nkey : ~0ull);
-      if (kv0 < bu) {
-        if constexpr (kBits) {
-          int r0 = 0;
-#pragma unroll
-          for (int k = 0; k < Q; k++) r0 += __popcll(__ballot(ck[k] < (kv0 & ~1ull)));
-          selpos = r0;
-        } else {
-          selpos = read_lane_i32(r, __ffsll((long long)__ballot(valid && nkey == kv0)) - 1);
-        }
-        selkey = kv0;
-      }
-    }
-    if constexpr (PF) {
-      // (the key test, not the position: a winning candidate lands at u too)
-      hit = spec && selkey == bu;
-      if (!hit) fetch((int32_t)key_id(selkey), lane, nr);
-    }
-    if (vm == 0) {
-      mark_visited(selpos, selkey, lane);
-      find_unvisited(lane);
-      return (int32_t)key_id(selkey);
-    }
-
-    // For each surviving candidate c (few per hop: most neighbours below the
-    // beam's end are already in it): its rank t among the candidates and the
-    // shift of every old entry at or above its rank in the beam.
-    int t = 0;
-    uint32_t sh[Q];
-#pragma unroll
-    for (int k = 0; k < Q; k++) sh[k] = 0u;
-    for (uint64_t rest = vm; rest; rest &= rest - 1) {
-      const int l = __ffsll((long long)rest) - 1;
-      const uint64_t c = read_lane_u64(nkey, l);
-      int rc;
-      if constexpr (kBits) {
-        rc = 0;
-#pragma unroll
-        for (int k = 0; k < Q; k++) rc += __popcll(__ballot(ck[k] < (c & ~1ull)));
-        if (lane == l) r = rc;
-      } else {
-        rc = read_lane_i32(r, l);
-      }
-      t += c < nkey ? 1 : 0;
-#pragma unroll
-      for (int k = 0; k < Q; k++) sh[k] += lane * Q + k >= rc ? 1u : 0u;
-    }
-
-    // Scatter in place; entries pushed to ef or beyond drop out (and leave
-    // the bitmap), inserted candidates join it.
-#pragma unroll
-    for (int k = 0; k < Q; k++) {
-      const int pos = lane * Q + k;
-      const int g = pos + (int)sh[k];
-      if (pos < sz) {
-        if (g < ef) {
-          beam[g] = g == selpos ? (ck[k] & ~1ull) : ck[k];
-        } else if constexpr (kBits) {
-          const uint32_t id = key_id(ck[k]);
-          atomicAnd(bits + (id >> 5), ~(1u << (id & 31)));
-        }
-      }
-    }
-    const int f = r + t;
-    if (valid && f < ef) {
-      beam[f] = f == selpos ? (nkey & ~1ull) : nkey;
-      if constexpr (kBits) {
-        const uint32_t id = key_id(nkey);
-        atomicOr(bits + (id >> 5), 1u << (id & 31));
-      }
-    }
-    sz = min(sz + (int)__popcll(vm), ef);
-    // Register copy of the new beam (the wave's LDS accesses complete in order).
-#pragma unroll
-    for (int k = 0; k < Q; k++) {
-      const int pos = lane * Q + k;
-      ck[k] = pos < sz ? beam[pos] : kPadKey;
-    }
-    find_unvisited(lane);
-    return (int32_t)key_id(selkey);
-  }
-
-  // Clears the bitmap bits of the final beam (bitmaps are zero between queries).
-  __device__ __forceinline__ void clear_bits(int lane) {
-    if constexpr (kBits) {
-#pragma unroll
-      for (int k = 0; k < Q; k++) {
-        const int pos = lane * Q + k;
-        if (pos < sz) {
-          const uint32_t id = key_id(ck[k]);
-          atomicAnd(bits + (id >> 5), ~(1u << (id & 31)));
-        }
-      }
-    }
-  }
-
-  // persistent_select_next_no_compact (kernel_helpers.cuh:491-518): the first
-  // unvisited entry (the beam never exceeds ef here) is taken and marked.
-  __device__ __forceinline__ int32_t select_next_no_compact() {
-    const int lane = opaque_lane();
-    if (u >= sz) return -1;
-    const uint64_t sel = bu;
-    mark_visited(u, sel, lane);
-    find_unvisited(lane);
-    return (int32_t)key_id(sel);
-  }
-};
-
-// gpruning bookkeeping (kernel_q1.cuh:294-315, 524-545).
-struct GPrune {
-  int no_improve = 0, last_fc = 0;
-  float last_top1 = __int_as_float(0x7f800000), last_topk = __int_as_float(0x7f800000);
-};
-
-// Orders a query's LDS set-up before its reads: a workgroup barrier when the
-// workgroup is the query's one wave, a compiler fence otherwise (a wave's LDS
-// accesses complete in order).
-template <int SC>
-__device__ __forceinline__ void query_sync() {
-  if constexpr (SC == 0)
-    __syncthreads();
-  else
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-}
-
-// The persistent query loop of one wave: smem is its LDS area, piv the
-// shared pivots (SC > 0), slot its bitmap index (SC == 0).
-template <class T, int Q, int MC, int SC>
-__device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, const float* piv, int64_t slot) {
-  const int lane = lane_id();
-
-  while (true) {
-    // ---- acquire (StreamingDispatch, src/quiver/kernel_core/policies/dispatch.cuh:39-79)
-    int32_t qid = -1;
-    if (lane == 0) {
-      qid = atomicAdd(&a.counters[0], 1);
-      if (qid >= a.nq) {
-        qid = -1;
-      } else if (a.terminate &&
-                 __hip_atomic_load(a.terminate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
-        qid = -1;
-      } else if (a.feed_count) {
-        const uint64_t t0 = wall_ticks();
-        while (qid >= __hip_atomic_load(a.feed_count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM)) {
-          if (a.terminate &&
-              __hip_atomic_load(a.terminate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
-            qid = -1;
-            break;
-          }
-          if (wall_ticks() - t0 > a.spin_limit_ticks) {
-            atomicOr(&a.counters[2], kErrSpinTimeout);
-            qid = -1;
-            break;
-          }
-          __builtin_amdgcn_s_sleep(4);
-        }
-      }
-    }
-    qid = read_lane_i32(qid, 0);
-    if (qid < 0) break;
-    if (a.t_start && lane == 0) a.t_start[qid] = wall_ticks();
-
-    Query<T, Q, MC, SC> Qy(a, smem, piv, slot);
-    const float* q = a.queries + (int64_t)qid * a.dim;
-    // ---- entry node: the nav-graph search on the raw query when a nav graph is
-    // loaded (kernel_q1.cuh:148-174, 199-206), else the medoid.
-    const int32_t entry = a.nav_data ? nav_entry<T>(q, a.nav_data, a.nav_graph, a.nav_map, a.nav_nodes, a.dim,
-                                                    a.nav_max_m, a.nav_start, (int32_t)a.medoid)
-                                     : a.medoid;
-    // ---- query into LDS: q - mu for the LUT, fl(fl(q - mu) + mu) for the exact
-    // distance (pq_device.cuh:18-20, 33-35).
-    for (int i = lane; i < a.dim; i += kWave) {
-      const float c = q[i] - a.centroid[i];
-      Qy.qc[i] = c;
-      Qy.qu[i] = c + a.centroid[i];
-    }
-    query_sync<SC>();
-    if constexpr (SC == 0) {
-      build_lut_lds(Qy.qc, a.pivots_t, a.chunk_off, a.num_chunks, Qy.lut);
-      query_sync<SC>();
-    }
-    load_query_pre(Qy.qu, a.dim, lane, Qy.quv);
-    // qu may share its LDS with the beam (lds_plan): no beam store may move
-    // above these reads.
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    Qy.pad_beam(lane);
-
-    GPrune g;
-    int step = 0;
-    bool stop = false;
-    const bool gpr = a.early_exit == QV_EXIT_GPRUNING;
-    auto check = [&]() -> bool {
-      const float top1 = read_lane_f32(Qy.td, 0);
-      const float topk = read_lane_f32(Qy.td, a.topk - 1);
-      const int fc = read_lane_i32(Qy.fc, 0);  // equal in every lane; read as uniform
-      const bool improved = fc > g.last_fc || top1 < g.last_top1 || topk < g.last_topk;
-      if (step < a.warmup) g.no_improve = 0;
-      else g.no_improve = improved ? 0 : g.no_improve + 1;
-      g.last_fc = fc;
-      g.last_top1 = top1;
-      g.last_topk = topk;
-      return gpr && step >= a.warmup && a.patience > 0 && g.no_improve >= a.patience;
-    };
-
-    // count_topk_gt_hits (kernel_helpers.cuh:520-535): top-k entries (a
-    // repeated id counted each time, -1 padding skipped) found anywhere in the
-    // query's ground-truth row, read four ids per lane.
-    const bool sr = a.sr_gt != nullptr;
-    int sr_at = -1, sr_h = 0;
-    auto sr_hits = [&]() -> int {
-      const int32_t* row = a.sr_gt + (int64_t)(qid % a.sr_count) * a.sr_width;
-      int32_t g[4];
-#pragma unroll
-      for (int t = 0; t < 4; t++) g[t] = lane + kWave * t < a.sr_width ? row[lane + kWave * t] : -1;
-      int hits = 0;
-      for (int i = 0; i < a.topk; i++) {
-        const int32_t id = read_lane_i32(Qy.ti, i);
-        if (id < 0) continue;
-        hits += __ballot(g[0] == id || g[1] == id || g[2] == id || g[3] == id) != 0 ? 1 : 0;
-      }
-      return hits;
-    };
-
-    auto log_hop = [&](int32_t v) {
-      if (a.rec_ids && lane == 0 && step < a.rec_cap) {
-        a.rec_ids[(int64_t)qid * a.rec_cap + step] = v;
-        a.rec_dists[(int64_t)qid * a.rec_cap + step] = Qy.last_e;
-      }
-    };
-
-    NodeRec nr;
-    CodeRow<MC> cr;
-    bool have = false;
-    auto expand = [&](int32_t v) -> int32_t {
-      Qy.fetch(v, lane, nr);
-      return Qy.template hop<false>(v, nr, cr, have);
-    };
-
-    if (a.pipe_w == 1) {
-      // One pipe lane (kernel_q1.cuh:199-397 boot, then 407-670): the node a
-      // hop selects is the next one expanded, so its record is requested while
-      // the hop finishes.
-      Qy.fetch(entry, lane, nr);
-      int32_t v = entry;
-      while (true) {
-        const int32_t nx = Qy.template hop<true>(v, nr, cr, have);
-        log_hop(v);
-        ++step;
-        if (check()) {
-          stop = true;
-          break;
-        }
-        // per-step recall, after the early-exit test (kernel_q1.cuh:354-364)
-        if (sr) {
-          const int h = sr_hits();
-          if (h >= a.sr_required) {
-            sr_at = step;
-            sr_h = h;
-            stop = true;
-            break;
-          }
-        }
-        if (nx < 0) break;
-        v = nx;
-      }
-      goto finish;
-    }
-    {
-    // ---- boot (kernel_q1.cuh:199-397)
-    int32_t first = expand(entry);
-    log_hop(entry);
-    step = 1;
-    if (check()) {
-      stop = true;
-      first = -1;
-    }
-    // Lane w < W of pipe_node holds the node of pipe lane w (-1: idle).  The
-    // pipe state stays in registers: no LDS round trip and no barrier, whose
-    // memory fence would also wait for the record requested by the last hop.
-    const int W = a.pipe_w;
-    int32_t pipe_node = lane == 0 ? first : -1;
-    for (int w = 1; w < W; w++) {
-      const int32_t nx = Qy.select_next_no_compact();
-      pipe_node = lane == w ? nx : pipe_node;
-    }
-    uint32_t ready = stop ? 0u : (uint32_t)__ballot(lane < W && pipe_node != -1);
-
-    // ---- pipe loop, every issued lane served at once (kernel_q1.cuh:407-670)
-    while (!stop && ready) {
-      const uint32_t cur = ready;
-      for (int w = 0; w < W; w++) {
-        if (!(cur & (1u << w))) continue;
-        const int32_t v = read_lane_i32(pipe_node, w);
-        int32_t nx = expand(v);
-        log_hop(v);
-        ++step;
-        if (check()) {
-          stop = true;
-          nx = -1;
-        }
-        pipe_node = lane == w ? nx : pipe_node;
-      }
-      if (stop) break;
-      for (int w = 0; w < W; w++) {
-        if (cur & (1u << w)) continue;
-        const int32_t nx = Qy.select_next_no_compact();
-        pipe_node = lane == w ? nx : pipe_node;
-      }
-      ready = (uint32_t)__ballot(lane < W && pipe_node != -1);
-    }
-    }
-
-  finish:
-    // ---- finish (kernel_q1.cuh:662-704)
-    if (sr) {
-      if (sr_at < 0) sr_h = sr_hits();
-      if (lane == 0) {
-        a.sr_step[qid] = sr_at;
-        a.sr_hits[qid] = sr_h;
-      }
-    }
-    Qy.clear_bits(lane);
-    if (lane < a.topk) {
-      a.out_ids[(int64_t)qid * a.topk + lane] = Qy.ti;
-      a.out_dists[(int64_t)qid * a.topk + lane] = Qy.td;
-    }
-    if (lane == 0) {
-      if (a.out_found) a.out_found[qid] = Qy.fc;
-      if (a.out_hops) a.out_hops[qid] = step;
-      if (a.out_stopped) a.out_stopped[qid] = stop ? 1 : 0;
-      if (a.out_evals) a.out_evals[qid] = Qy.evals;
-      if (a.t_end) a.t_end[qid] = wall_ticks();
-      atomicAdd(&a.counters[1], 1);
-      if (a.ring) {
-        const int32_t pos = atomicAdd(&a.counters[3], 1);
-        __hip_atomic_store(&a.ring[pos], qid + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-      }
-    }
-    query_sync<SC>();
-  }
-}
-
-// One query per workgroup of one wave, its LUT in LDS.
-template <class T, int Q, int MC>
-__global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
-  extern __shared__ __align__(16) char smem[];
-  run_queries<T, Q, MC, 0>(a, smem, nullptr, blockIdx.x);
-}
-
-// One workgroup per CU, one query per wave: the workgroup holds the pivots
-// once and every wave recomputes the LUT entries it needs (chunks of SC
-// dimensions), so the CU's LDS serves more queries than with a 32 KB LUT per
-// query.
-template <class T, int Q, int MC, int SC>
-__global__ __launch_bounds__(1024) void search_kernel_sp(SearchArgs a) {
-  extern __shared__ __align__(16) char smem[];
-  float* piv = reinterpret_cast<float*>(smem);
-  // pivots_t is [dim][256]; dim i of code c goes where adc_recompute reads it
-  for (int idx = threadIdx.x; idx < a.dim * kPivots; idx += blockDim.x) {
-    const int i = idx >> 8, c = idx & (kPivots - 1);
-    piv[piv_index<SC>(i, c)] = a.pivots_t[idx];
-  }
-  __syncthreads();
-  const int w = threadIdx.x / kWave;
-  const LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, false, a.ef);
-  run_queries<T, Q, MC, SC>(a, smem + piv_bytes(a.dim) + w * pl.total, piv, 0);
-}
 
 // Graph check run once at open: degree <= R, neighbour ids < n, no duplicate id
 // inside one adjacency list (the reference's merge-path sort assumes distinct
-// keys, kernel_helpers.cuh:300-329).  One wave per node.
+// keys, kernel_helpers.cuh:300-329).  One wave per node; with R > 64 lane l
+// also holds slot l + 64, and each id is compared with every later one.
 __global__ __launch_bounds__(256) void validate_kernel(const uint8_t* pages, int64_t n,
                                                        int64_t npp, int64_t node_size,
                                                        int64_t data_size, int R,
@@ -823,17 +65,27 @@ __global__ __launch_bounds__(256) void validate_kernel(const uint8_t* pages, int
     const int64_t page = v / npp;
     const uint8_t* rec = pages + page * 4096 + (v - page * npp) * node_size;
     const uint32_t* r32 = reinterpret_cast<const uint32_t*>(rec + data_size);
-    const uint32_t deg = r32[0];
+    const uint32_t deg = (uint32_t)__builtin_amdgcn_readfirstlane((int)r32[0]);
     int32_t bits = 0;
     if (deg > (uint32_t)R) bits |= 1;
     const uint32_t lim = deg < (uint32_t)R ? deg : (uint32_t)R;
     const bool has = (uint32_t)lane < lim;
     const uint32_t nb = has ? r32[1 + lane] : 0u;
     if (has && (int64_t)nb >= n) bits |= 2;
-    uint64_t key = has ? (uint64_t)nb : ((1ull << 32) + (uint64_t)lane);
-    key = wave_sort_desc(key);
-    const uint64_t up = ((uint64_t)lane_up1_u32((uint32_t)(key >> 32)) << 32) | lane_up1_u32((uint32_t)key);
-    if (lane > 0 && up == key) bits |= 4;
+    if (R <= kWave) {
+      uint64_t key = has ? (uint64_t)nb : ((1ull << 32) + (uint64_t)lane);
+      key = wave_sort_desc(key);
+      const uint64_t up = ((uint64_t)lane_up1_u32((uint32_t)(key >> 32)) << 32) | lane_up1_u32((uint32_t)key);
+      if (lane > 0 && up == key) bits |= 4;
+    } else {
+      const bool has2 = (uint32_t)(lane + kWave) < lim;
+      const uint32_t nb2 = has2 ? r32[1 + kWave + lane] : 0u;
+      if (has2 && (int64_t)nb2 >= n) bits |= 2;
+      for (uint32_t j = 0; j < lim; j++) {
+        const uint32_t b = j < (uint32_t)kWave ? read_lane_u32(nb, (int)j) : read_lane_u32(nb2, (int)j - kWave);
+        if ((has && (uint32_t)lane > j && nb == b) || (has2 && (uint32_t)(lane + kWave) > j && nb2 == b)) bits |= 4;
+      }
+    }
     const uint64_t any = __ballot(bits != 0);
     if (any) {
       int32_t all = bits;
@@ -846,13 +98,14 @@ __global__ __launch_bounds__(256) void validate_kernel(const uint8_t* pages, int
   }
 }
 
-using KernelFn = void (*)(SearchArgs);
-
+// Kernels of this translation unit: one neighbour per lane (R <= 64) and up
+// to 7 beam positions per lane (ef <= 448); the others come from
+// qv_search_r128.hip and qv_search_deep.hip.
 template <class T, int Q>
 KernelFn pick_mc(int M) {
-  if (M == 32) return search_kernel<T, Q, 32>;
-  if (M == 48) return search_kernel<T, Q, 48>;
-  return search_kernel<T, Q, 0>;
+  if (M == 32) return search_kernel<T, Q, 32, 1>;
+  if (M == 48) return search_kernel<T, Q, 48, 1>;
+  return search_kernel<T, Q, 0, 1>;
 }
 
 template <class T>
@@ -863,23 +116,33 @@ KernelFn pick_q(int Q, int M) {
   return pick_mc<T, 7>(M);
 }
 
-KernelFn pick_kernel(int dtype, int Q, int M) {
-  if (dtype == QV_UINT8) return pick_q<uint8_t>(Q, M);
-  if (dtype == QV_INT8) return pick_q<int8_t>(Q, M);
-  return pick_q<float>(Q, M);
+KernelFn pick_kernel(int dtype, int Q, int M, int npl) {
+  KernelFn k = nullptr;
+  if (npl > 1)
+    k = pick_kernel_r128(dtype, Q, M);
+  else if (Q > 7)
+    k = pick_kernel_deep(dtype, Q, M);
+  else if (dtype == QV_UINT8)
+    k = pick_q<uint8_t>(Q, M);
+  else if (dtype == QV_INT8)
+    k = pick_q<int8_t>(Q, M);
+  else
+    k = pick_q<float>(Q, M);
+  if (!k) fail(QV_EUNSUPPORTED, "no search kernel for this degree and ef");
+  return k;
 }
 
 // Shared-pivot kernels: M = 32 chunks of 4 dimensions, M = 48 chunks of 2.
 template <class T, int MC, int SC>
 KernelFn pick_sp_q(int Q) {
   switch (Q) {
-    case 1: return search_kernel_sp<T, 1, MC, SC>;
-    case 2: return search_kernel_sp<T, 2, MC, SC>;
-    case 3: return search_kernel_sp<T, 3, MC, SC>;
-    case 4: return search_kernel_sp<T, 4, MC, SC>;
-    case 5: return search_kernel_sp<T, 5, MC, SC>;
-    case 6: return search_kernel_sp<T, 6, MC, SC>;
-    default: return search_kernel_sp<T, 7, MC, SC>;
+    case 1: return search_kernel_sp<T, 1, MC, SC, 1>;
+    case 2: return search_kernel_sp<T, 2, MC, SC, 1>;
+    case 3: return search_kernel_sp<T, 3, MC, SC, 1>;
+    case 4: return search_kernel_sp<T, 4, MC, SC, 1>;
+    case 5: return search_kernel_sp<T, 5, MC, SC, 1>;
+    case 6: return search_kernel_sp<T, 6, MC, SC, 1>;
+    default: return search_kernel_sp<T, 7, MC, SC, 1>;
   }
 }
 
@@ -888,20 +151,39 @@ KernelFn pick_sp_t(int Q, int M) {
   return M == 32 ? pick_sp_q<T, 32, 4>(Q) : pick_sp_q<T, 48, 2>(Q);
 }
 
-KernelFn pick_kernel_sp(int dtype, int Q, int M) {
-  if (dtype == QV_UINT8) return pick_sp_t<uint8_t>(Q, M);
-  if (dtype == QV_INT8) return pick_sp_t<int8_t>(Q, M);
-  return pick_sp_t<float>(Q, M);
+KernelFn pick_kernel_sp(int dtype, int Q, int M, int npl) {
+  KernelFn k = nullptr;
+  if (npl > 1)
+    k = pick_kernel_sp_r128(dtype, Q, M);
+  else if (Q > 7)
+    k = pick_kernel_sp_deep(dtype, Q, M);
+  else if (dtype == QV_UINT8)
+    k = pick_sp_t<uint8_t>(Q, M);
+  else if (dtype == QV_INT8)
+    k = pick_sp_t<int8_t>(Q, M);
+  else
+    k = pick_sp_t<float>(Q, M);
+  if (!k) fail(QV_EUNSUPPORTED, "no shared-pivot kernel for this degree and ef");
+  return k;
 }
 
-// Beam positions per lane for ef (beam capacity 64 Q >= ef; kMaxEf = 448 = 64 * 7).
-// The per-query-LUT kernel comes in Q = 1, 2, 4, 7 (its 32 KB LUT, not the
-// beam, sets how many queries a CU holds); the shared-pivot kernel in every Q
-// from 1 to 7 (its LDS beam holds ef rounded up to 8 entries, and that decides
-// how many queries a CU holds: at d = 128, 16 up to ef = 192, then 15 at 208,
-// 13 at 240, 12 at 256, 11 at 288, 10 at 320, 9 at 384, 8 at 448).
-int beam_chunks(int ef) { return ef <= 64 ? 1 : (ef <= 128 ? 2 : (ef <= 256 ? 4 : 7)); }
-int beam_chunks_sp(int ef) { return (std::max(ef, 1) + kWave - 1) / kWave; }
+// Beam positions per lane for ef (beam capacity 64 Q >= ef; kMaxEf = 1024 = 64 * 16).
+// The per-query-LUT kernel comes in Q = 1, 2, 4, 7, 10, 16 (its 32 KB LUT, not
+// the beam, sets how many queries a CU holds); the shared-pivot kernel in
+// every Q from 1 to 7, then 10 and 16 (its LDS beam holds ef rounded up to 8
+// entries, and that decides how many queries a CU holds: at d = 128, 16 up to
+// ef = 192, then 15 at 208, 13 at 240, 12 at 256, 11 at 288, 10 at 320, 9 at
+// 384, 8 at 448, 7 at 512 and 3 at 1024).
+int beam_chunks(int ef) {
+  return ef <= 64 ? 1 : (ef <= 128 ? 2 : (ef <= 256 ? 4 : (ef <= 448 ? 7 : (ef <= 640 ? 10 : 16))));
+}
+int beam_chunks_sp(int ef) {
+  const int q = (std::max(ef, 1) + kWave - 1) / kWave;
+  return q <= 7 ? q : (q <= 10 ? 10 : 16);
+}
+
+// Neighbour slots per lane for an index of max degree R.
+int slots_per_lane(int64_t R) { return R <= kWave ? 1 : 2; }
 
 // A search launch: kernel, workgroup size (waves = queries per workgroup),
 // dynamic LDS and the query slots (waves) one CU holds.
@@ -1198,7 +480,7 @@ qv_index* open_index(const std::string& index_dir, const std::string& dtype_s,
     fail(QV_EIO, "PQ point count " + std::to_string(pq.num_pts) + " != index point count " +
                      std::to_string(lay.num_data));
   if (lay.max_m0 > kMaxDegree || lay.max_m0 < 1)
-    fail(QV_EUNSUPPORTED, "max degree " + std::to_string(lay.max_m0) + " outside [1, 64]");
+    fail(QV_EUNSUPPORTED, "max degree " + std::to_string(lay.max_m0) + " outside [1, 128]");
   if ((lay.data_size & 3) || (lay.node_size & 3))
     fail(QV_EUNSUPPORTED, "node records must be 4-byte aligned");
   if (lay.num_data > INT32_MAX) fail(QV_EUNSUPPORTED, "more than 2^31-1 points");
@@ -1260,7 +542,7 @@ qv_index* index_from_memory(const qv_index_info& li, const uint8_t* pages, const
   if (lay.num_dims <= 0 || lay.data_size != lay.num_dims * elem_size(lay.data_type))
     fail(QV_EINDEX, "data_size must be num_dims x the element size");
   if (lay.max_m0 > kMaxDegree || lay.max_m0 < 1)
-    fail(QV_EUNSUPPORTED, "max degree " + std::to_string(lay.max_m0) + " outside [1, 64]");
+    fail(QV_EUNSUPPORTED, "max degree " + std::to_string(lay.max_m0) + " outside [1, 128]");
   if (lay.node_size != lay.data_size + 4 + 4 * lay.max_m0)
     fail(QV_EINDEX, "node_size must be data_size + 4 + 4 max_m0");
   if ((lay.data_size & 3) || (lay.node_size & 3)) fail(QV_EUNSUPPORTED, "node records must be 4-byte aligned");
@@ -1417,7 +699,7 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
   const int P = beam_chunks(ef);
   const int M = ix->M, d = (int)ix->lay.num_dims;
   LaunchPlan lut;
-  lut.kern = pick_kernel(ix->lay.data_type, P, M);
+  lut.kern = pick_kernel(ix->lay.data_type, P, M, slots_per_lane(ix->lay.max_m0));
   lut.waves = 1;
   lut.lds = lds_plan(M, d, P, true, ef).total;
   lut.slots_per_cu = occupancy(ix->device, ix->lds_cu, lut.kern, 1, lut.lds);
@@ -1434,10 +716,10 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
   const int lds_cu = ix->lds_cu;
   const int Psp = beam_chunks_sp(ef);
   const int per_wave = lds_plan(M, d, Psp, false, ef).total;
-  const int waves = std::min(16, (lds_cu - piv_bytes(d)) / per_wave);
+  const int waves = std::min(sp_max_waves(Psp, slots_per_lane(ix->lay.max_m0)), (lds_cu - piv_bytes(d)) / per_wave);
   if (!forced && waves <= lut.slots_per_cu) return lut;
   LaunchPlan sp;
-  sp.kern = pick_kernel_sp(ix->lay.data_type, Psp, M);
+  sp.kern = pick_kernel_sp(ix->lay.data_type, Psp, M, slots_per_lane(ix->lay.max_m0));
   sp.waves = waves;
   sp.lds = piv_bytes(d) + waves * per_wave;
   sp.lds_shared = piv_bytes(d);
@@ -1501,7 +783,7 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
                    int32_t* d_hops, int num_blocks) {
   std::lock_guard<std::mutex> lk(ix->mu);
   if (nq <= 0 || nq > INT32_MAX - 1) fail(QV_EINVAL, "number of queries out of range: " + std::to_string(nq));
-  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 448]");
+  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 1024]");
   HIP_OK(hipSetDevice(ix->device));
   ensure_scratch(ix, nq, 1);
   const LaunchPlan lp = launch_plan(ix, ef, QV_KERNEL_AUTO, num_blocks > 0 ? std::min<int64_t>(nq, num_blocks) : nq);
@@ -1566,7 +848,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     fail(QV_EINVAL, "Query dimension mismatch: queries have " + std::to_string(dim) +
                         " dims, but the index expects " + std::to_string(L.num_dims));
   if (topk <= 0 || topk > kMaxTopk) fail(QV_EINVAL, "topk must be in [1, 64]");
-  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 448]");
+  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 1024]");
   if (o.pipe_width < 1 || o.pipe_width > kMaxPipeWidth) fail(QV_EINVAL, "--pipe-width must be in [1, 16]");
   if (o.queries_per_block < 1 || o.queries_per_block > kMaxQueriesPerBlock)
     fail(QV_EINVAL, "--queries-per-block must be in [1, 8]");
@@ -1918,7 +1200,7 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
     fail(QV_EINVAL, "Query dimension mismatch: queries have " + std::to_string(dim) +
                         " dims, but the index expects " + std::to_string(L.num_dims));
   if (topk <= 0 || topk > kMaxTopk) fail(QV_EINVAL, "topk must be in [1, 64]");
-  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 448]");
+  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 1024]");
   if (o.pipe_width < 1 || o.pipe_width > kMaxPipeWidth) fail(QV_EINVAL, "--pipe-width must be in [1, 16]");
   if (o.queries_per_block < 1 || o.queries_per_block > kMaxQueriesPerBlock)
     fail(QV_EINVAL, "--queries-per-block must be in [1, 8]");

@@ -1,0 +1,878 @@
+// qv_search_kernels.hpp -- the persistent beam-search kernels (device code),
+// shared by the translation units that instantiate them: qv_search.hip (one
+// neighbour per lane, beams up to 448 entries), qv_search_deep.hip (beams up
+// to 1024 entries) and qv_search_r128.hip (two neighbours per lane, R <= 128).
+// The reference path each part follows is cited where it is defined.
+#pragma once
+
+#include <cstdint>
+
+#include "qv_common.hpp"
+#include "qv_device.hpp"
+
+namespace qv {
+namespace sk {
+
+using namespace qv::dev;
+
+struct SearchArgs {
+  // index (HBM)
+  const uint8_t* pages;
+  const uint8_t* codes;
+  const float* centroid;
+  const float* pivots_t;
+  const int32_t* chunk_off;
+  int64_t num_points;
+  int64_t nodes_per_page;
+  uint64_t npp_magic;              // page = (v * npp_magic) >> npp_shift, exact for 0 <= v < 2^31
+  int32_t npp_shift;
+  int64_t node_size;
+  int64_t data_size;
+  int32_t dim;
+  int32_t num_chunks;
+  int32_t max_m;
+  int32_t medoid;
+  // queries / params
+  const float* queries;
+  int32_t nq;
+  int32_t topk;
+  int32_t ef;
+  int32_t pipe_w;
+  int32_t early_exit;
+  int32_t warmup;
+  int32_t patience;
+  // outputs (device)
+  int32_t* out_ids;
+  float* out_dists;
+  int32_t* out_found;
+  int32_t* out_hops;
+  int32_t* out_stopped;
+  int32_t* out_evals;              // neighbour distance evaluations per query
+  uint64_t* t_start;
+  uint64_t* t_end;
+  // dispatch
+  int32_t* counters;               // [0] next ticket, [1] done count, [2] error bits
+  const int32_t* feed_count;       // host-coherent, may be null (then nq)
+  const int32_t* terminate;        // host-coherent, may be null
+  int32_t* ring;                   // host-coherent completion ring, may be null
+  uint64_t spin_limit_ticks;       // watchdog on feed waits (100 MHz ticks)
+  // navigation graph for the per-query entry node (nav_data null: the medoid)
+  const uint8_t* nav_data;
+  const int32_t* nav_graph;
+  const int32_t* nav_map;
+  int64_t nav_nodes;
+  int32_t nav_max_m;
+  int32_t nav_start;
+  // optional record of expanded nodes (graph construction)
+  int32_t* rec_ids;
+  float* rec_dists;
+  int32_t rec_cap;
+  // per-slot beam membership bitmaps of the per-query-LUT kernel (bit v set
+  // <=> v in the beam), bits_words 32-bit words per slot, zero between queries
+  uint32_t* bits;
+  int64_t bits_words;
+  // per-step recall (pipe width 1): query q stops once sr_required of its
+  // top-k ids appear in ground-truth row q % sr_count (sr_width <= 256 ids);
+  // sr_gt null: off
+  const int32_t* sr_gt;
+  int32_t sr_width;
+  int32_t sr_count;
+  int32_t sr_required;
+  int32_t* sr_step;                // [nq] step at which it was reached, -1 if never
+  int32_t* sr_hits;                // [nq] hits then (else at the end)
+};
+
+enum : int32_t { kErrSpinTimeout = 1 };
+
+// Dynamic LDS carve-up of one query (one wave), shared by the kernel and its
+// launcher.  Q = beam positions per lane: the register beam holds Q * 64 >= ef
+// entries, the LDS beam cap of them (beam_cap).  With a per-query LUT (lut) the
+// table comes first; the shared-
+// pivot kernel has none, and when every query element the exact distance
+// needs fits the lanes' registers (dim <= 32 kVecPre) its beam overlays the
+// query copy qu, which is only read once, into those registers, before the
+// first hop.
+struct LdsPlan {
+  int lut_off, qc_off, qu_off, beam_off, total;
+};
+
+// LDS beam entries: Q * 64 with the per-query LUT (its table, not the beam,
+// limits the queries per CU); ef rounded up to 8 with shared pivots, where the
+// beam's LDS decides how many queries a CU holds.
+__host__ __device__ inline int beam_cap(int ef, int Q, bool lut) { return lut ? Q * kWave : (ef + 7) & ~7; }
+
+__host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool lut, int ef) {
+  LdsPlan p;
+  p.lut_off = 0;
+  p.qc_off = p.lut_off + (lut ? num_chunks * kPivots * 4 : 0);
+  const int dpad = (dim + 3) & ~3;
+  p.qu_off = p.qc_off + dpad * 4;
+  const bool overlay = !lut && dim <= 32 * kVecPre;
+  p.beam_off = overlay ? p.qu_off : (p.qu_off + dpad * 4 + 15) & ~15;
+  const int beam_bytes = beam_cap(ef, Q, lut) * 8;
+  p.total = p.beam_off + (overlay && dpad * 4 > beam_bytes ? dpad * 4 : beam_bytes);
+  return p;
+}
+
+// Shared-pivot kernel: the PQ pivots chunk-major, [chunk m][code c][SC dims]
+// (entry (m, c) at float (m * 256 + c) * SC), ahead of the per-wave query
+// areas.  The SC floats one LUT entry needs are one aligned vector read, and
+// lanes reading different codes of one chunk hit consecutive 4 SC-byte slots,
+// so rows need no padding against bank conflicts.
+__host__ __device__ inline int piv_bytes(int dim) { return kPivots * dim * 4; }
+
+using KernelFn = void (*)(SearchArgs);
+
+// Waves (queries) one shared-pivot workgroup holds at most, by beam positions
+// per lane and neighbour slots per lane: 16 (128 registers per wave), or 8
+// (256) for beams of more than 7 positions per lane and for two slots.
+__host__ __device__ constexpr int sp_max_waves(int Q, int NPL) { return Q <= 7 && NPL == 1 ? 16 : 8; }
+
+// Kernels instantiated in qv_search_r128.hip (two neighbour slots per lane,
+// Q rounded up to 1, 2, 4, 7, 10 or 16) and qv_search_deep.hip (one slot per
+// lane, Q = 10 or 16); null for a combination they do not hold.
+KernelFn pick_kernel_r128(int dtype, int Q, int M);
+KernelFn pick_kernel_sp_r128(int dtype, int Q, int M);
+KernelFn pick_kernel_deep(int dtype, int Q, int M);
+KernelFn pick_kernel_sp_deep(int dtype, int Q, int M);
+
+}  // namespace sk
+}  // namespace qv
+
+namespace {
+
+using namespace qv::sk;
+
+// Registers holding the start of a node record (see Query::fetch): NPL
+// neighbour slots per lane (lane l holds neighbours l and l + 64).
+template <int NPL>
+struct NodeRec {
+  int deg;
+  uint32_t nbr[NPL];
+  uint32_t xv[kVecPre];  // raw vector elements (load_vec_pre)
+};
+
+// SC = 0: per-query LUT in LDS; SC > 0: LUT entries recomputed from the
+// shared pivots (chunks of SC dimensions).  NPL = 1: R <= 64, lane l owns
+// neighbour l; NPL = 2: R <= 128, lane l also owns neighbour l + 64.
+template <class T, int Q, int MC, int SC, int NPL>
+struct Query {
+  static_assert(NPL == 1 || NPL == 2, "one or two neighbours per lane");
+  using Rec = NodeRec<NPL>;
+  const SearchArgs& a;
+  float* lut;
+  const float* piv;  // shared pivots (SC > 0)
+  float* qc;
+  float* qu;
+  float quv[kVecPre];  // qu elements of this lane for the exact distance
+  uint64_t* beam;
+  uint32_t* bits;  // this slot's membership bitmap (SC == 0)
+  int sz;        // beam size (ctx.size)
+  int cap;       // LDS beam entries (beam_cap >= ef)
+  // The beam in registers, chunk-major (lane l holds positions [l Q, l Q + Q),
+  // kPadKey at and beyond sz), and its first unvisited entry u with key bu
+  // (INT32_MAX and ~0 when every entry is visited).  LDS holds the same beam
+  // for the scatter of each merge.
+  uint64_t ck[Q];
+  int u;
+  uint64_t bu;
+  float td;      // top-k entry of this lane
+  int32_t ti;
+  int fc;        // found count
+  int evals;     // ADC evaluations so far
+  float last_e;  // exact distance of the node expanded by the last hop
+
+  // Membership test: a bitmap in HBM (SC == 0), else the rank in the LDS
+  // beam.  The bitmap costs a random read per neighbour but nothing on the
+  // hop's critical path (the read overlaps the code rows); the rank costs a
+  // dependent LDS binary search after the ADC but no memory traffic, which
+  // pays when 8 to 16 queries per CU compete for the device's random accesses.
+  static constexpr bool kBits = SC == 0;
+  // The shared-pivot kernels serve dim = MC SC only (uniform chunks).
+  static constexpr int kD = SC > 0 ? MC * SC : 0;
+  // Loop-invariant byte offsets of this lane's loads inside a record: its
+  // neighbour slot (past the degree word) and its first vector element.
+  uint32_t off_nbr[NPL], off_x;
+
+  // smem: this query's LDS area; slot: this wave's bitmap index.
+  __device__ Query(const SearchArgs& args, char* smem, const float* pivots_lds, int64_t slot)
+      : a(args), piv(pivots_lds), sz(0), u(INT32_MAX), bu(~0ull), td(__int_as_float(0x7f800000)), ti(-1), fc(0),
+        evals(0) {
+#pragma unroll
+    for (int k = 0; k < Q; k++) ck[k] = kPadKey;
+    LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, SC == 0, a.ef);
+    cap = beam_cap(a.ef, Q, SC == 0);
+    lut = reinterpret_cast<float*>(smem + pl.lut_off);
+    qc = reinterpret_cast<float*>(smem + pl.qc_off);
+    qu = reinterpret_cast<float*>(smem + pl.qu_off);
+    beam = reinterpret_cast<uint64_t*>(smem + pl.beam_off);
+    bits = kBits ? a.bits + slot * a.bits_words : nullptr;
+    const int lane = lane_id();
+#pragma unroll
+    for (int j = 0; j < NPL; j++)  // slots >= max_m are masked by the degree
+      off_nbr[j] = 4u * (uint32_t)(1 + min(lane + kWave * j, a.max_m - 1));
+    off_x = (uint32_t)(lane & 31) * (uint32_t)sizeof(T);
+  }
+
+  __device__ __forceinline__ const uint8_t* record(int32_t v) const {
+    const int64_t page = (int64_t)(((uint64_t)(uint32_t)v * a.npp_magic) >> a.npp_shift);
+    const int64_t slot = (int64_t)v - page * a.nodes_per_page;
+    return a.pages + page * 4096 + slot * a.node_size;
+  }
+
+  // Requests the parts of v's record a hop reads: degree, the max_m neighbour
+  // slots (inside the record) and the first vector elements.  Only vector
+  // loads are used, so waits on LDS traffic never wait for these.
+  __device__ __forceinline__ void fetch(int32_t v, int lane, Rec& nr) const {
+    const uint8_t* rec = record(v);
+    const uint8_t* nb = rec + a.data_size;
+    uint32_t z = 0;
+    asm volatile("" : "+v"(z));  // per-lane address: a vector load of the degree
+    nr.deg = *reinterpret_cast<const int*>(nb + z);
+#pragma unroll
+    for (int j = 0; j < NPL; j++) nr.nbr[j] = *reinterpret_cast<const uint32_t*>(nb + off_nbr[j]);
+    if constexpr (kD > 0)
+      load_vec_pre_fixed<T, kD>(rec, off_x, nr.xv);
+    else
+      load_vec_pre<T>(rec, a.dim, lane, nr.xv);
+  }
+
+  // Exact distance of v and the top-k insert (the reference's second warp).
+  __device__ __forceinline__ void exact_and_topk(int32_t v, const uint32_t (&xv)[kVecPre], const uint8_t* rec,
+                                                 int lane) {
+    float e;
+    if constexpr (kD > 0)
+      e = exact_l2_pre_fixed<T, kD>(xv, quv, lane);
+    else
+      e = exact_l2_pre<T>(xv, quv, rec, qu, a.dim, lane);
+    last_e = e;
+    const float dlast = read_lane_f32(td, a.topk - 1);
+    if (fc < a.topk || e < dlast) topk_insert(td, ti, fc, a.topk, e, v);
+  }
+
+  // One expansion of node v: persistent_merge_data (kernel_helpers.cuh:232-357)
+  // followed by persistent_visit_select_dualwarp (kernel_helpers.cuh:422-489).
+  // nr holds v's record (fetch); with PF the selected next node's record is
+  // requested into nr as soon as it is known.  Returns the next node or -1.
+  //
+  // With PF, cr carries code rows from one hop to the next: when `have`, cr
+  // holds (or is loading) v's neighbours' rows, requested by the previous hop.
+  // A hop that guesses its successor (the beam's first unvisited entry, spec)
+  // requests that node's record at its start and, once the ADC no longer
+  // needs cr, that node's code rows, so the next hop's rows are in flight
+  // through this hop's merge; `have` is set when the guess was the node
+  // selected.  Only loads move: every result is the same.
+  template <bool PF>
+  __device__ __forceinline__ int32_t hop(int32_t v, Rec& nr, CodeRow<MC>& cr, bool& have) {
+    if constexpr (NPL == 2) return hop2<PF>(v, nr);
+    const int lane = opaque_lane();
+    const int deg = read_lane_i32(nr.deg, 0);
+    evals += deg;
+    const bool has = lane < deg;
+    const uint32_t nbr = has ? nr.nbr[0] : 0u;
+    uint32_t xv[kVecPre];
+#pragma unroll
+    for (int k = 0; k < kVecPre; k++) xv[k] = nr.xv[k];
+    const uint8_t* rec = kD == 0 && a.dim > 32 * kVecPre ? record(v) : nullptr;
+    // With PF, the next node is most often the beam's first unvisited entry
+    // (whenever no new candidate beats it), so its record is requested right
+    // after this hop's code rows, and the merge only requests another record
+    // when a candidate wins.
+    const bool spec = PF && u < sz;
+
+    // Beam membership of each neighbour from the bitmap.  The bitmap updates
+    // of the previous hop were issued before this hop's record arrived;
+    // waiting for every outstanding vector memory operation here (the record
+    // is complete by now) orders them before these reads, which bypass the
+    // vector L1.
+    uint32_t bword = 0;
+    if constexpr (kBits) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      bword = __hip_atomic_load(bits + (nbr >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // ADC gather-sum over the neighbour's code row (LUT in LDS); the code rows
+    // are in flight while the exact distance of v is computed.  Lanes without
+    // a neighbour read code row 0 and discard the sum.
+    float d;
+    if constexpr (MC > 0 && MC % 16 == 0) {
+      if (!(PF && have)) adc_load<MC>(cr, a.codes, nbr);
+      // Issued on every hop (v's own record when there is no unvisited entry
+      // to guess), so every path reaches the ADC with the same loads in
+      // flight and the compiler's wait for the code rows can leave the
+      // record outstanding.
+      if constexpr (PF) fetch(spec ? (int32_t)key_id(bu) : v, lane, nr);
+      exact_and_topk(v, xv, rec, lane);
+      if constexpr (SC > 0)
+        d = adc_recompute<MC, SC>(cr, qc, piv);
+      else
+        d = adc_sum<MC>(cr, lut);
+      // the guessed successor's code rows (lanes past its degree read row 0)
+      if constexpr (PF) {
+        if (spec) {
+          const int ndeg = read_lane_i32(nr.deg, 0);
+          adc_load<MC>(cr, a.codes, lane < ndeg ? nr.nbr[0] : 0u);
+        }
+      }
+    } else {
+      if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
+      d = adc_row<MC>(a.codes + (int64_t)nbr * a.num_chunks, lut, a.num_chunks);
+      exact_and_topk(v, xv, rec, lane);
+    }
+    const uint64_t nkey = has ? make_key(d, nbr, false) : sentinel_key(lane);
+    const bool fresh = kBits ? has && !((bword >> (nbr & 31)) & 1u) : has;
+    bool hit = false;
+    const int32_t nx = merge_select<true, PF>(nkey, fresh, lane, nr, spec, bu, hit);
+    if constexpr (PF) have = MC > 0 && MC % 16 == 0 && hit;
+    return nx;
+  }
+
+  // hop with two neighbours per lane (R <= 128): the same expansion with the
+  // candidates merged as two batches of 64, neighbours 0-63 first without a
+  // selection, then 64-127 with it.  The first ef entries of
+  // (first ef of beam U A) U B are the first ef of beam U A U B; a B
+  // neighbour whose entry A pushed out of the beam would have landed at or
+  // beyond ef anyway, and no id repeats within one adjacency list.  The
+  // guessed successor is the first unvisited entry before A (its record is
+  // requested at the start), compared by key after B.
+  template <bool PF>
+  __device__ __forceinline__ int32_t hop2(int32_t v, Rec& nr) {
+    const int lane = opaque_lane();
+    const int deg = read_lane_i32(nr.deg, 0);
+    evals += deg;
+    const bool has0 = lane < deg, has1 = lane + kWave < deg;
+    const uint32_t nbr0 = has0 ? nr.nbr[0] : 0u, nbr1 = has1 ? nr.nbr[1] : 0u;
+    uint32_t xv[kVecPre];
+#pragma unroll
+    for (int k = 0; k < kVecPre; k++) xv[k] = nr.xv[k];
+    const uint8_t* rec = kD == 0 && a.dim > 32 * kVecPre ? record(v) : nullptr;
+    const bool spec = PF && u < sz;
+    const uint64_t spec_key = bu;
+    uint32_t bw0 = 0, bw1 = 0;
+    if constexpr (kBits) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      bw0 = __hip_atomic_load(bits + (nbr0 >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bw1 = __hip_atomic_load(bits + (nbr1 >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    float d0, d1;
+    if constexpr (MC > 0 && MC % 16 == 0) {
+      CodeRow<MC> c0, c1;
+      adc_load<MC>(c0, a.codes, nbr0);
+      adc_load<MC>(c1, a.codes, nbr1);
+      if constexpr (PF) fetch(spec ? (int32_t)key_id(bu) : v, lane, nr);
+      exact_and_topk(v, xv, rec, lane);
+      if constexpr (SC > 0) {
+        d0 = adc_recompute<MC, SC>(c0, qc, piv);
+        d1 = adc_recompute<MC, SC>(c1, qc, piv);
+      } else {
+        d0 = adc_sum<MC>(c0, lut);
+        d1 = adc_sum<MC>(c1, lut);
+      }
+    } else {
+      if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
+      d0 = adc_row<MC>(a.codes + (int64_t)nbr0 * a.num_chunks, lut, a.num_chunks);
+      d1 = adc_row<MC>(a.codes + (int64_t)nbr1 * a.num_chunks, lut, a.num_chunks);
+      exact_and_topk(v, xv, rec, lane);
+    }
+    const uint64_t k0 = has0 ? make_key(d0, nbr0, false) : sentinel_key(lane);
+    const uint64_t k1 = has1 ? make_key(d1, nbr1, false) : sentinel_key(lane + kWave);
+    const bool f0 = kBits ? has0 && !((bw0 >> (nbr0 & 31)) & 1u) : has0;
+    const bool f1 = kBits ? has1 && !((bw1 >> (nbr1 & 31)) & 1u) : has1;
+    bool hit = false;
+    merge_select<false, false>(k0, f0, lane, nr, false, spec_key, hit);
+    return merge_select<true, PF>(k1, f1, lane, nr, spec, spec_key, hit);
+  }
+
+  // Without the bitmap, every LDS beam position from sz to cap holds kPadKey
+  // (above every key): set once per query; merges only write below the new
+  // sz, which never shrinks.  The rank search then needs no bounds test.
+  __device__ __forceinline__ void pad_beam(int lane) {
+    if constexpr (!kBits) {
+#pragma unroll
+      for (int k = 0; k < Q; k++)
+        if (k * kWave + lane < cap) beam[k * kWave + lane] = kPadKey;
+    }
+  }
+
+  // First unvisited entry of the beam from the register copy.
+  __device__ __forceinline__ void find_unvisited(int lane) {
+    int first = INT32_MAX;
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      const uint64_t m = __ballot(lane * Q + k < sz && key_unvisited(ck[k]));
+      if (m) first = min(first, (__ffsll((long long)m) - 1) * Q + k);
+    }
+    u = first;
+    // its key from the register copy: slot first % Q of lane first / Q
+    // (wave-uniform, so the next node's record address is scalar work)
+    if (first < sz) {
+      const int kk = first % Q;
+      uint64_t e = ck[0];
+#pragma unroll
+      for (int k = 1; k < Q; k++) e = kk == k ? ck[k] : e;
+      bu = read_lane_u64(e, first / Q);
+    } else {
+      bu = ~0ull;
+    }
+  }
+
+  // Marks the entry at position pos visited (LDS and registers).
+  __device__ __forceinline__ void mark_visited(int pos, uint64_t key, int lane) {
+    if (lane == 0) beam[pos] = key & ~1ull;
+#pragma unroll
+    for (int k = 0; k < Q; k++) ck[k] &= lane * Q + k == pos ? ~1ull : ~0ull;
+  }
+
+  // persistent_merge_data's result after persistent_visit_select_dualwarp's
+  // compaction and truncation (kernel_helpers.cuh:288-357, 440-472), built by
+  // rank.  The reference places a candidate equal to a beam entry (same id,
+  // hence same distance) right after it (lower_bound + 1, :300-329) and the
+  // adjacent-id compaction then drops it; the min(sz + deg, 2 ef) cap (:350)
+  // only removes entries that sit at or beyond ef after compaction, since at
+  // most sz <= ef entries are compacted away.  So the new beam is the first ef
+  // entries of  beam  U  {candidates whose id is not in the beam}, in key
+  // order, and its first unvisited entry is taken and marked visited.
+  // fresh: lane holds a neighbour, not in the beam by the bitmap (kBits).
+  //
+  // Without the bitmap: a neighbour whose id is in the beam has that entry's
+  // key (the ADC of one code row against one query is one value), visited
+  // bit aside.  So the lower bound r of (c & ~1) in the sorted beam is both
+  // the candidate's rank and its membership test: c is in the beam iff
+  // beam[r] and c differ only in the visited bit.  Only neighbours below the
+  // end of a full beam need it.
+  //
+  // The selected node only depends on the smallest surviving candidate and
+  // the old first unvisited entry, so it is found first and its record is
+  // requested (PF) before the rest of the merge, which then overlaps that load,
+  // unless it is the first unvisited entry whose record the hop requested at
+  // its start (spec).
+  // hit: (PF) the selected node is the guessed one (key spec_key), whose
+  // record the hop requested at its start.  SEL = false merges without a
+  // selection (the first batch of a two-slot hop) and returns -1.
+  template <bool SEL, bool PF>
+  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool fresh, int lane, Rec& nr, bool spec,
+                                                  uint64_t spec_key, bool& hit) {
+    const int ef = a.ef;
+    // Candidates at or above the last entry of a full beam end beyond ef.
+    const uint64_t last = sz >= ef ? beam[ef - 1] : ~0ull;
+    const bool below = fresh && nkey < last;
+    int r = 0;  // rank in the beam (valid lanes)
+    bool valid = below;
+    if constexpr (!kBits) {
+      if (__ballot(below)) {
+        // r = #{beam entries e : e < (nkey & ~1)} by a 4-ary search over the
+        // LDS beam: sorted, kPadKey from sz to its capacity cap (>= ef), so
+        // a read clamped to cap - 1 sees either a key of the beam or kPadKey
+        // (a below candidate is under the last key of a full beam, so even a
+        // full-capacity beam never lifts r past it).  A level of step s reads
+        // r + s - 1, r + 2 s - 1 and r + 3 s - 1 at once (one LDS round trip)
+        // and adds s per key below; steps 4^i from kTop cover 4 kTop - 1 >=
+        // 64 Q - 1 positions.  The last level (s = 1) also reads r + 3, so
+        // beam[r] for the membership test is one of its four keys.
+        constexpr int kCap = Q * kWave;
+        constexpr int kTop = kCap <= 64 ? 16 : (kCap <= 256 ? 64 : 256);
+        const int top = cap - 1;
+        const uint64_t c0 = nkey & ~1ull;
+#pragma unroll
+        for (int step = kTop; step > 1; step >>= 2) {
+          const uint64_t e1 = beam[min(r + step - 1, top)];
+          const uint64_t e2 = beam[min(r + 2 * step - 1, top)];
+          const uint64_t e3 = beam[min(r + 3 * step - 1, top)];
+          r += ((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * step;
+        }
+        const uint64_t e0 = beam[min(r, top)];
+        const uint64_t e1 = beam[min(r + 1, top)];
+        const uint64_t e2 = beam[min(r + 2, top)];
+        const uint64_t e3 = beam[min(r + 3, top)];
+        const int n = (e0 < c0 ? 1 : 0) + (e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0);
+        r += n;
+        const uint64_t at = n == 0 ? e0 : (n == 1 ? e1 : (n == 2 ? e2 : e3));
+        valid = below && (at >> 1) != (nkey >> 1);
+      }
+    }
+    const uint64_t vm = __ballot(valid);
+
+    int selpos = -1;
+    uint64_t selkey = ~0ull;
+    if constexpr (!SEL) {
+      if (vm == 0) return -1;
+    } else {
+    if (vm == 0 && u >= sz) return -1;
+    // Smallest surviving candidate and its rank in the beam (with the bitmap:
+    // entries below it by ballots against the register beam, visited bit
+    // ignored: e < c iff e < (c & ~1)).
+    selpos = u;
+    selkey = bu;
+    if (vm != 0) {
+      const uint64_t kv0 = wave_min_u64(valid ? nkey : ~0ull);
+      if (kv0 < bu) {
+        if constexpr (kBits) {
+          int r0 = 0;
+#pragma unroll
+          for (int k = 0; k < Q; k++) r0 += __popcll(__ballot(ck[k] < (kv0 & ~1ull)));
+          selpos = r0;
+        } else {
+          selpos = read_lane_i32(r, __ffsll((long long)__ballot(valid && nkey == kv0)) - 1);
+        }
+        selkey = kv0;
+      }
+    }
+    if constexpr (PF) {
+      // (the key test, not the position: a winning candidate lands at u too)
+      hit = spec && selkey == spec_key;
+      if (!hit) fetch((int32_t)key_id(selkey), lane, nr);
+    }
+    if (vm == 0) {
+      mark_visited(selpos, selkey, lane);
+      find_unvisited(lane);
+      return (int32_t)key_id(selkey);
+    }
+    }
+
+    // For each surviving candidate c (few per hop: most neighbours below the
+    // beam's end are already in it): its rank t among the candidates and the
+    // shift of every old entry at or above its rank in the beam.
+    int t = 0;
+    uint32_t sh[Q];
+#pragma unroll
+    for (int k = 0; k < Q; k++) sh[k] = 0u;
+    for (uint64_t rest = vm; rest; rest &= rest - 1) {
+      const int l = __ffsll((long long)rest) - 1;
+      const uint64_t c = read_lane_u64(nkey, l);
+      int rc;
+      if constexpr (kBits) {
+        rc = 0;
+#pragma unroll
+        for (int k = 0; k < Q; k++) rc += __popcll(__ballot(ck[k] < (c & ~1ull)));
+        if (lane == l) r = rc;
+      } else {
+        rc = read_lane_i32(r, l);
+      }
+      t += c < nkey ? 1 : 0;
+#pragma unroll
+      for (int k = 0; k < Q; k++) sh[k] += lane * Q + k >= rc ? 1u : 0u;
+    }
+
+    // Scatter in place; entries pushed to ef or beyond drop out (and leave
+    // the bitmap), inserted candidates join it.
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      const int pos = lane * Q + k;
+      const int g = pos + (int)sh[k];
+      if (pos < sz) {
+        if (g < ef) {
+          beam[g] = g == selpos ? (ck[k] & ~1ull) : ck[k];
+        } else if constexpr (kBits) {
+          const uint32_t id = key_id(ck[k]);
+          atomicAnd(bits + (id >> 5), ~(1u << (id & 31)));
+        }
+      }
+    }
+    const int f = r + t;
+    if (valid && f < ef) {
+      beam[f] = f == selpos ? (nkey & ~1ull) : nkey;
+      if constexpr (kBits) {
+        const uint32_t id = key_id(nkey);
+        atomicOr(bits + (id >> 5), 1u << (id & 31));
+      }
+    }
+    sz = min(sz + (int)__popcll(vm), ef);
+    // Register copy of the new beam (the wave's LDS accesses complete in order).
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      const int pos = lane * Q + k;
+      ck[k] = pos < sz ? beam[pos] : kPadKey;
+    }
+    find_unvisited(lane);
+    return SEL ? (int32_t)key_id(selkey) : -1;
+  }
+
+  // Clears the bitmap bits of the final beam (bitmaps are zero between queries).
+  __device__ __forceinline__ void clear_bits(int lane) {
+    if constexpr (kBits) {
+#pragma unroll
+      for (int k = 0; k < Q; k++) {
+        const int pos = lane * Q + k;
+        if (pos < sz) {
+          const uint32_t id = key_id(ck[k]);
+          atomicAnd(bits + (id >> 5), ~(1u << (id & 31)));
+        }
+      }
+    }
+  }
+
+  // persistent_select_next_no_compact (kernel_helpers.cuh:491-518): the first
+  // unvisited entry (the beam never exceeds ef here) is taken and marked.
+  __device__ __forceinline__ int32_t select_next_no_compact() {
+    const int lane = opaque_lane();
+    if (u >= sz) return -1;
+    const uint64_t sel = bu;
+    mark_visited(u, sel, lane);
+    find_unvisited(lane);
+    return (int32_t)key_id(sel);
+  }
+};
+
+// gpruning bookkeeping (kernel_q1.cuh:294-315, 524-545).
+struct GPrune {
+  int no_improve = 0, last_fc = 0;
+  float last_top1 = __int_as_float(0x7f800000), last_topk = __int_as_float(0x7f800000);
+};
+
+// Orders a query's LDS set-up before its reads: a workgroup barrier when the
+// workgroup is the query's one wave, a compiler fence otherwise (a wave's LDS
+// accesses complete in order).
+template <int SC>
+__device__ __forceinline__ void query_sync() {
+  if constexpr (SC == 0)
+    __syncthreads();
+  else
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
+// The persistent query loop of one wave: smem is its LDS area, piv the
+// shared pivots (SC > 0), slot its bitmap index (SC == 0).
+template <class T, int Q, int MC, int SC, int NPL>
+__device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, const float* piv, int64_t slot) {
+  const int lane = lane_id();
+
+  while (true) {
+    // ---- acquire (StreamingDispatch, src/quiver/kernel_core/policies/dispatch.cuh:39-79)
+    int32_t qid = -1;
+    if (lane == 0) {
+      qid = atomicAdd(&a.counters[0], 1);
+      if (qid >= a.nq) {
+        qid = -1;
+      } else if (a.terminate &&
+                 __hip_atomic_load(a.terminate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
+        qid = -1;
+      } else if (a.feed_count) {
+        const uint64_t t0 = wall_ticks();
+        while (qid >= __hip_atomic_load(a.feed_count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM)) {
+          if (a.terminate &&
+              __hip_atomic_load(a.terminate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
+            qid = -1;
+            break;
+          }
+          if (wall_ticks() - t0 > a.spin_limit_ticks) {
+            atomicOr(&a.counters[2], kErrSpinTimeout);
+            qid = -1;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(4);
+        }
+      }
+    }
+    qid = read_lane_i32(qid, 0);
+    if (qid < 0) break;
+    if (a.t_start && lane == 0) a.t_start[qid] = wall_ticks();
+
+    Query<T, Q, MC, SC, NPL> Qy(a, smem, piv, slot);
+    const float* q = a.queries + (int64_t)qid * a.dim;
+    // ---- entry node: the nav-graph search on the raw query when a nav graph is
+    // loaded (kernel_q1.cuh:148-174, 199-206), else the medoid.
+    const int32_t entry = a.nav_data ? nav_entry<T>(q, a.nav_data, a.nav_graph, a.nav_map, a.nav_nodes, a.dim,
+                                                    a.nav_max_m, a.nav_start, (int32_t)a.medoid)
+                                     : a.medoid;
+    // ---- query into LDS: q - mu for the LUT, fl(fl(q - mu) + mu) for the exact
+    // distance (pq_device.cuh:18-20, 33-35).
+    for (int i = lane; i < a.dim; i += kWave) {
+      const float c = q[i] - a.centroid[i];
+      Qy.qc[i] = c;
+      Qy.qu[i] = c + a.centroid[i];
+    }
+    query_sync<SC>();
+    if constexpr (SC == 0) {
+      build_lut_lds(Qy.qc, a.pivots_t, a.chunk_off, a.num_chunks, Qy.lut);
+      query_sync<SC>();
+    }
+    load_query_pre(Qy.qu, a.dim, lane, Qy.quv);
+    // qu may share its LDS with the beam (lds_plan): no beam store may move
+    // above these reads.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    Qy.pad_beam(lane);
+
+    GPrune g;
+    int step = 0;
+    bool stop = false;
+    const bool gpr = a.early_exit == QV_EXIT_GPRUNING;
+    auto check = [&]() -> bool {
+      const float top1 = read_lane_f32(Qy.td, 0);
+      const float topk = read_lane_f32(Qy.td, a.topk - 1);
+      const int fc = read_lane_i32(Qy.fc, 0);  // equal in every lane; read as uniform
+      const bool improved = fc > g.last_fc || top1 < g.last_top1 || topk < g.last_topk;
+      if (step < a.warmup) g.no_improve = 0;
+      else g.no_improve = improved ? 0 : g.no_improve + 1;
+      g.last_fc = fc;
+      g.last_top1 = top1;
+      g.last_topk = topk;
+      return gpr && step >= a.warmup && a.patience > 0 && g.no_improve >= a.patience;
+    };
+
+    // count_topk_gt_hits (kernel_helpers.cuh:520-535): top-k entries (a
+    // repeated id counted each time, -1 padding skipped) found anywhere in the
+    // query's ground-truth row, read four ids per lane.
+    const bool sr = a.sr_gt != nullptr;
+    int sr_at = -1, sr_h = 0;
+    auto sr_hits = [&]() -> int {
+      const int32_t* row = a.sr_gt + (int64_t)(qid % a.sr_count) * a.sr_width;
+      int32_t g[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) g[t] = lane + kWave * t < a.sr_width ? row[lane + kWave * t] : -1;
+      int hits = 0;
+      for (int i = 0; i < a.topk; i++) {
+        const int32_t id = read_lane_i32(Qy.ti, i);
+        if (id < 0) continue;
+        hits += __ballot(g[0] == id || g[1] == id || g[2] == id || g[3] == id) != 0 ? 1 : 0;
+      }
+      return hits;
+    };
+
+    auto log_hop = [&](int32_t v) {
+      if (a.rec_ids && lane == 0 && step < a.rec_cap) {
+        a.rec_ids[(int64_t)qid * a.rec_cap + step] = v;
+        a.rec_dists[(int64_t)qid * a.rec_cap + step] = Qy.last_e;
+      }
+    };
+
+    NodeRec<NPL> nr;
+    CodeRow<MC> cr;
+    bool have = false;
+    auto expand = [&](int32_t v) -> int32_t {
+      Qy.fetch(v, lane, nr);
+      return Qy.template hop<false>(v, nr, cr, have);
+    };
+
+    if (a.pipe_w == 1) {
+      // One pipe lane (kernel_q1.cuh:199-397 boot, then 407-670): the node a
+      // hop selects is the next one expanded, so its record is requested while
+      // the hop finishes.
+      Qy.fetch(entry, lane, nr);
+      int32_t v = entry;
+      while (true) {
+        const int32_t nx = Qy.template hop<true>(v, nr, cr, have);
+        log_hop(v);
+        ++step;
+        if (check()) {
+          stop = true;
+          break;
+        }
+        // per-step recall, after the early-exit test (kernel_q1.cuh:354-364)
+        if (sr) {
+          const int h = sr_hits();
+          if (h >= a.sr_required) {
+            sr_at = step;
+            sr_h = h;
+            stop = true;
+            break;
+          }
+        }
+        if (nx < 0) break;
+        v = nx;
+      }
+      goto finish;
+    }
+    {
+    // ---- boot (kernel_q1.cuh:199-397)
+    int32_t first = expand(entry);
+    log_hop(entry);
+    step = 1;
+    if (check()) {
+      stop = true;
+      first = -1;
+    }
+    // Lane w < W of pipe_node holds the node of pipe lane w (-1: idle).  The
+    // pipe state stays in registers: no LDS round trip and no barrier, whose
+    // memory fence would also wait for the record requested by the last hop.
+    const int W = a.pipe_w;
+    int32_t pipe_node = lane == 0 ? first : -1;
+    for (int w = 1; w < W; w++) {
+      const int32_t nx = Qy.select_next_no_compact();
+      pipe_node = lane == w ? nx : pipe_node;
+    }
+    uint32_t ready = stop ? 0u : (uint32_t)__ballot(lane < W && pipe_node != -1);
+
+    // ---- pipe loop, every issued lane served at once (kernel_q1.cuh:407-670)
+    while (!stop && ready) {
+      const uint32_t cur = ready;
+      for (int w = 0; w < W; w++) {
+        if (!(cur & (1u << w))) continue;
+        const int32_t v = read_lane_i32(pipe_node, w);
+        int32_t nx = expand(v);
+        log_hop(v);
+        ++step;
+        if (check()) {
+          stop = true;
+          nx = -1;
+        }
+        pipe_node = lane == w ? nx : pipe_node;
+      }
+      if (stop) break;
+      for (int w = 0; w < W; w++) {
+        if (cur & (1u << w)) continue;
+        const int32_t nx = Qy.select_next_no_compact();
+        pipe_node = lane == w ? nx : pipe_node;
+      }
+      ready = (uint32_t)__ballot(lane < W && pipe_node != -1);
+    }
+    }
+
+  finish:
+    // ---- finish (kernel_q1.cuh:662-704)
+    if (sr) {
+      if (sr_at < 0) sr_h = sr_hits();
+      if (lane == 0) {
+        a.sr_step[qid] = sr_at;
+        a.sr_hits[qid] = sr_h;
+      }
+    }
+    Qy.clear_bits(lane);
+    if (lane < a.topk) {
+      a.out_ids[(int64_t)qid * a.topk + lane] = Qy.ti;
+      a.out_dists[(int64_t)qid * a.topk + lane] = Qy.td;
+    }
+    if (lane == 0) {
+      if (a.out_found) a.out_found[qid] = Qy.fc;
+      if (a.out_hops) a.out_hops[qid] = step;
+      if (a.out_stopped) a.out_stopped[qid] = stop ? 1 : 0;
+      if (a.out_evals) a.out_evals[qid] = Qy.evals;
+      if (a.t_end) a.t_end[qid] = wall_ticks();
+      atomicAdd(&a.counters[1], 1);
+      if (a.ring) {
+        const int32_t pos = atomicAdd(&a.counters[3], 1);
+        __hip_atomic_store(&a.ring[pos], qid + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+    }
+    query_sync<SC>();
+  }
+}
+
+// One query per workgroup of one wave, its LUT in LDS.
+template <class T, int Q, int MC, int NPL>
+__global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  run_queries<T, Q, MC, 0, NPL>(a, smem, nullptr, blockIdx.x);
+}
+
+// One workgroup per CU, one query per wave: the workgroup holds the pivots
+// once and every wave recomputes the LUT entries it needs (chunks of SC
+// dimensions), so the CU's LDS serves more queries than with a 32 KB LUT per
+// query.  Beams of more than 7 positions per lane (ef > 448; their LDS beams
+// allow 3 to 7 queries per CU) and two neighbour slots per lane (two code
+// rows per lane in flight) take 8 waves at most, which leaves each wave up to
+// 256 registers.
+template <class T, int Q, int MC, int SC, int NPL>
+__global__ __launch_bounds__(kWave * sp_max_waves(Q, NPL)) void search_kernel_sp(SearchArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  float* piv = reinterpret_cast<float*>(smem);
+  // pivots_t is [dim][256]; dim i of code c goes where adc_recompute reads it
+  for (int idx = threadIdx.x; idx < a.dim * kPivots; idx += blockDim.x) {
+    const int i = idx >> 8, c = idx & (kPivots - 1);
+    piv[piv_index<SC>(i, c)] = a.pivots_t[idx];
+  }
+  __syncthreads();
+  const int w = threadIdx.x / kWave;
+  const LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, false, a.ef);
+  run_queries<T, Q, MC, SC, NPL>(a, smem + piv_bytes(a.dim) + w * pl.total, piv, 0);
+}
+
+}  // namespace

@@ -93,6 +93,6 @@ def test_cpu_builder_rejects_bad_params(tmp_path):
 
     base = np.zeros((10, 8), np.uint8)
     with pytest.raises(QuiverError, match="R must be"):
-        quiver.build_index(base, tmp_path / "x", R=65, L=100)
+        quiver.build_index(base, tmp_path / "x", R=129, L=160)
     with pytest.raises(QuiverError, match="L must be"):
         quiver.build_index(base, tmp_path / "x", R=8, L=4)
