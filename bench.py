@@ -38,7 +38,7 @@ WORKLOADS = {
     "small-1M-u8": dict(n=1_000_000, dim=128, dtype="uint8", centers=1024, sigma=20.0, R=64, L=100, M=32,
                         nq=10_000, efs=(45, 64, 96, 128, 160, 192, 200, 208, 216, 224, 256, 288, 320, 384, 448)),
     "float-10M-d96": dict(n=10_000_000, dim=96, dtype="float", centers=4096, sigma=1.0, R=64, L=100, M=48,
-                          nq=10_000, efs=(45, 64, 80, 88, 96, 112, 128, 144, 160, 200, 256, 320, 448)),
+                          nq=10_000, efs=(45, 64, 80, 88, 96, 100, 104, 112, 128, 144, 160, 200, 256, 320, 448)),
     "large-100M-u8": dict(n=100_000_000, dim=128, dtype="uint8", centers=65536, sigma=20.0, R=64, L=100, M=32,
                           nq=10_000, efs=(128, 192, 256, 272, 288, 304, 320, 352, 384, 416, 448)),
 }
