@@ -75,6 +75,8 @@ def main() -> int:
                     help="search kernel variant (auto: the one with more queries per CU)")
     ap.add_argument("--nav-sample", type=int, default=0,
                     help="build a nav graph over every K-th base vector and start queries from it (0: medoid)")
+    ap.add_argument("--no-neighbour-codes", action="store_true",
+                    help="search without the neighbour code table (by default it is built when HBM has room)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "bench.py measures one GPU only; run with --gpus 1",
@@ -159,6 +161,18 @@ def main() -> int:
         del rows
         _lib.check(L.qv_index_load_nav(h, nav_dir.encode()))
         log(f"nav graph over {sample.size} sampled vectors: {time.time() - t:.1f}s")
+
+    # ---- neighbour code table (untimed setup): each node's neighbours' code rows
+    # stored together, so a hop reads one block whose address needs no ids
+    nbr_codes = False
+    if not args.no_neighbour_codes:
+        t = time.time()
+        rc = L.qv_index_neighbour_codes(h, 1)
+        if rc == _lib.QV_OK:
+            nbr_codes = True
+            log(f"neighbour code table ({n * w['R'] * w['M'] / 2**30:.1f} GiB): {time.time() - t:.1f}s")
+        else:
+            log(f"neighbour code table not built: {L.qv_last_error().decode()}")
 
     info = _lib.IndexInfo()
     _lib.check(L.qv_index_get_info(h, C.byref(info)))
@@ -305,6 +319,7 @@ def main() -> int:
                                f"Vamana R={w['R']} L={w['L']} alpha=1.2, PQ {w['M']}x256, {nq} queries, top-10",
                    "ef_search": ef, "early_exit": pname, "pipe_width": 1, "num_blocks": last.num_blocks,
                    "graph_placement": args.graph_placement, "nav_nodes": int(info.nav_nodes),
+                   "neighbour_codes": nbr_codes,
                    "admission": "streaming (window = num_blocks)", "recall_at_10": round(recall, 4),
                    "p50_ms": round(p50, 3), "p99_ms": round(p99, 3), "avg_hops": round(last.avg_hops, 2),
                    "build_s": round(build_s, 1),
@@ -329,6 +344,8 @@ def main() -> int:
 
     # ---- PQ-ADC gather microbenchmark: 1B x 32 B codes, 10k LUTs, 200 x 64 ids
     if not args.no_adc:
+        if nbr_codes:
+            _lib.check(L.qv_index_neighbour_codes(h, 0))  # room for the 32 GB code table
         result["adc"] = adc_leg(_lib, L, args.adc_codes, log)
 
     # The search kernel is bound by random accesses, not by HBM bytes: one code

@@ -154,6 +154,18 @@ int qv_index_get_info(const qv_index* index, qv_index_info* out);
  * inkernel_nav.cuh:61-200) instead of the medoid. */
 int qv_index_load_nav(qv_index* index, const char* nav_dir);
 
+/* Builds (enable != 0) or frees the handle's neighbour code table: for every
+ * node v, the PQ code rows of its max_m neighbour slots stored contiguously
+ * ([num_data][max_m][num_chunks] bytes in HBM, zero past v's degree; 20.5 GB
+ * at 10M points with R = 64, M = 32).  No counterpart in the reference: it is
+ * a second layout of the codes the reference reads row by row
+ * (kernel_helpers.cuh:271-287).  With it a hop reads its node's rows as one
+ * block whose address needs no neighbour ids, so the next node's rows are
+ * requested together with its record; results are unchanged.  Needs
+ * num_chunks a multiple of 16 and max_m <= 64; QV_ENOMEM when the device
+ * lacks the room (plus 1 GiB). */
+int qv_index_neighbour_codes(qv_index* index, int32_t enable);
+
 /* ---- Host-only pieces of the setup path (no GPU needed) ---------------------
  * qv_find_index_files: find_index_file + find_pq_prefix
  * (bin/common/index_discovery.hpp:57-103); writes NUL-terminated paths.

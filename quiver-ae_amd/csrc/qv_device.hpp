@@ -213,6 +213,20 @@ __device__ __forceinline__ void adc_load(CodeRow<MC>& cr, const uint8_t* __restr
   }
 }
 
+// The same from a row address (a row of the neighbour-code table).
+template <int MC>
+__device__ __forceinline__ void adc_load(CodeRow<MC>& cr, const uint8_t* __restrict__ row) {
+  const uint4* r4 = reinterpret_cast<const uint4*>(row);
+#pragma unroll
+  for (int t = 0; t < MC / 16; t++) {
+    const uint4 v = r4[t];
+    cr.w[4 * t + 0] = v.x;
+    cr.w[4 * t + 1] = v.y;
+    cr.w[4 * t + 2] = v.z;
+    cr.w[4 * t + 3] = v.w;
+  }
+}
+
 template <int MC>
 __device__ __forceinline__ float adc_sum(const CodeRow<MC>& cr, const float* __restrict__ lut) {
   float dist = 0.f;

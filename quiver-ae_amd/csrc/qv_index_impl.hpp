@@ -27,6 +27,9 @@ struct qv_index {
   int32_t* d_nav_map = nullptr;
   int64_t nav_nodes = 0;
   int32_t nav_max_m = 0, nav_start = 0;
+  // neighbour code table (optional): [n][max_m][M], node v's neighbours' code rows
+  uint8_t* d_nbr_codes = nullptr;
+  int64_t nbr_codes_bytes = 0;
   int64_t device_bytes = 0;
   int num_cus = 0;
   int lds_cu = 0;  // LDS bytes per CU
@@ -81,6 +84,9 @@ void release_index(qv_index* ix);
 void load_nav(qv_index* ix, const std::string& dir);
 // Checks a nav graph held in host memory and moves it to the handle's device.
 void upload_nav(qv_index* ix, const NavGraphHost& nav);
+
+// Builds (enable) or frees the neighbour code table on the handle's device.
+void set_neighbour_codes(qv_index* ix, bool enable);
 
 // Checks degree <= R, neighbour ids < n and duplicate-free lists on the device;
 // throws QV_EINDEX on the first violation.

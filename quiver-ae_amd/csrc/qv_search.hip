@@ -98,6 +98,29 @@ __global__ __launch_bounds__(256) void validate_kernel(const uint8_t* pages, int
   }
 }
 
+// Neighbour code table: row (v, j) of [n][R][M] is the code row of node v's
+// neighbour j, zero past v's degree.  One thread per row, 16 bytes at a time.
+__global__ __launch_bounds__(256) void neighbour_codes_kernel(const uint8_t* pages, int64_t n, int64_t npp,
+                                                              int64_t node_size, int64_t data_size, int R,
+                                                              const uint8_t* codes, int M, uint8_t* out) {
+  const int64_t rows = n * R;
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t v = r / R;
+    const int j = (int)(r - v * R);
+    const int64_t page = v / npp;
+    const uint32_t* r32 =
+        reinterpret_cast<const uint32_t*>(pages + page * 4096 + (v - page * npp) * node_size + data_size);
+    const uint32_t deg = r32[0];
+    uint4* dst = reinterpret_cast<uint4*>(out + r * M);
+    if ((uint32_t)j < deg) {
+      const uint4* src = reinterpret_cast<const uint4*>(codes + (int64_t)r32[1 + j] * M);
+      for (int t = 0; t < M / 16; t++) dst[t] = src[t];
+    } else {
+      for (int t = 0; t < M / 16; t++) dst[t] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+}
+
 // Kernels of this translation unit: one neighbour per lane (R <= 64) and up
 // to 7 beam positions per lane (ef <= 448); the others come from
 // qv_search_r128.hip and qv_search_deep.hip.
@@ -346,6 +369,7 @@ void release_index(qv_index* ix) {
   hipFree(ix->d_nav_data);
   hipFree(ix->d_nav_graph);
   hipFree(ix->d_nav_map);
+  hipFree(ix->d_nbr_codes);
   if (ix->pages_in_host)
     hipHostFree(ix->d_pages);
   else
@@ -592,6 +616,48 @@ qv_index* index_from_memory(const qv_index_info& li, const uint8_t* pages, const
 }
 
 // NavGraph::init + copy_to_dev (nav_graph.cu:12-73) into this handle's device.
+void set_neighbour_codes(qv_index* ix, bool enable) {
+  HIP_OK(hipSetDevice(ix->device));
+  if (!enable) {
+    if (ix->d_nbr_codes) {
+      HIP_OK(hipStreamSynchronize(ix->stream));
+      hipFree(ix->d_nbr_codes);
+      ix->device_bytes -= ix->nbr_codes_bytes;
+    }
+    ix->d_nbr_codes = nullptr;
+    ix->nbr_codes_bytes = 0;
+    return;
+  }
+  if (ix->d_nbr_codes) return;
+  const Layout& L = ix->lay;
+  if (ix->M % 16 != 0) fail(QV_EUNSUPPORTED, "the neighbour code table needs M a multiple of 16");
+  if (L.max_m0 > kWave) fail(QV_EUNSUPPORTED, "the neighbour code table needs R <= 64");
+  const int64_t bytes = L.num_data * L.max_m0 * ix->M;
+  size_t free_b = 0, total_b = 0;
+  HIP_OK(hipMemGetInfo(&free_b, &total_b));
+  if ((int64_t)free_b < bytes + (int64_t)(1ll << 30))
+    fail(QV_ENOMEM, "the neighbour code table needs " + std::to_string(bytes >> 20) + " MiB, " +
+                        std::to_string(free_b >> 20) + " MiB free");
+  uint8_t* d = nullptr;
+  HIP_OK(hipMalloc(&d, (size_t)bytes));
+  hipLaunchKernelGGL(neighbour_codes_kernel, dim3(65536), dim3(256), 0, ix->stream, ix->d_pages, L.num_data,
+                     L.nodes_per_page, L.node_size, L.data_size, (int)L.max_m0, ix->d_codes, ix->M, d);
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) {
+    const hipError_t s2 = hipStreamSynchronize(ix->stream);
+    if (s2 == hipSuccess) {
+      ix->d_nbr_codes = d;
+      ix->nbr_codes_bytes = bytes;
+      ix->device_bytes += bytes;
+      return;
+    }
+    hipFree(d);
+    fail(QV_EHIP, std::string("neighbour_codes_kernel: ") + hipGetErrorString(s2));
+  }
+  hipFree(d);
+  fail(QV_EHIP, std::string("neighbour_codes_kernel: ") + hipGetErrorString(e));
+}
+
 void load_nav(qv_index* ix, const std::string& dir) {
   NavGraphHost nav;
   read_nav(dir, ix->lay.data_type, ix->lay.num_data, ix->lay.num_dims, nav);
@@ -774,6 +840,7 @@ static SearchArgs base_args(qv_index* ix) {
   a.nav_nodes = ix->nav_nodes;
   a.nav_max_m = ix->nav_max_m;
   a.nav_start = ix->nav_start;
+  a.nbr_codes = ix->d_nbr_codes;
   return a;
 }
 
@@ -1419,6 +1486,14 @@ int qv_index_set_nav(qv_index* ix, const void* data, const int32_t* graph, const
     nav.graph.assign(graph, graph + (size_t)num_node * (size_t)max_m);
     nav.mapping.assign(mapping, mapping + num_node);
     qv::upload_nav(ix, nav);
+  });
+}
+
+int qv_index_neighbour_codes(qv_index* ix, int32_t enable) {
+  return qv::guard([&] {
+    if (!ix) qv::fail(QV_EINVAL, "null index");
+    std::lock_guard<std::mutex> lk(ix->mu);
+    qv::set_neighbour_codes(ix, enable != 0);
   });
 }
 

@@ -80,6 +80,9 @@ struct SearchArgs {
   int32_t sr_required;
   int32_t* sr_step;                // [nq] step at which it was reached, -1 if never
   int32_t* sr_hits;                // [nq] hits then (else at the end)
+  // neighbour code table (optional, null: off): node v's neighbours' code
+  // rows, slot order, at nbr_codes + v * max_m * num_chunks (zero past its degree)
+  const uint8_t* nbr_codes;
 };
 
 enum : int32_t { kErrSpinTimeout = 1 };
@@ -193,6 +196,7 @@ struct Query {
   // Loop-invariant byte offsets of this lane's loads inside a record: its
   // neighbour slot (past the degree word) and its first vector element.
   uint32_t off_nbr[NPL], off_x;
+  uint32_t off_blk;  // this lane's row in a node's neighbour-code block
 
   // smem: this query's LDS area; slot: this wave's bitmap index.
   __device__ Query(const SearchArgs& args, char* smem, const float* pivots_lds, int64_t slot)
@@ -212,6 +216,12 @@ struct Query {
     for (int j = 0; j < NPL; j++)  // slots >= max_m are masked by the degree
       off_nbr[j] = 4u * (uint32_t)(1 + min(lane + kWave * j, a.max_m - 1));
     off_x = (uint32_t)(lane & 31) * (uint32_t)sizeof(T);
+    off_blk = (uint32_t)(min(lane, a.max_m - 1) * a.num_chunks);
+  }
+
+  // This lane's code row in node v's neighbour-code block.
+  __device__ __forceinline__ const uint8_t* block_row(int32_t v) const {
+    return a.nbr_codes + (int64_t)v * (a.max_m * a.num_chunks) + off_blk;
   }
 
   __device__ __forceinline__ const uint8_t* record(int32_t v) const {
@@ -294,8 +304,18 @@ struct Query {
     // are in flight while the exact distance of v is computed.  Lanes without
     // a neighbour read code row 0 and discard the sum.
     float d;
+    // With the neighbour-code table a node's rows are one contiguous block
+    // whose address needs no neighbour ids, so the guessed successor's rows
+    // are requested without waiting for its record, and after a wrong guess
+    // the chosen node's rows follow its record at once.
+    const bool blk = a.nbr_codes != nullptr;
     if constexpr (MC > 0 && MC % 16 == 0) {
-      if (!(PF && have)) adc_load<MC>(cr, a.codes, nbr);
+      if (!(PF && have)) {
+        if (blk)
+          adc_load<MC>(cr, block_row(v));
+        else
+          adc_load<MC>(cr, a.codes, nbr);
+      }
       // Issued on every hop (v's own record when there is no unvisited entry
       // to guess), so every path reaches the ADC with the same loads in
       // flight and the compiler's wait for the code rows can leave the
@@ -309,8 +329,12 @@ struct Query {
       // the guessed successor's code rows (lanes past its degree read row 0)
       if constexpr (PF) {
         if (spec) {
-          const int ndeg = read_lane_i32(nr.deg, 0);
-          adc_load<MC>(cr, a.codes, lane < ndeg ? nr.nbr[0] : 0u);
+          if (blk) {
+            adc_load<MC>(cr, block_row((int32_t)key_id(bu)));
+          } else {
+            const int ndeg = read_lane_i32(nr.deg, 0);
+            adc_load<MC>(cr, a.codes, lane < ndeg ? nr.nbr[0] : 0u);
+          }
         }
       }
     } else {
@@ -322,7 +346,10 @@ struct Query {
     const bool fresh = kBits ? has && !((bword >> (nbr & 31)) & 1u) : has;
     bool hit = false;
     const int32_t nx = merge_select<true, PF>(nkey, fresh, lane, nr, spec, bu, hit);
-    if constexpr (PF) have = MC > 0 && MC % 16 == 0 && hit;
+    if constexpr (PF && MC > 0 && MC % 16 == 0) {
+      if (blk && !hit && nx >= 0) adc_load<MC>(cr, block_row(nx));
+      have = hit || (blk && nx >= 0);
+    }
     return nx;
   }
 

@@ -155,6 +155,7 @@ SIGNATURES = {
     "qv_index_set_nav": (_I32, [_P, _P, _P, _P, _I64, _I32, _I32]),
     "qv_index_get_info": (_I32, [_P, C.POINTER(IndexInfo)]),
     "qv_index_load_nav": (_I32, [_P, C.c_char_p]),
+    "qv_index_neighbour_codes": (_I32, [_P, C.c_int32]),
     "qv_build_nav": (_I32, [_P, _P, _I64, _I32, _I32, C.POINTER(BuildParams), C.c_char_p]),
     "qv_index_close": (None, [_P]),
     "qv_search_opts_default": (None, [C.POINTER(SearchOpts)]),
