@@ -303,7 +303,8 @@ def main() -> int:
     achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic(args.workload, ef, pname, kname, log),
+                "traffic": measured_traffic(args.workload, ef, pname,
+                                              kname + (" neighbour-codes" if nbr_codes else ""), log),
                 "kernel": kname, "kernel_ms": round(kernel_ms, 3),
                 "bytes_per_launch": int(alg_bytes),
                 "bytes_per_launch_without_lut": int(alg_bytes - nq * info.num_chunks * 256 * 4),

@@ -36,7 +36,7 @@ const char* kUsage =
     "  [--poll-threads 6] [--runners-per-ssd 1] [--early-exit-policy gpruning|none]\n"
     "  [--result-prefix P] [--final-recall-csv F] [--skip-nav] [--help]\n"
     "  [--per-step-recall [--recall-threshold 0.9] [--step-recall-csv quiver_step_recall.csv]]\n"
-    "  [--static-batches]\n";
+    "  [--static-batches] [--neighbour-codes]\n";
 
 bool parse_int(const std::string& s, int& out) {
   char* end = nullptr;
@@ -153,7 +153,8 @@ int main(int argc, char** argv) {
                                "--runners-per-ssd", "--num-blocks-list", "--recall-threshold",
                                "--step-recall-csv", "--final-recall-csv", "--result-prefix",
                                "--early-exit-policy", "--graph-placement", "--search-kernel"};
-  const char* bool_flags[] = {"--skip-nav", "--per-step-recall", "--static-batches", "--help"};
+  const char* bool_flags[] = {"--skip-nav", "--per-step-recall", "--static-batches", "--neighbour-codes",
+                              "--help"};
   for (auto* s : value_flags) f[s] = Flag{};
   for (auto* s : bool_flags) f[s] = Flag{"", false, true};
   f["--topk"].value = "10";
@@ -311,6 +312,13 @@ int main(int argc, char** argv) {
                        f["--memory-backend"].value.c_str(), mem_file, 0,
                        placement == "host" ? QV_GRAPH_HOST : QV_GRAPH_HBM, &ix) != QV_OK) {
     std::cerr << qv_last_error() << std::endl;
+    return 1;
+  }
+  // each node's neighbours' code rows as one block in HBM: the same results,
+  // fewer bytes per hop, n * R * M bytes of device memory
+  if (f["--neighbour-codes"].used && qv_index_neighbour_codes(ix, 1) != QV_OK) {
+    std::cerr << qv_last_error() << std::endl;
+    qv_index_close(ix);
     return 1;
   }
   qv_index_info info;

@@ -66,11 +66,13 @@ class _EngineKnobs:
 class _LibraryEngine:
     """Searches through libquiver_hip's C ABI on one GPU."""
 
-    def __init__(self, owner: "IndexQuiver", device: int, graph_placement: str, search_kernel: str) -> None:
+    def __init__(self, owner: "IndexQuiver", device: int, graph_placement: str, search_kernel: str,
+                 neighbour_codes: bool) -> None:
         self._owner = owner
         self._device = device
         self._placement = _lib.QV_GRAPH_HOST if graph_placement == "host" else _lib.QV_GRAPH_HBM
         self._kernel = _lib.KERNEL_NAMES[search_kernel]
+        self._neighbour_codes = neighbour_codes
         self._handle: C.c_void_p | None = None
         _lib.load()  # a missing library fails here, not at the first search
 
@@ -81,6 +83,12 @@ class _LibraryEngine:
             _lib.check(_lib.load().qv_index_open_ex(
                 str(o.index_dir).encode(), o.data_type.encode(), o.memory_backend.encode(), None,
                 self._device, self._placement, C.byref(handle)))
+            if self._neighbour_codes:
+                try:
+                    _lib.check(_lib.load().qv_index_neighbour_codes(handle, 1))
+                except QuiverError:
+                    _lib.load().qv_index_close(handle)
+                    raise
             self._handle = handle
         return self._handle
 
@@ -223,8 +231,11 @@ class IndexQuiver:
     accepted for compatibility; the SPDK backend is not part of this library,
     so searching with SSDs configured raises ``QuiverError`` unless an
     external ``binary`` is used.  Extra keyword arguments beyond the
-    reference's: ``device``, ``graph_placement`` ("hbm" or "host") and
-    ``search_kernel`` ("auto", "lut" or "shared-pivots").
+    reference's: ``device``, ``graph_placement`` ("hbm" or "host"),
+    ``search_kernel`` ("auto", "lut" or "shared-pivots") and
+    ``neighbour_codes`` (store each node's neighbours' PQ code rows as one
+    block in device memory, n * R * M bytes: the same results with fewer
+    bytes read per hop; indexes with R <= 64 and M a multiple of 16).
     """
 
     def __init__(
@@ -246,6 +257,7 @@ class IndexQuiver:
         device: int = 0,
         graph_placement: str = "hbm",
         search_kernel: str = "auto",
+        neighbour_codes: bool = False,
     ) -> None:
         root = Path(index_dir).expanduser().resolve()
         if not root.is_dir():
@@ -280,6 +292,7 @@ class IndexQuiver:
         if search_kernel not in _lib.KERNEL_NAMES:
             raise ValueError("search_kernel must be auto, lut or shared-pivots")
         self.search_kernel = search_kernel
+        self.neighbour_codes = bool(neighbour_codes)
 
         external = _external_engine_path(binary)
         self._knobs = _EngineKnobs(
@@ -293,7 +306,8 @@ class IndexQuiver:
         self.device = int(device)
         self.last_report: dict | None = None
         self._engine = (_ProcessEngine(self, external) if external is not None
-                        else _LibraryEngine(self, self.device, graph_placement, search_kernel))
+                        else _LibraryEngine(self, self.device, graph_placement, search_kernel,
+                                       self.neighbour_codes))
 
     # the engine knobs, readable as attributes like the reference's
     num_blocks = property(lambda self: self._knobs.num_blocks)
