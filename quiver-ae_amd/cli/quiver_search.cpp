@@ -32,7 +32,7 @@ const char* kUsage =
     "  [--topk 10] [--ef-search 30] [--repeat 20] [--ground-truth FILE]\n"
     "  [--memory-backend heap|mmap] [--memory-index-file FILE] [--ssd-list-file FILE]\n"
     "  [--graph-placement hbm|host] [--search-kernel auto|lut|shared-pivots]\n"
-    "  [--num-blocks 756] [--num-blocks-list L] [--pipe-width 2] [--queries-per-block 1]\n"
+    "  [--num-blocks N (default: fill the GPU)] [--num-blocks-list L] [--pipe-width 2] [--queries-per-block 1]\n"
     "  [--poll-threads 6] [--runners-per-ssd 1] [--early-exit-policy gpruning|none]\n"
     "  [--result-prefix P] [--final-recall-csv F] [--skip-nav] [--help]\n"
     "  [--per-step-recall [--recall-threshold 0.9] [--step-recall-csv quiver_step_recall.csv]]\n"
@@ -161,7 +161,10 @@ int main(int argc, char** argv) {
   f["--ef-search"].value = "30";
   f["--repeat"].value = "20";
   f["--memory-backend"].value = "heap";
-  f["--num-blocks"].value = "756";
+  // Unset, --num-blocks fills the GPU with query slots (0 below); a value
+  // given is the slot count, validated as the reference validates it.  The
+  // count changes only how many queries run at once, never their results.
+  f["--num-blocks"].value = "0";
   f["--poll-threads"].value = "6";
   f["--pipe-width"].value = "2";
   f["--queries-per-block"].value = "1";
@@ -219,7 +222,10 @@ int main(int argc, char** argv) {
     }
   }
   // bin/common/cli_validation.hpp:9-30
-  if (num_blocks <= 0) { std::cerr << "--num-blocks must be positive" << std::endl; return 1; }
+  if (f["--num-blocks"].used && num_blocks <= 0) {
+    std::cerr << "--num-blocks must be positive" << std::endl;
+    return 1;
+  }
   if (poll <= 0) { std::cerr << "--poll-threads must be positive" << std::endl; return 1; }
   if (pipe_w < 1 || pipe_w > 16) { std::cerr << "--pipe-width must be in [1, 16]" << std::endl; return 1; }
   if (qpb < 1 || qpb > 8) { std::cerr << "--queries-per-block must be in [1, 8]" << std::endl; return 1; }

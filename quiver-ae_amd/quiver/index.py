@@ -37,6 +37,8 @@ from ._lib import QuiverError
 _ELEMENTS = {"float": ("<f4", ".fbin"), "uint8": ("u1", ".u8bin"), "int8": ("i1", ".i8bin")}
 _TYPE_ALIASES = {"float32": "float"}
 _POLICIES = ("gpruning", "none")
+# The reference's --num-blocks default (python/quiver/index.py:45).
+_REFERENCE_NUM_BLOCKS = 756
 
 
 def _positive(name: str, value) -> int:
@@ -236,6 +238,9 @@ class IndexQuiver:
     ``neighbour_codes`` (store each node's neighbours' PQ code rows as one
     block in device memory, n * R * M bytes: the same results with fewer
     bytes read per hop; indexes with R <= 64 and M a multiple of 16).
+    ``num_blocks`` left unset fills the GPU with concurrent query slots (an
+    external ``binary`` gets the reference's 756); a number given is the slot
+    count, as in the reference.  Results do not depend on it.
     """
 
     def __init__(
@@ -248,7 +253,7 @@ class IndexQuiver:
         spdk_base_lba: int | None = None,
         binary: str | os.PathLike[str] | None = None,
         memory_backend: str = "heap",
-        num_blocks: int = 756,
+        num_blocks: int | None = None,
         queries_per_block: int = 1,
         pipe_width: int = 2,
         poll_threads: int = 6,
@@ -295,8 +300,15 @@ class IndexQuiver:
         self.neighbour_codes = bool(neighbour_codes)
 
         external = _external_engine_path(binary)
+        # Unset, the library fills the GPU with query slots (0); an external
+        # binary gets the reference's own default, 756.  The count changes
+        # only how many queries run at once, never a query's results.
+        if num_blocks is None:
+            num_blocks = 0 if external is None else _REFERENCE_NUM_BLOCKS
+        else:
+            num_blocks = _positive("num_blocks", num_blocks)
         self._knobs = _EngineKnobs(
-            num_blocks=_positive("num_blocks", num_blocks),
+            num_blocks=num_blocks,
             queries_per_block=_positive("queries_per_block", queries_per_block),
             pipe_width=_positive("pipe_width", pipe_width),
             poll_threads=_positive("poll_threads", poll_threads),

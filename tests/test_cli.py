@@ -132,3 +132,30 @@ def test_cli_per_step_recall_matches_oracle(small_u8_index, tmp_path):
     reached = int((step >= 0).sum())
     assert f"[Quiver] Step recall reached={reached} unreached={120 - reached} threshold=0.8 required_hits=8" in r.stdout
     assert "[Quiver] per-step recall enabled: threshold=0.8" in r.stdout
+
+
+@pytest.mark.gpu
+def test_cli_default_slots_fill_the_gpu(small_u8_index, tmp_path):
+    """Without --num-blocks the whole GPU holds query slots: a batch larger
+    than the per-query-LUT kernel's resident slots runs the shared-pivot
+    kernel, with the same results as an explicit small slot count."""
+    ix = small_u8_index
+    q = ix["queries"][:200]
+    qf = tmp_path / "q.u8bin"
+    qf.write_bytes(struct.pack("<ii", *q.shape) + q.tobytes())
+    common = ["--index-dir", ix["dir"], "--query", qf, "--data-type", "uint8", "--ef-search", "64",
+              "--repeat", "12", "--pipe-width", "1", "--early-exit-policy", "none"]
+    print("[gpu] CLI default slots, 2400 queries", flush=True)
+    r = run(*common, "--result-prefix", tmp_path / "a")
+    assert r.returncode == 0, r.stderr
+    assert "[Quiver] search_kernel=shared-pivots" in r.stdout
+    slots = int(r.stdout.split("Runtime Params:\n  num_blocks=")[1].split()[0])
+    assert slots > 1024
+    print("[gpu] CLI --num-blocks 756, 2400 queries", flush=True)
+    r2 = run(*common, "--num-blocks", "756", "--result-prefix", tmp_path / "b")
+    assert r2.returncode == 0, r2.stderr
+    slots2 = int(r2.stdout.split("Runtime Params:\n  num_blocks=")[1].split()[0])
+    assert 756 <= slots2 < 756 + 16  # a launch may round the slots up to whole workgroups
+    a = np.fromfile(tmp_path / "a_ids.bin", dtype="<i4")
+    b = np.fromfile(tmp_path / "b_ids.bin", dtype="<i4")
+    np.testing.assert_array_equal(a, b)

@@ -266,3 +266,12 @@ def test_in_process_engine_refuses_ssds_and_reports_missing_index(index_dir: Pat
         IndexQuiver(index_dir, data_type="uint8").search(np.ones((1, 4), np.uint8), extra_args=["--x"])
     with pytest.raises(QuiverError, match=r"No \*_disk.index"):
         IndexQuiver(index_dir, data_type="uint8").search(np.ones((1, 4), np.uint8))
+
+
+def test_num_blocks_default_fills_the_gpu_in_process(index_dir: Path) -> None:
+    # the in-process engine opens the index only at the first search, so this
+    # runs without a GPU: unset, num_blocks is 0 (the whole device)
+    assert IndexQuiver(index_dir, data_type="uint8").num_blocks == 0
+    assert IndexQuiver(index_dir, data_type="uint8", num_blocks=756).num_blocks == 756
+    with pytest.raises(ValueError, match="num_blocks must be positive"):
+        IndexQuiver(index_dir, data_type="uint8", num_blocks=0)
