@@ -236,20 +236,27 @@ __device__ __forceinline__ float adc_sum(const CodeRow<MC>& cr, const float* __r
 }
 
 typedef float qv_float4 __attribute__((ext_vector_type(4)));
+typedef float qv_float2 __attribute__((ext_vector_type(2)));
 
-// LDS reads of one group of four chunks (M0 .. M0 + 3, whose codes are the
+// Query elements of the shared-pivot ADC, held in registers for the whole
+// query: lane l holds q'[16 j + (l & 15)] in qd[j], so each 16-lane row of the
+// wave holds the whole query.  DPP row_newbcast:i gives every lane of a row
+// the value of the row's lane i, so dimension t is row_newbcast:(t & 15) of
+// qd[t >> 4], read by the subtract that uses it (v_sub_f32_dpp): the query
+// operand costs no LDS read and no instruction.  A group of four chunks reads
+// one qd register (16 dims at SC = 4, 8 at SC = 2).
+
+// Pivot reads of one group of four chunks (M0 .. M0 + 3, whose codes are the
 // bytes of the code word w) for adc_recompute<MC, 4>, in one block so that
 // the group costs one LDS round trip: per chunk, an SDWA shift (the source
 // operand selects the byte) makes the address 8 c of the pivot entry, whose
 // two halves one ds_read2st64_b64 reads at 4096 m and 4096 m + 2048 (offsets
-// 8 m and 8 m + 4 in 512-byte units) from the pivot table at LDS address 0;
-// the query chunks are broadcast reads at qa + 16 m.  The block ends with
-// its own wait, since the compiler does not count these reads.  dep is not
-// read: it orders the block after the previous group's arithmetic, so a
-// group's operands are the only ones held at a time.
+// 8 m and 8 m + 4 in 512-byte units) from the pivot table at LDS address 0.
+// The block ends with its own wait, since the compiler does not count these
+// reads.  dep is not read: it orders the block after the previous group's
+// arithmetic, so a group's operands are the only ones held at a time.
 template <int M0>
-__device__ __forceinline__ void adc_group_reads(uint32_t w, uint32_t qa, float dep, qv_float4 (&pc)[4],
-                                                qv_float4 (&qq)[4]) {
+__device__ __forceinline__ void adc_group_reads(uint32_t w, float dep, qv_float4 (&pc)[4]) {
   static_assert(M0 % 4 == 0 && M0 + 3 < 32, "read2st64 offsets cover 32 chunks");
   uint32_t a0, a1, a2, a3;
   asm volatile(
@@ -261,56 +268,68 @@ __device__ __forceinline__ void adc_group_reads(uint32_t w, uint32_t qa, float d
       "ds_read2st64_b64 %[p1], %[a1] offset0:%[o1] offset1:%[o1h]\n\t"
       "ds_read2st64_b64 %[p2], %[a2] offset0:%[o2] offset1:%[o2h]\n\t"
       "ds_read2st64_b64 %[p3], %[a3] offset0:%[o3] offset1:%[o3h]\n\t"
-      "ds_read_b128 %[q0], %[qa] offset:%[qo0]\n\t"
-      "ds_read_b128 %[q1], %[qa] offset:%[qo1]\n\t"
-      "ds_read_b128 %[q2], %[qa] offset:%[qo2]\n\t"
-      "ds_read_b128 %[q3], %[qa] offset:%[qo3]\n\t"
       "s_waitcnt lgkmcnt(0)"
       : [a0] "=&v"(a0), [a1] "=&v"(a1), [a2] "=&v"(a2), [a3] "=&v"(a3), [p0] "=&v"(pc[0]), [p1] "=&v"(pc[1]),
-        [p2] "=&v"(pc[2]), [p3] "=&v"(pc[3]), [q0] "=&v"(qq[0]), [q1] "=&v"(qq[1]), [q2] "=&v"(qq[2]),
-        [q3] "=&v"(qq[3])
-      : [w] "v"(w), [qa] "v"(qa), [dep] "v"(dep), [o0] "i"(8 * M0), [o0h] "i"(8 * M0 + 4),
-        [o1] "i"(8 * M0 + 8), [o1h] "i"(8 * M0 + 12), [o2] "i"(8 * M0 + 16), [o2h] "i"(8 * M0 + 20),
-        [o3] "i"(8 * M0 + 24), [o3h] "i"(8 * M0 + 28), [qo0] "i"(16 * M0), [qo1] "i"(16 * M0 + 16),
-        [qo2] "i"(16 * M0 + 32), [qo3] "i"(16 * M0 + 48));
+        [p2] "=&v"(pc[2]), [p3] "=&v"(pc[3])
+      : [w] "v"(w), [dep] "v"(dep), [o0] "i"(8 * M0), [o0h] "i"(8 * M0 + 4), [o1] "i"(8 * M0 + 8),
+        [o1h] "i"(8 * M0 + 12), [o2] "i"(8 * M0 + 16), [o2h] "i"(8 * M0 + 20), [o3] "i"(8 * M0 + 24),
+        [o3h] "i"(8 * M0 + 28));
+}
+
+// The arithmetic of one group of four chunks of 4 dims: per chunk, in its
+// dims' order, d_k = q'_t - P[c][t] (q'_t by DPP from q, row lane t & 15),
+// acc = d_0 * d_0 (the fused chain's first step from 0: fma(d, d, 0) rounds
+// d * d once, as the multiply does), acc = fma(d_k, d_k, acc) for k = 1..3,
+// then dist += acc -- the LUT build's entry and the table ADC's sum, bit for
+// bit.  The block starts with s_nop 1: a DPP read needs two wait states after
+// a VALU write of its source, and the compiler does not look inside it.
+__device__ __forceinline__ float adc_math4(const qv_float4 (&pc)[4], float q, float dist) {
+  float t0, t1, t2, t3, acc;
+#define QV_CHUNK4(P, L0, L1, L2, L3)                                                          \
+  "v_sub_f32_dpp %[t0], %[q], %[" P "x] row_newbcast:" L0 " row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_sub_f32_dpp %[t1], %[q], %[" P "y] row_newbcast:" L1 " row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_sub_f32_dpp %[t2], %[q], %[" P "z] row_newbcast:" L2 " row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_sub_f32_dpp %[t3], %[q], %[" P "w] row_newbcast:" L3 " row_mask:0xf bank_mask:0xf\n\t"  \
+  "v_mul_f32 %[acc], %[t0], %[t0]\n\t"                                                     \
+  "v_fmac_f32 %[acc], %[t1], %[t1]\n\t"                                                    \
+  "v_fmac_f32 %[acc], %[t2], %[t2]\n\t"                                                    \
+  "v_fmac_f32 %[acc], %[t3], %[t3]\n\t"                                                    \
+  "v_add_f32 %[dist], %[dist], %[acc]\n\t"
+  asm volatile("s_nop 1\n\t"
+               QV_CHUNK4("p0", "0", "1", "2", "3")
+               QV_CHUNK4("p1", "4", "5", "6", "7")
+               QV_CHUNK4("p2", "8", "9", "10", "11")
+               QV_CHUNK4("p3", "12", "13", "14", "15")
+               : [dist] "+v"(dist), [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [t3] "=&v"(t3),
+                 [acc] "=&v"(acc)
+               : [q] "v"(q), [p0x] "v"(pc[0].x), [p0y] "v"(pc[0].y), [p0z] "v"(pc[0].z), [p0w] "v"(pc[0].w),
+                 [p1x] "v"(pc[1].x), [p1y] "v"(pc[1].y), [p1z] "v"(pc[1].z), [p1w] "v"(pc[1].w),
+                 [p2x] "v"(pc[2].x), [p2y] "v"(pc[2].y), [p2z] "v"(pc[2].z), [p2w] "v"(pc[2].w),
+                 [p3x] "v"(pc[3].x), [p3y] "v"(pc[3].y), [p3z] "v"(pc[3].z), [p3w] "v"(pc[3].w));
+#undef QV_CHUNK4
+  return dist;
 }
 
 // Groups G .. MC/4 - 1 of adc_recompute<MC, 4>: dist += LUT[m][c_m] in chunk
-// order, each LUT entry the LUT build's fused chain from acc = 0.
-template <int G, int MC>
-__device__ __forceinline__ float adc_groups(const uint32_t* w, uint32_t qa, float dist) {
+// order; group G's 16 dims are qd[G].
+template <int G, int MC, int NQ>
+__device__ __forceinline__ float adc_groups(const uint32_t* w, const float (&qd)[NQ], float dist) {
   if constexpr (4 * G >= MC) {
     return dist;
   } else {
-    qv_float4 pc[4], qq[4];
-    adc_group_reads<4 * G>(w[G], qa, dist, pc, qq);
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      float acc = 0.f;
-      float d = qq[j].x - pc[j].x;
-      acc = __fmaf_rn(d, d, acc);
-      d = qq[j].y - pc[j].y;
-      acc = __fmaf_rn(d, d, acc);
-      d = qq[j].z - pc[j].z;
-      acc = __fmaf_rn(d, d, acc);
-      d = qq[j].w - pc[j].w;
-      acc = __fmaf_rn(d, d, acc);
-      dist += acc;
-    }
-    return adc_groups<G + 1, MC>(w, qa, dist);
+    qv_float4 pc[4];
+    adc_group_reads<4 * G>(w[G], dist, pc);
+    dist = adc_math4(pc, qd[G], dist);
+    return adc_groups<G + 1, MC, NQ>(w, qd, dist);
   }
 }
-
-typedef float qv_float2 __attribute__((ext_vector_type(2)));
 
 // The same for adc_recompute<MC, 2> (M0 + 3 < 48): the pivot entry of chunk m
 // (8 bytes at 2048 m + 8 c) is one ds_read_b64 from the address 8 c when its
 // offset fits the instruction's 16 bits (m < 32), else one ds_read2st64_b64
-// reading it twice (offsets 4 m in 512-byte units); the query chunks are two
-// broadcast reads of 16 bytes at qa + 8 m.
+// reading it twice (offsets 4 m in 512-byte units).
 template <int M0>
-__device__ __forceinline__ void adc_group_reads2(uint32_t w, uint32_t qa, float dep, qv_float2 (&pc)[4],
-                                                 qv_float4 (&qq)[2]) {
+__device__ __forceinline__ void adc_group_reads2(uint32_t w, float dep, qv_float2 (&pc)[4]) {
   static_assert(M0 % 4 == 0 && M0 + 3 < 48, "chunks of two dimensions, M <= 48");
   uint32_t a0, a1, a2, a3;
   if constexpr (M0 < 32) {
@@ -323,13 +342,11 @@ __device__ __forceinline__ void adc_group_reads2(uint32_t w, uint32_t qa, float 
         "ds_read_b64 %[p1], %[a1] offset:%[o1]\n\t"
         "ds_read_b64 %[p2], %[a2] offset:%[o2]\n\t"
         "ds_read_b64 %[p3], %[a3] offset:%[o3]\n\t"
-        "ds_read_b128 %[q0], %[qa] offset:%[qo0]\n\t"
-        "ds_read_b128 %[q1], %[qa] offset:%[qo1]\n\t"
         "s_waitcnt lgkmcnt(0)"
         : [a0] "=&v"(a0), [a1] "=&v"(a1), [a2] "=&v"(a2), [a3] "=&v"(a3), [p0] "=&v"(pc[0]), [p1] "=&v"(pc[1]),
-          [p2] "=&v"(pc[2]), [p3] "=&v"(pc[3]), [q0] "=&v"(qq[0]), [q1] "=&v"(qq[1])
-        : [w] "v"(w), [qa] "v"(qa), [dep] "v"(dep), [o0] "i"(2048 * M0), [o1] "i"(2048 * (M0 + 1)),
-          [o2] "i"(2048 * (M0 + 2)), [o3] "i"(2048 * (M0 + 3)), [qo0] "i"(8 * M0), [qo1] "i"(8 * M0 + 16));
+          [p2] "=&v"(pc[2]), [p3] "=&v"(pc[3])
+        : [w] "v"(w), [dep] "v"(dep), [o0] "i"(2048 * M0), [o1] "i"(2048 * (M0 + 1)),
+          [o2] "i"(2048 * (M0 + 2)), [o3] "i"(2048 * (M0 + 3)));
   } else {
     qv_float4 t0, t1, t2, t3;
     asm volatile(
@@ -341,13 +358,11 @@ __device__ __forceinline__ void adc_group_reads2(uint32_t w, uint32_t qa, float 
         "ds_read2st64_b64 %[p1], %[a1] offset0:%[o1] offset1:%[o1]\n\t"
         "ds_read2st64_b64 %[p2], %[a2] offset0:%[o2] offset1:%[o2]\n\t"
         "ds_read2st64_b64 %[p3], %[a3] offset0:%[o3] offset1:%[o3]\n\t"
-        "ds_read_b128 %[q0], %[qa] offset:%[qo0]\n\t"
-        "ds_read_b128 %[q1], %[qa] offset:%[qo1]\n\t"
         "s_waitcnt lgkmcnt(0)"
         : [a0] "=&v"(a0), [a1] "=&v"(a1), [a2] "=&v"(a2), [a3] "=&v"(a3), [p0] "=&v"(t0), [p1] "=&v"(t1),
-          [p2] "=&v"(t2), [p3] "=&v"(t3), [q0] "=&v"(qq[0]), [q1] "=&v"(qq[1])
-        : [w] "v"(w), [qa] "v"(qa), [dep] "v"(dep), [o0] "i"(4 * M0), [o1] "i"(4 * (M0 + 1)),
-          [o2] "i"(4 * (M0 + 2)), [o3] "i"(4 * (M0 + 3)), [qo0] "i"(8 * M0), [qo1] "i"(8 * M0 + 16));
+          [p2] "=&v"(t2), [p3] "=&v"(t3)
+        : [w] "v"(w), [dep] "v"(dep), [o0] "i"(4 * M0), [o1] "i"(4 * (M0 + 1)), [o2] "i"(4 * (M0 + 2)),
+          [o3] "i"(4 * (M0 + 3)));
     pc[0] = t0.xy;
     pc[1] = t1.xy;
     pc[2] = t2.xy;
@@ -355,26 +370,43 @@ __device__ __forceinline__ void adc_group_reads2(uint32_t w, uint32_t qa, float 
   }
 }
 
-// Groups G .. MC/4 - 1 of adc_recompute<MC, 2>.
-template <int G, int MC>
-__device__ __forceinline__ float adc_groups2(const uint32_t* w, uint32_t qa, float dist) {
+// adc_math4 for four chunks of 2 dims, whose 8 dims are row lanes B .. B + 7
+// of q.
+template <int B>
+__device__ __forceinline__ float adc_math2(const qv_float2 (&pc)[4], float q, float dist) {
+  static_assert(B == 0 || B == 8, "half a row");
+  float t0, t1, acc;
+#define QV_CHUNK2(P, L0, L1)                                                                   \
+  "v_sub_f32_dpp %[t0], %[q], %[" P "x] row_newbcast:%[" L0 "] row_mask:0xf bank_mask:0xf\n\t" \
+  "v_sub_f32_dpp %[t1], %[q], %[" P "y] row_newbcast:%[" L1 "] row_mask:0xf bank_mask:0xf\n\t" \
+  "v_mul_f32 %[acc], %[t0], %[t0]\n\t"                                                      \
+  "v_fmac_f32 %[acc], %[t1], %[t1]\n\t"                                                     \
+  "v_add_f32 %[dist], %[dist], %[acc]\n\t"
+  asm volatile("s_nop 1\n\t"
+               QV_CHUNK2("p0", "l0", "l1")
+               QV_CHUNK2("p1", "l2", "l3")
+               QV_CHUNK2("p2", "l4", "l5")
+               QV_CHUNK2("p3", "l6", "l7")
+               : [dist] "+v"(dist), [t0] "=&v"(t0), [t1] "=&v"(t1), [acc] "=&v"(acc)
+               : [q] "v"(q), [p0x] "v"(pc[0].x), [p0y] "v"(pc[0].y), [p1x] "v"(pc[1].x), [p1y] "v"(pc[1].y),
+                 [p2x] "v"(pc[2].x), [p2y] "v"(pc[2].y), [p3x] "v"(pc[3].x), [p3y] "v"(pc[3].y), [l0] "i"(B),
+                 [l1] "i"(B + 1), [l2] "i"(B + 2), [l3] "i"(B + 3), [l4] "i"(B + 4), [l5] "i"(B + 5),
+                 [l6] "i"(B + 6), [l7] "i"(B + 7));
+#undef QV_CHUNK2
+  return dist;
+}
+
+// Groups G .. MC/4 - 1 of adc_recompute<MC, 2>; group G's 8 dims are row
+// lanes 8 (G & 1) .. 8 (G & 1) + 7 of qd[G / 2].
+template <int G, int MC, int NQ>
+__device__ __forceinline__ float adc_groups2(const uint32_t* w, const float (&qd)[NQ], float dist) {
   if constexpr (4 * G >= MC) {
     return dist;
   } else {
     qv_float2 pc[4];
-    qv_float4 qq[2];
-    adc_group_reads2<4 * G>(w[G], qa, dist, pc, qq);
-    const float q[8] = {qq[0].x, qq[0].y, qq[0].z, qq[0].w, qq[1].x, qq[1].y, qq[1].z, qq[1].w};
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      float acc = 0.f;
-      float d = q[2 * j] - pc[j].x;
-      acc = __fmaf_rn(d, d, acc);
-      d = q[2 * j + 1] - pc[j].y;
-      acc = __fmaf_rn(d, d, acc);
-      dist += acc;
-    }
-    return adc_groups2<G + 1, MC>(w, qa, dist);
+    adc_group_reads2<4 * G>(w[G], dist, pc);
+    dist = adc_math2<8 * (G & 1)>(pc, qd[G / 2], dist);
+    return adc_groups2<G + 1, MC, NQ>(w, qd, dist);
   }
 }
 
@@ -396,24 +428,32 @@ __host__ __device__ __forceinline__ int piv_index(int i, int c) {
 // read from a per-query table: LUT[m][c] is the fused chain
 // acc = fma(q'_i - P[c][i], q'_i - P[c][i], acc) over the SC dims i of chunk m
 // from acc = 0 (the LUT build's own order), then dist += LUT[m][c] in chunk
-// order, so the result is the table ADC's bit for bit.  piv holds P as
-// piv_index<SC> places it (LDS at address 0, shared by the waves of a
-// workgroup); qv holds q' (LDS, read as broadcasts).
-template <int MC, int SC>
-__device__ __forceinline__ float adc_recompute(const CodeRow<MC>& cr, const float* __restrict__ qv,
-                                               const float* __restrict__ piv) {
-  // the pivot table sits at LDS address 0 (piv), the query at qv
-  (void)piv;
-  float dist = 0.f;
+// order, so the result is the table ADC's bit for bit.  The pivots sit in LDS
+// at address 0 as piv_index<SC> places them (shared by the waves of a
+// workgroup); qd holds q' as adc_math4 / adc_math2 read it (load_query_dpp).
+template <int MC, int SC, int NQ>
+__device__ __forceinline__ float adc_recompute(const CodeRow<MC>& cr, const float (&qd)[NQ]) {
+  static_assert(MC % 4 == 0, "chunks in groups of four");
+  static_assert(16 * NQ >= MC * SC, "every dimension in the query registers");
   if constexpr (SC == 4) {
-    static_assert(MC % 4 == 0, "chunks in groups of four");
-    dist = adc_groups<0, MC>(cr.w, (uint32_t)(uintptr_t)qv, dist);
+    return adc_groups<0, MC, NQ>(cr.w, qd, 0.f);
   } else {
     static_assert(SC == 2, "chunks of 2 or 4 dimensions");
-    static_assert(MC % 4 == 0, "chunks in groups of four");
-    dist = adc_groups2<0, MC>(cr.w, (uint32_t)(uintptr_t)qv, dist);
+    return adc_groups2<0, MC, NQ>(cr.w, qd, 0.f);
   }
-  return dist;
+}
+
+// q' (LDS, dim elements) into the registers adc_math4 / adc_math2 read: lane l takes
+// element 16 j + (l & 15) into qd[j] (0 past dim).
+template <int NQ>
+__device__ __forceinline__ void load_query_dpp(const float* __restrict__ qc_lds, int dim, int lane,
+                                               float (&qd)[NQ]) {
+#pragma unroll
+  for (int j = 0; j < NQ; j++) {
+    const int i = 16 * j + (lane & 15);
+    const float v = qc_lds[min(i, dim - 1)];
+    qd[j] = i < dim ? v : 0.f;
+  }
 }
 
 // Sequential fp32 ADC of one code row against an LDS LUT

@@ -90,11 +90,11 @@ enum : int32_t { kErrSpinTimeout = 1 };
 // Dynamic LDS carve-up of one query (one wave), shared by the kernel and its
 // launcher.  Q = beam positions per lane: the register beam holds Q * 64 >= ef
 // entries, the LDS beam cap of them (beam_cap).  With a per-query LUT (lut) the
-// table comes first; the shared-
-// pivot kernel has none, and when every query element the exact distance
-// needs fits the lanes' registers (dim <= 32 kVecPre) its beam overlays the
-// query copy qu, which is only read once, into those registers, before the
-// first hop.
+// table comes first; the shared-pivot kernel has none, and when every query
+// element the exact distance needs fits the lanes' registers
+// (dim <= 32 kVecPre) its beam overlays both query copies, qc and qu, which
+// are only read once, into registers (load_query_dpp, load_query_pre),
+// before the first hop.
 struct LdsPlan {
   int lut_off, qc_off, qu_off, beam_off, total;
 };
@@ -111,9 +111,9 @@ __host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool
   const int dpad = (dim + 3) & ~3;
   p.qu_off = p.qc_off + dpad * 4;
   const bool overlay = !lut && dim <= 32 * kVecPre;
-  p.beam_off = overlay ? p.qu_off : (p.qu_off + dpad * 4 + 15) & ~15;
+  p.beam_off = overlay ? p.qc_off : (p.qu_off + dpad * 4 + 15) & ~15;
   const int beam_bytes = beam_cap(ef, Q, lut) * 8;
-  p.total = p.beam_off + (overlay && dpad * 4 > beam_bytes ? dpad * 4 : beam_bytes);
+  p.total = p.beam_off + (overlay && 2 * dpad * 4 > beam_bytes ? 2 * dpad * 4 : beam_bytes);
   return p;
 }
 
@@ -168,6 +168,9 @@ struct Query {
   float* qc;
   float* qu;
   float quv[kVecPre];  // qu elements of this lane for the exact distance
+  // q' for the shared-pivot ADC, 16 elements per register (load_query_dpp)
+  static constexpr int kQd = SC > 0 ? (MC * SC + 15) / 16 : 1;
+  float qd[kQd];
   uint64_t* beam;
   uint32_t* bits;  // this slot's membership bitmap (SC == 0)
   int sz;        // beam size (ctx.size)
@@ -323,7 +326,7 @@ struct Query {
       if constexpr (PF) fetch(spec ? (int32_t)key_id(bu) : v, lane, nr);
       exact_and_topk(v, xv, rec, lane);
       if constexpr (SC > 0)
-        d = adc_recompute<MC, SC>(cr, qc, piv);
+        d = adc_recompute<MC, SC, kQd>(cr, qd);
       else
         d = adc_sum<MC>(cr, lut);
       // the guessed successor's code rows (lanes past its degree read row 0)
@@ -388,8 +391,8 @@ struct Query {
       if constexpr (PF) fetch(spec ? (int32_t)key_id(bu) : v, lane, nr);
       exact_and_topk(v, xv, rec, lane);
       if constexpr (SC > 0) {
-        d0 = adc_recompute<MC, SC>(c0, qc, piv);
-        d1 = adc_recompute<MC, SC>(c1, qc, piv);
+        d0 = adc_recompute<MC, SC, kQd>(c0, qd);
+        d1 = adc_recompute<MC, SC, kQd>(c1, qd);
       } else {
         d0 = adc_sum<MC>(c0, lut);
         d1 = adc_sum<MC>(c1, lut);
@@ -418,6 +421,15 @@ struct Query {
       for (int k = 0; k < Q; k++)
         if (k * kWave + lane < cap) beam[k * kWave + lane] = kPadKey;
     }
+  }
+
+  // Beam position P from the register copy (kPadKey past it), wave-uniform.
+  template <int P>
+  __device__ __forceinline__ uint64_t reg_pos() const {
+    if constexpr (P < Q * kWave)
+      return read_lane_u64(ck[P % Q], P / Q);
+    else
+      return kPadKey;
   }
 
   // First unvisited entry of the beam from the register copy.
@@ -495,12 +507,23 @@ struct Query {
         // and adds s per key below; steps 4^i from kTop cover 4 kTop - 1 >=
         // 64 Q - 1 positions.  The last level (s = 1) also reads r + 3, so
         // beam[r] for the membership test is one of its four keys.
+        //
+        // The first level (r = 0 in every lane) reads the same three positions
+        // for every lane, so it compares against the register beam's copies,
+        // read as wave-uniform values: the same keys, or kPadKey past sz where
+        // the LDS read would be clamped to cap - 1 -- equal for the
+        // comparison, since a below candidate is under the last key of a
+        // full beam.  Visited bits do not matter: e < c0 ignores them.
         constexpr int kCap = Q * kWave;
         constexpr int kTop = kCap <= 64 ? 16 : (kCap <= 256 ? 64 : 256);
         const int top = cap - 1;
         const uint64_t c0 = nkey & ~1ull;
+        {
+          const uint64_t e1 = reg_pos<kTop - 1>(), e2 = reg_pos<2 * kTop - 1>(), e3 = reg_pos<3 * kTop - 1>();
+          r = ((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * kTop;
+        }
 #pragma unroll
-        for (int step = kTop; step > 1; step >>= 2) {
+        for (int step = kTop / 4; step > 1; step >>= 2) {
           const uint64_t e1 = beam[min(r + step - 1, top)];
           const uint64_t e2 = beam[min(r + 2 * step - 1, top)];
           const uint64_t e3 = beam[min(r + 3 * step - 1, top)];
@@ -713,8 +736,9 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       query_sync<SC>();
     }
     load_query_pre(Qy.qu, a.dim, lane, Qy.quv);
-    // qu may share its LDS with the beam (lds_plan): no beam store may move
-    // above these reads.
+    if constexpr (SC > 0) load_query_dpp(Qy.qc, a.dim, lane, Qy.qd);
+    // qc and qu may share their LDS with the beam (lds_plan): no beam store
+    // may move above these reads.
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     Qy.pad_beam(lane);
 
@@ -732,7 +756,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       g.last_fc = fc;
       g.last_top1 = top1;
       g.last_topk = topk;
-      return gpr && step >= a.warmup && a.patience > 0 && g.no_improve >= a.patience;
+      return step >= a.warmup && a.patience > 0 && g.no_improve >= a.patience;
     };
 
     // count_topk_gt_hits (kernel_helpers.cuh:520-535): top-k entries (a
@@ -779,7 +803,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
         const int32_t nx = Qy.template hop<true>(v, nr, cr, have);
         log_hop(v);
         ++step;
-        if (check()) {
+        if (gpr && check()) {
           stop = true;
           break;
         }
@@ -803,7 +827,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     int32_t first = expand(entry);
     log_hop(entry);
     step = 1;
-    if (check()) {
+    if (gpr && check()) {
       stop = true;
       first = -1;
     }
@@ -827,7 +851,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
         int32_t nx = expand(v);
         log_hop(v);
         ++step;
-        if (check()) {
+        if (gpr && check()) {
           stop = true;
           nx = -1;
         }
