@@ -265,8 +265,11 @@ struct Query {
 
   // One expansion of node v: persistent_merge_data (kernel_helpers.cuh:232-357)
   // followed by persistent_visit_select_dualwarp (kernel_helpers.cuh:422-489).
-  // nr holds v's record (fetch); with PF the selected next node's record is
-  // requested into nr as soon as it is known.  Returns the next node or -1.
+  // nr holds v's record (fetch).  Returns the selected node or -1.  PF says
+  // which node's record the hop requests into nr once it has read v's: 0 none,
+  // 1 the speculated successor (below; with PF = 1 the selected node's record
+  // is also requested as soon as the merge knows it, when the guess missed),
+  // 2 the caller's nxt (the pipe lanes' next expansion; -1: not known).
   //
   // With PF, cr carries code rows from one hop to the next: when `have`, cr
   // holds (or is loading) v's neighbours' rows, requested by the previous hop.
@@ -274,10 +277,11 @@ struct Query {
   // requests that node's record at its start and, once the ADC no longer
   // needs cr, that node's code rows, so the next hop's rows are in flight
   // through this hop's merge; `have` is set when the guess was the node
-  // selected.  Only loads move: every result is the same.
-  template <bool PF>
-  __device__ __forceinline__ int32_t hop(int32_t v, Rec& nr, CodeRow<MC>& cr, bool& have) {
-    if constexpr (NPL == 2) return hop2<PF>(v, nr);
+  // selected.  PF = 2 does the same for nxt, and `have` says nxt's rows are
+  // in cr.  Only loads move: every result is the same.
+  template <int PF>
+  __device__ __forceinline__ int32_t hop(int32_t v, Rec& nr, CodeRow<MC>& cr, bool& have, int32_t nxt = -1) {
+    if constexpr (NPL == 2) return hop2<PF == 1>(v, nr);
     const int lane = opaque_lane();
     const int deg = read_lane_i32(nr.deg, 0);
     evals += deg;
@@ -291,7 +295,7 @@ struct Query {
     // (whenever no new candidate beats it), so its record is requested right
     // after this hop's code rows, and the merge only requests another record
     // when a candidate wins.
-    const bool spec = PF && u < sz;
+    const bool spec = PF == 1 && u < sz;
 
     // Beam membership of each neighbour from the bitmap.  The bitmap updates
     // of the previous hop were issued before this hop's record arrived;
@@ -313,7 +317,7 @@ struct Query {
     // the chosen node's rows follow its record at once.
     const bool blk = a.nbr_codes != nullptr;
     if constexpr (MC > 0 && MC % 16 == 0) {
-      if (!(PF && have)) {
+      if (!(PF != 0 && have)) {
         if (blk)
           adc_load<MC>(cr, block_row(v));
         else
@@ -323,17 +327,22 @@ struct Query {
       // to guess), so every path reaches the ADC with the same loads in
       // flight and the compiler's wait for the code rows can leave the
       // record outstanding.
-      if constexpr (PF) fetch(spec ? (int32_t)key_id(bu) : v, lane, nr);
+      if constexpr (PF == 1) fetch(spec ? (int32_t)key_id(bu) : v, lane, nr);
+      if constexpr (PF == 2) {
+        if (nxt >= 0) fetch(nxt, lane, nr);
+      }
       exact_and_topk(v, xv, rec, lane);
       if constexpr (SC > 0)
         d = adc_recompute<MC, SC, kQd>(cr, qd);
       else
         d = adc_sum<MC>(cr, lut);
-      // the guessed successor's code rows (lanes past its degree read row 0)
-      if constexpr (PF) {
-        if (spec) {
+      // the next node's code rows (lanes past its degree read row 0): the
+      // guessed successor's (PF = 1) or nxt's (PF = 2)
+      if constexpr (PF != 0) {
+        const bool go = PF == 1 ? spec : nxt >= 0;
+        if (go) {
           if (blk) {
-            adc_load<MC>(cr, block_row((int32_t)key_id(bu)));
+            adc_load<MC>(cr, block_row(PF == 1 ? (int32_t)key_id(bu) : nxt));
           } else {
             const int ndeg = read_lane_i32(nr.deg, 0);
             adc_load<MC>(cr, a.codes, lane < ndeg ? nr.nbr[0] : 0u);
@@ -341,18 +350,20 @@ struct Query {
         }
       }
     } else {
-      if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
+      if (PF == 1 && spec) fetch((int32_t)key_id(bu), lane, nr);
+      if (PF == 2 && nxt >= 0) fetch(nxt, lane, nr);
       d = adc_row<MC>(a.codes + (int64_t)nbr * a.num_chunks, lut, a.num_chunks);
       exact_and_topk(v, xv, rec, lane);
     }
     const uint64_t nkey = has ? make_key(d, nbr, false) : sentinel_key(lane);
     const bool fresh = kBits ? has && !((bword >> (nbr & 31)) & 1u) : has;
     bool hit = false;
-    const int32_t nx = merge_select<true, PF>(nkey, fresh, lane, nr, spec, bu, hit);
-    if constexpr (PF && MC > 0 && MC % 16 == 0) {
+    const int32_t nx = merge_select<true, PF == 1>(nkey, fresh, lane, nr, spec, bu, hit);
+    if constexpr (PF == 1 && MC > 0 && MC % 16 == 0) {
       if (blk && !hit && nx >= 0) adc_load<MC>(cr, block_row(nx));
       have = hit || (blk && nx >= 0);
     }
+    if constexpr (PF == 2 && MC > 0 && MC % 16 == 0) have = nxt >= 0;
     return nx;
   }
 
@@ -788,9 +799,18 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     NodeRec<NPL> nr;
     CodeRow<MC> cr;
     bool have = false;
-    auto expand = [&](int32_t v) -> int32_t {
-      Qy.fetch(v, lane, nr);
-      return Qy.template hop<false>(v, nr, cr, have);
+    // Expansion for the pipe lanes: nxt is the expansion expected next (-1:
+    // not known), whose record (and rows) the hop requests once it has read
+    // v's; pf is the node so requested, fetched again when the guess was wrong.
+    int32_t pf = -1;
+    auto expand = [&](int32_t v, int32_t nxt) -> int32_t {
+      if (v != pf) {
+        Qy.fetch(v, lane, nr);
+        have = false;
+      }
+      const int32_t nx = Qy.template hop<2>(v, nr, cr, have, nxt);
+      pf = NPL == 1 ? nxt : -1;
+      return nx;
     };
 
     if (a.pipe_w == 1) {
@@ -800,7 +820,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       Qy.fetch(entry, lane, nr);
       int32_t v = entry;
       while (true) {
-        const int32_t nx = Qy.template hop<true>(v, nr, cr, have);
+        const int32_t nx = Qy.template hop<1>(v, nr, cr, have);
         log_hop(v);
         ++step;
         if (gpr && check()) {
@@ -824,7 +844,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     }
     {
     // ---- boot (kernel_q1.cuh:199-397)
-    int32_t first = expand(entry);
+    int32_t first = expand(entry, -1);
     log_hop(entry);
     step = 1;
     if (gpr && check()) {
@@ -848,7 +868,14 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       for (int w = 0; w < W; w++) {
         if (!(cur & (1u << w))) continue;
         const int32_t v = read_lane_i32(pipe_node, w);
-        int32_t nx = expand(v);
+        // expected next: the round's next issued lane, else the node this
+        // round gave its first lane (the next round starts there unless an
+        // idle lane below it is refilled)
+        const uint32_t later = cur & ~((2u << w) - 1u);
+        const int f = __builtin_ctz(cur);
+        const int32_t nxt = later ? read_lane_i32(pipe_node, __builtin_ctz(later))
+                                  : (f == w ? -1 : read_lane_i32(pipe_node, f));
+        int32_t nx = expand(v, nxt);
         log_hop(v);
         ++step;
         if (gpr && check()) {
