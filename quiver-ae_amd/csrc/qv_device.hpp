@@ -249,31 +249,52 @@ typedef float qv_float2 __attribute__((ext_vector_type(2)));
 // Pivot reads of one group of four chunks (M0 .. M0 + 3, whose codes are the
 // bytes of the code word w) for adc_recompute<MC, 4>, in one block so that
 // the group costs one LDS round trip: per chunk, an SDWA shift (the source
-// operand selects the byte) makes the address 8 c of the pivot entry, whose
-// two halves one ds_read2st64_b64 reads at 4096 m and 4096 m + 2048 (offsets
-// 8 m and 8 m + 4 in 512-byte units) from the pivot table at LDS address 0.
-// The block ends with its own wait, since the compiler does not count these
+// operand selects the byte) makes the address 16 c of the pivot entry (its 4
+// dims contiguous, 16 bytes), which one ds_read_b128 reads at 4096 m + 16 c
+// from the pivot table at LDS address 0.  The 16-bit instruction offset
+// reaches chunks below 16; above, the address gets 65536 added first.  The
+// block ends with its own wait, since the compiler does not count these
 // reads.  dep is not read: it orders the block after the previous group's
 // arithmetic, so a group's operands are the only ones held at a time.
 template <int M0>
 __device__ __forceinline__ void adc_group_reads(uint32_t w, float dep, qv_float4 (&pc)[4]) {
-  static_assert(M0 % 4 == 0 && M0 + 3 < 32, "read2st64 offsets cover 32 chunks");
+  static_assert(M0 % 4 == 0 && M0 + 3 < 32, "32 chunks of 4 KB");
   uint32_t a0, a1, a2, a3;
+  if constexpr (M0 < 16) {
   asm volatile(
-      "v_lshlrev_b32_sdwa %[a0], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0\n\t"
-      "v_lshlrev_b32_sdwa %[a1], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1\n\t"
-      "v_lshlrev_b32_sdwa %[a2], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2\n\t"
-      "v_lshlrev_b32_sdwa %[a3], 3, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3\n\t"
-      "ds_read2st64_b64 %[p0], %[a0] offset0:%[o0] offset1:%[o0h]\n\t"
-      "ds_read2st64_b64 %[p1], %[a1] offset0:%[o1] offset1:%[o1h]\n\t"
-      "ds_read2st64_b64 %[p2], %[a2] offset0:%[o2] offset1:%[o2h]\n\t"
-      "ds_read2st64_b64 %[p3], %[a3] offset0:%[o3] offset1:%[o3h]\n\t"
+      "v_lshlrev_b32_sdwa %[a0], 4, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0\n\t"
+      "v_lshlrev_b32_sdwa %[a1], 4, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1\n\t"
+      "v_lshlrev_b32_sdwa %[a2], 4, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2\n\t"
+      "v_lshlrev_b32_sdwa %[a3], 4, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3\n\t"
+      "ds_read_b128 %[p0], %[a0] offset:%[o0]\n\t"
+      "ds_read_b128 %[p1], %[a1] offset:%[o1]\n\t"
+      "ds_read_b128 %[p2], %[a2] offset:%[o2]\n\t"
+      "ds_read_b128 %[p3], %[a3] offset:%[o3]\n\t"
       "s_waitcnt lgkmcnt(0)"
       : [a0] "=&v"(a0), [a1] "=&v"(a1), [a2] "=&v"(a2), [a3] "=&v"(a3), [p0] "=&v"(pc[0]), [p1] "=&v"(pc[1]),
         [p2] "=&v"(pc[2]), [p3] "=&v"(pc[3])
-      : [w] "v"(w), [dep] "v"(dep), [o0] "i"(8 * M0), [o0h] "i"(8 * M0 + 4), [o1] "i"(8 * M0 + 8),
-        [o1h] "i"(8 * M0 + 12), [o2] "i"(8 * M0 + 16), [o2h] "i"(8 * M0 + 20), [o3] "i"(8 * M0 + 24),
-        [o3h] "i"(8 * M0 + 28));
+      : [w] "v"(w), [dep] "v"(dep), [o0] "i"(4096 * M0), [o1] "i"(4096 * (M0 + 1)), [o2] "i"(4096 * (M0 + 2)),
+        [o3] "i"(4096 * (M0 + 3)));
+  } else {
+  asm volatile(
+      "v_lshlrev_b32_sdwa %[a0], 4, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0\n\t"
+      "v_lshlrev_b32_sdwa %[a1], 4, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1\n\t"
+      "v_lshlrev_b32_sdwa %[a2], 4, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2\n\t"
+      "v_lshlrev_b32_sdwa %[a3], 4, %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3\n\t"
+      "v_add_u32 %[a0], 0x10000, %[a0]\n\t"
+      "v_add_u32 %[a1], 0x10000, %[a1]\n\t"
+      "v_add_u32 %[a2], 0x10000, %[a2]\n\t"
+      "v_add_u32 %[a3], 0x10000, %[a3]\n\t"
+      "ds_read_b128 %[p0], %[a0] offset:%[o0]\n\t"
+      "ds_read_b128 %[p1], %[a1] offset:%[o1]\n\t"
+      "ds_read_b128 %[p2], %[a2] offset:%[o2]\n\t"
+      "ds_read_b128 %[p3], %[a3] offset:%[o3]\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : [a0] "=&v"(a0), [a1] "=&v"(a1), [a2] "=&v"(a2), [a3] "=&v"(a3), [p0] "=&v"(pc[0]), [p1] "=&v"(pc[1]),
+        [p2] "=&v"(pc[2]), [p3] "=&v"(pc[3])
+      : [w] "v"(w), [dep] "v"(dep), [o0] "i"(4096 * M0 - 65536), [o1] "i"(4096 * (M0 + 1) - 65536),
+        [o2] "i"(4096 * (M0 + 2) - 65536), [o3] "i"(4096 * (M0 + 3) - 65536));
+  }
 }
 
 // The arithmetic of one group of four chunks of 4 dims: per chunk, in its
@@ -412,14 +433,14 @@ __device__ __forceinline__ float adc_groups2(const uint32_t* w, const float (&qd
 
 // LDS float index of pivot dimension i for code c in the shared pivot table
 // of adc_recompute<MC, SC>:
-//  SC = 4: chunk m owns bytes [4096 m, 4096 (m + 1)); dims 0-1 of code c at
-//          4096 m + 8 c, dims 2-3 at 4096 m + 2048 + 8 c (adc_group_reads);
+//  SC = 4: entry (m, c) at float (m * 256 + c) * 4, its 4 dims contiguous
+//          (one ds_read_b128 in adc_group_reads);
 //  SC = 2: entry (m, c) at float (m * 256 + c) * 2 (adc_group_reads2).
 template <int SC>
 __host__ __device__ __forceinline__ int piv_index(int i, int c) {
   const int m = i / SC, j = i % SC;
   if constexpr (SC == 4)
-    return m * 1024 + (j >> 1) * 512 + c * 2 + (j & 1);
+    return m * 1024 + c * 4 + j;
   else
     return (m * 256 + c) * SC + j;
 }

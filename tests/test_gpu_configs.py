@@ -118,7 +118,7 @@ def _same(got, want, what):
 
 @pytest.mark.parametrize("kernel", ["lut", "shared-pivots"])
 @pytest.mark.parametrize("policy", ["none", "gpruning"])
-@pytest.mark.parametrize("ef", [45, 64, 128, 240, 288])
+@pytest.mark.parametrize("ef", [45, 64, 128, 240, 256, 288])
 def test_c1_matches_oracle(c1, kernel, policy, ef):
     _say(f"[gpu] C1 kernel={kernel} policy={policy} ef={ef}")
     rc, got = _search(c1, c1["q"][:NQ], ef, policy, kernel)
@@ -132,13 +132,16 @@ def test_c1_matches_oracle(c1, kernel, policy, ef):
         assert r_gpu >= 0.90, f"Recall@10 {r_gpu:.4f} at ef={ef}"
 
 
-@pytest.mark.parametrize("pipe", [2, 4])
-def test_c1_pipe_lanes_match_oracle(c1, pipe):
-    _say(f"[gpu] C1 pipe_width={pipe}")
+@pytest.mark.parametrize("pipe,ef,policy", [(2, 128, "gpruning"), (4, 128, "gpruning"), (2, 256, "none"),
+                                             (3, 45, "none")])
+def test_c1_pipe_lanes_match_oracle(c1, pipe, ef, policy):
+    """Pipe lanes, whose expansions request the record and code rows of the
+    expansion expected next (a wrong guess is fetched again)."""
+    _say(f"[gpu] C1 pipe_width={pipe} ef={ef} policy={policy}")
     for kernel in ("lut", "shared-pivots"):
-        rc, got = _search(c1, c1["q"][:500], 128, "gpruning", kernel, pipe=pipe)
+        rc, got = _search(c1, c1["q"][:500], ef, policy, kernel, pipe=pipe)
         assert rc == 0
-        _same(got, _oracle(c1, 128, "gpruning", pipe=pipe, n=500), f"{kernel} W={pipe}")
+        _same(got, _oracle(c1, ef, policy, pipe=pipe, n=500), f"{kernel} W={pipe} ef={ef} {policy}")
 
 
 @pytest.mark.parametrize("batch", [1, 16, 256])

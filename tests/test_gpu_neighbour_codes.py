@@ -54,7 +54,7 @@ def _search(lib, L, h, q, ef, policy, kernel, pipe):
 
 
 @pytest.mark.parametrize("kernel", ["lut", "shared-pivots"])
-@pytest.mark.parametrize("pipe", [1, 2])
+@pytest.mark.parametrize("pipe", [1, 2, 4])
 @pytest.mark.parametrize("policy", ["none", "gpruning"])
 @pytest.mark.parametrize("ef", [24, 100, 300, 700])
 def test_with_neighbour_codes_matches_oracle(opened, ef, policy, pipe, kernel):
