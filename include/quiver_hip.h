@@ -248,19 +248,15 @@ int qv_search(qv_index* index, const float* queries, int64_t nq, int32_t dim,
  * hipMalloc): qv_search with every query admitted at launch, all of
  * d_queries / d_ids / d_dists / d_found (may be NULL) device pointers, and
  * the search's scratch (dispatch counters, per-query hop and evaluation
- * counts, the per-query-LUT kernel's beam-membership bitmaps) taken from one
- * fixed device array of QV_NOALLOC_SCRATCH_BYTES per GPU, held until the
- * process ends.  It calls no hipMalloc, hipHostMalloc, hipFree or memset.
- * Limits: 1..QV_NOALLOC_MAX_QUERIES queries per call (QV_EINVAL beyond);
- * opts->timeout_s must be 0 (no deadline); the per-query-LUT kernel launches at
- * most as many query slots as the array's bitmap region holds (n / 8 bytes
- * each; QV_EUNSUPPORTED when not even one fits, about 200M points), and with
- * QV_KERNEL_AUTO the shared-pivot kernel is taken instead when that would cut
- * the slots and the index allows it.  Results equal qv_search's.  Calls share
- * the GPU's array: calls from one process are serialised; work captured from
- * it and replayed concurrently on one GPU races.  Blocking; the report has no
- * latency percentiles (queries are not stamped). */
-#define QV_NOALLOC_SCRATCH_BYTES (32 * 1024 * 1024)
+ * counts) taken from one fixed device array of QV_NOALLOC_SCRATCH_BYTES per
+ * GPU, held until the process ends.  It calls no hipMalloc, hipHostMalloc,
+ * hipFree or memset.  Limits: 1..QV_NOALLOC_MAX_QUERIES queries per call
+ * (QV_EINVAL beyond); opts->timeout_s must be 0 (no deadline).  Results equal
+ * qv_search's.  Calls share the GPU's array: calls from one process are
+ * serialised; work captured from it and replayed concurrently on one GPU
+ * races.  Blocking; the report has no latency percentiles (queries are not
+ * stamped). */
+#define QV_NOALLOC_SCRATCH_BYTES (8 * 1024 * 1024 + 256)
 #define QV_NOALLOC_MAX_QUERIES (1024 * 1024)
 int qv_search_noalloc(qv_index* index, const float* d_queries, int64_t nq, int32_t dim,
                       int32_t topk, int32_t ef_search, const qv_search_opts* opts,

@@ -48,9 +48,6 @@ struct qv_index {
   uint64_t* d_tstart = nullptr;
   uint64_t* d_tend = nullptr;
   int32_t* d_counters = nullptr;
-  uint32_t* d_bits = nullptr;  // beam membership bitmaps (per-query-LUT kernel), bits_slots x bits_words
-  int64_t bits_slots = 0, bits_words = 0;
-  bool bits_dirty = false;     // set while a launch may have left bits behind
   int32_t* h_ctrl = nullptr;   // [0] feed_count, [1] terminate (host-coherent)
   int32_t* h_ring = nullptr;   // [cap_q] completion ring (host-coherent)
   int32_t* h_stage = nullptr;  // pinned: counters[4], hops, stopped, evals [cap_q each]

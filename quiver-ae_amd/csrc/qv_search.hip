@@ -11,8 +11,7 @@
 //     poll threads, no 4 KB page copies), and the next node's record is
 //     requested while the current hop finishes;
 //   * the merge is built by rank: "is this neighbour already in the beam" is
-//     answered by a per-query bitmap in HBM (per-query-LUT kernel) or by the
-//     neighbour's own rank in the sorted LDS beam (shared-pivot kernel: a beam
+//     answered by the neighbour's own rank in the sorted LDS beam (a beam
 //     entry of the same id has the same key), and the few new candidates are
 //     scattered into LDS in place, instead of merge-path rounds with block
 //     barriers;
@@ -242,17 +241,13 @@ LaunchShape shape_launch(const LaunchPlan& lp, int64_t slots, int num_cus) {
 //   [0, 256)                     dispatch counters (ticket, done, error bits)
 //   [256, +4 kNoAllocMaxQueries) per-query hop counts
 //   [.., +4 kNoAllocMaxQueries)  per-query ADC evaluation counts
-//   [kNoAllocBitsOff, end)       beam-membership bitmaps of the per-query-LUT
-//                                kernel (zero between queries, as ensure_bits'),
-//                                as many query slots as fit
 // Host code never uses the symbol's name as an address: each device's copy is
 // looked up once with hipGetSymbolAddress.
 constexpr int64_t kNoAllocBytes = QV_NOALLOC_SCRATCH_BYTES;
 constexpr int64_t kNoAllocMaxQueries = QV_NOALLOC_MAX_QUERIES;
 constexpr int64_t kNoAllocHopsOff = 256;
 constexpr int64_t kNoAllocEvalsOff = kNoAllocHopsOff + 4 * kNoAllocMaxQueries;
-constexpr int64_t kNoAllocBitsOff = kNoAllocEvalsOff + 4 * kNoAllocMaxQueries;
-static_assert(kNoAllocBitsOff < kNoAllocBytes, "no room for bitmaps");
+static_assert(kNoAllocEvalsOff + 4 * kNoAllocMaxQueries <= kNoAllocBytes, "scratch holds every count");
 __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
 
 // Zero fill by vector stores (no hipMemsetAsync: a caller may capture the
@@ -308,31 +303,6 @@ static void free_scratch(qv_index* ix) {
   ix->cap_k = 0;
 }
 
-// Beam membership bitmaps of the per-query-LUT kernel, one per query slot,
-// zero between queries (each query clears the bits of its final beam).
-// Reallocated when more slots are launched and zeroed again after a search
-// that did not finish.
-static void ensure_bits(qv_index* ix, int64_t slots) {
-  const int64_t words = ((ix->lay.num_data + 31) / 32 + 15) / 16 * 16;
-  if (slots > ix->bits_slots || words != ix->bits_words) {
-    hipFree(ix->d_bits);
-    ix->d_bits = nullptr;
-    ix->bits_slots = 0;
-    HIP_OK(hipMalloc(&ix->d_bits, sizeof(uint32_t) * (size_t)(slots * words)));
-    ix->bits_slots = slots;
-    ix->bits_words = words;
-    ix->bits_dirty = true;
-  }
-  if (ix->bits_dirty) {
-    // On the search stream, so the next kernel starts after it (a plain
-    // hipMemset runs on the null stream, which the non-blocking search stream
-    // does not wait for).
-    HIP_OK(hipMemsetAsync(ix->d_bits, 0, sizeof(uint32_t) * (size_t)(ix->bits_slots * ix->bits_words),
-                          ix->stream));
-    ix->bits_dirty = false;
-  }
-}
-
 static void ensure_scratch(qv_index* ix, int64_t nq, int k) {
   if (!ix->d_counters) {
     HIP_OK(hipMalloc(&ix->d_counters, 64));
@@ -365,7 +335,6 @@ void release_index(qv_index* ix) {
   free_scratch(ix);
   hipFree(ix->d_counters);
   hipHostFree(ix->h_ctrl);
-  hipFree(ix->d_bits);
   hipFree(ix->d_nav_data);
   hipFree(ix->d_nav_graph);
   hipFree(ix->d_nav_map);
@@ -832,8 +801,6 @@ static SearchArgs base_args(qv_index* ix) {
   a.num_chunks = ix->M;
   a.max_m = (int32_t)L.max_m0;
   a.medoid = (int32_t)L.enter_point;
-  a.bits = ix->d_bits;
-  a.bits_words = ix->bits_words;
   a.nav_data = ix->d_nav_data;
   a.nav_graph = ix->d_nav_graph;
   a.nav_map = ix->d_nav_map;
@@ -859,8 +826,6 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
   nb = (int)std::min<int64_t>(std::min<int64_t>(nb, nq), (int64_t)lp.slots_per_cu * ix->num_cus);
   const LaunchShape ls = shape_launch(lp, nb, ix->num_cus);
   const int grid = ls.grid;
-  const bool use_bits = lp.variant == QV_KERNEL_LUT;
-  if (use_bits) ensure_bits(ix, (int64_t)grid * ls.waves);
   SearchArgs a = base_args(ix);
   a.queries = d_queries;
   a.nq = (int32_t)nq;
@@ -887,13 +852,11 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
   a.rec_dists = rec.dists;
   a.rec_cap = rec.cap;
   HIP_OK(hipMemsetAsync(ix->d_counters, 0, 64, ix->stream));
-  if (use_bits) ix->bits_dirty = true;
   hipLaunchKernelGGL(lp.kern, dim3(grid), dim3(kWave * ls.waves), (size_t)ls.lds, ix->stream, a);
   HIP_OK(hipGetLastError());
   HIP_OK(hipStreamSynchronize(ix->stream));
   int32_t counters[4] = {0, 0, 0, 0};
   HIP_OK(hipMemcpy(counters, ix->d_counters, sizeof(counters), hipMemcpyDeviceToHost));
-  if (use_bits) ix->bits_dirty = counters[1] < nq;  // conservative: zeroed again before the next launch
   if (counters[1] != nq)
     fail(QV_EHIP, "record search finished " + std::to_string(counters[1]) + " of " + std::to_string(nq) + " queries");
 }
@@ -959,8 +922,6 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     fail(QV_EINVAL, "admission must be QV_ADMIT_STREAMING, QV_ADMIT_BATCH or QV_ADMIT_STATIC");
   const int max_inflight = (int)std::min<int64_t>(
       nq, o.admission == QV_ADMIT_STATIC ? slots : slots + std::max(0, o.prefeed));
-  const bool use_bits = lp.variant == QV_KERNEL_LUT;
-  if (use_bits) ensure_bits(ix, num_blocks);
 
   const float* d_q = queries;
   if (!o.device_buffers) {
@@ -1044,7 +1005,6 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   }
 
   using clock = std::chrono::steady_clock;
-  if (use_bits) ix->bits_dirty = true;  // until every admitted query is seen to finish
   HIP_OK(hipEventRecord(ix->ev0, ix->stream));
   hipLaunchKernelGGL(lp.kern, dim3(grid), dim3(kWave * ls.waves), (size_t)ls.lds, ix->stream, a);
   HIP_OK(hipGetLastError());
@@ -1156,8 +1116,6 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   HIP_OK(hipStreamSynchronize(ix->stream));
   int32_t counters[4];
   std::memcpy(counters, st_counters, sizeof(counters));
-  // every query that took a ticket below nq ran to its end and cleared its bits
-  if (use_bits) ix->bits_dirty = counters[1] < std::min<int64_t>(counters[0], nq);
   if (counters[2] & kErrSpinTimeout) fail(QV_ETIMEDOUT, "search kernel watchdog: feed wait exceeded its limit");
   if (timed_out || counters[1] < nq) {
     char buf[96];
@@ -1223,10 +1181,9 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
 
 // ---- allocation-free search -------------------------------------------------
 // Per device: the address of its copy of `scratch` (hipGetSymbolAddress, once,
-// with the device current) and whether its bitmap region is known to be zero.
+// with the device current).
 struct NoAllocDevice {
   uint8_t* ptr = nullptr;
-  bool bits_clean = false;
 };
 static std::mutex g_noalloc_mu;
 static NoAllocDevice g_noalloc[64];
@@ -1252,9 +1209,7 @@ static void zero_words(uint8_t* p, int64_t bytes, hipStream_t s) {
 
 // qv_search with every query admitted at launch, device buffers only, and its
 // scratch taken from the fixed per-device array: no device or pinned-host
-// allocation, no memset.  The per-query-LUT kernel launches no more query
-// slots than the array's bitmap region holds (with the automatic choice the
-// shared-pivot kernel is taken instead when the index allows it).
+// allocation, no memset.
 void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, int topk, int ef,
                     const qv_search_opts& o, int32_t* d_ids, float* d_dists, int32_t* d_found,
                     qv_search_report* rep) {
@@ -1283,38 +1238,16 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
   NoAllocDevice& nd = noalloc_device(ix->device);
   uint8_t* const base = nd.ptr;
   const int64_t requested = o.num_blocks > 0 ? (int64_t)o.num_blocks * o.queries_per_block : INT64_MAX;
-  LaunchPlan lp = launch_plan(ix, ef, o.kernel, std::min<int64_t>(nq, requested));
-  const int64_t bits_words = ((L.num_data + 31) / 32 + 15) / 16 * 16;
-  const int64_t bits_slots = (kNoAllocBytes - kNoAllocBitsOff) / (4 * bits_words);
-  const int64_t slots = (int64_t)(o.num_blocks > 0 ? o.num_blocks : lp.slots_per_cu * ix->num_cus) * o.queries_per_block;
-  int64_t launched = std::min<int64_t>(std::min<int64_t>(slots, (int64_t)lp.slots_per_cu * ix->num_cus), nq);
-  if (lp.variant == QV_KERNEL_LUT && launched > bits_slots && o.kernel == QV_KERNEL_AUTO) {
-    try {
-      LaunchPlan sp = launch_plan(ix, ef, QV_KERNEL_SHARED_PIVOTS, std::min<int64_t>(nq, requested));
-      lp = sp;
-      launched = std::min<int64_t>(std::min<int64_t>(slots, (int64_t)lp.slots_per_cu * ix->num_cus), nq);
-    } catch (const Error&) {
-      // the index takes only the per-query-LUT kernel: fewer slots below
-    }
-  }
+  const LaunchPlan lp = launch_plan(ix, ef, o.kernel, std::min<int64_t>(nq, requested));
   if (lp.slots_per_cu <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
-  const bool use_bits = lp.variant == QV_KERNEL_LUT;
-  if (use_bits) {
-    if (bits_slots < 1)
-      fail(QV_EUNSUPPORTED, "index of " + std::to_string((long long)L.num_data) +
-                                " points: one query slot's membership bitmap (" + std::to_string(4 * bits_words) +
-                                " bytes) exceeds qv_search_noalloc's scratch (" +
-                                std::to_string(kNoAllocBytes - kNoAllocBitsOff) + " bytes)");
-    launched = std::min(launched, bits_slots);
-  }
+  const int64_t slots = (int64_t)(o.num_blocks > 0 ? o.num_blocks : lp.slots_per_cu * ix->num_cus) * o.queries_per_block;
+  const int64_t launched = std::min<int64_t>(std::min<int64_t>(slots, (int64_t)lp.slots_per_cu * ix->num_cus), nq);
   const LaunchShape ls = shape_launch(lp, launched, ix->num_cus);
 
   int32_t* const counters = reinterpret_cast<int32_t*>(base);
   int32_t* const hops = reinterpret_cast<int32_t*>(base + kNoAllocHopsOff);
   int32_t* const evals = reinterpret_cast<int32_t*>(base + kNoAllocEvalsOff);
-  uint32_t* const bits = reinterpret_cast<uint32_t*>(base + kNoAllocBitsOff);
   zero_words(base, kNoAllocHopsOff, ix->stream);  // counters and the 64-bit totals
-  if (use_bits && !nd.bits_clean) zero_words(base + kNoAllocBitsOff, kNoAllocBytes - kNoAllocBitsOff, ix->stream);
 
   SearchArgs a = base_args(ix);
   a.queries = d_queries;
@@ -1342,11 +1275,8 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
   a.rec_ids = nullptr;
   a.rec_dists = nullptr;
   a.rec_cap = 0;
-  a.bits = use_bits ? bits : nullptr;
-  a.bits_words = use_bits ? bits_words : 0;
 
   const auto t0 = std::chrono::steady_clock::now();
-  if (use_bits) nd.bits_clean = false;  // until every query is seen to finish
   HIP_OK(hipEventRecord(ix->ev0, ix->stream));
   hipLaunchKernelGGL(lp.kern, dim3(ls.grid), dim3(kWave * ls.waves), (size_t)ls.lds, ix->stream, a);
   HIP_OK(hipGetLastError());
@@ -1361,7 +1291,6 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
   unsigned long long tot[2] = {0, 0};
   HIP_OK(hipMemcpy(c, counters, sizeof(c), hipMemcpyDeviceToHost));
   HIP_OK(hipMemcpy(tot, totals, sizeof(tot), hipMemcpyDeviceToHost));
-  if (use_bits) nd.bits_clean = c[1] >= std::min<int64_t>(c[0], nq);  // every started query cleared its bits
   if (c[1] != nq)
     fail(QV_EHIP, "search kernel finished " + std::to_string(c[1]) + " of " + std::to_string(nq) + " queries");
   if (rep) {

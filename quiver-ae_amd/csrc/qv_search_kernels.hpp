@@ -67,10 +67,6 @@ struct SearchArgs {
   int32_t* rec_ids;
   float* rec_dists;
   int32_t rec_cap;
-  // per-slot beam membership bitmaps of the per-query-LUT kernel (bit v set
-  // <=> v in the beam), bits_words 32-bit words per slot, zero between queries
-  uint32_t* bits;
-  int64_t bits_words;
   // per-step recall (pipe width 1): query q stops once sr_required of its
   // top-k ids appear in ground-truth row q % sr_count (sr_width <= 256 ids);
   // sr_gt null: off
@@ -172,7 +168,6 @@ struct Query {
   static constexpr int kQd = SC > 0 ? (MC * SC + 15) / 16 : 1;
   float qd[kQd];
   uint64_t* beam;
-  uint32_t* bits;  // this slot's membership bitmap (SC == 0)
   int sz;        // beam size (ctx.size)
   int cap;       // LDS beam entries (beam_cap >= ef)
   // The beam in registers, chunk-major (lane l holds positions [l Q, l Q + Q),
@@ -188,12 +183,6 @@ struct Query {
   int evals;     // ADC evaluations so far
   float last_e;  // exact distance of the node expanded by the last hop
 
-  // Membership test: a bitmap in HBM (SC == 0), else the rank in the LDS
-  // beam.  The bitmap costs a random read per neighbour but nothing on the
-  // hop's critical path (the read overlaps the code rows); the rank costs a
-  // dependent LDS binary search after the ADC but no memory traffic, which
-  // pays when 8 to 16 queries per CU compete for the device's random accesses.
-  static constexpr bool kBits = SC == 0;
   // The shared-pivot kernels serve dim = MC SC only (uniform chunks).
   static constexpr int kD = SC > 0 ? MC * SC : 0;
   // Loop-invariant byte offsets of this lane's loads inside a record: its
@@ -201,8 +190,8 @@ struct Query {
   uint32_t off_nbr[NPL], off_x;
   uint32_t off_blk;  // this lane's row in a node's neighbour-code block
 
-  // smem: this query's LDS area; slot: this wave's bitmap index.
-  __device__ Query(const SearchArgs& args, char* smem, const float* pivots_lds, int64_t slot)
+  // smem: this query's LDS area.
+  __device__ Query(const SearchArgs& args, char* smem, const float* pivots_lds)
       : a(args), piv(pivots_lds), sz(0), u(INT32_MAX), bu(~0ull), td(__int_as_float(0x7f800000)), ti(-1), fc(0),
         evals(0) {
 #pragma unroll
@@ -213,7 +202,6 @@ struct Query {
     qc = reinterpret_cast<float*>(smem + pl.qc_off);
     qu = reinterpret_cast<float*>(smem + pl.qu_off);
     beam = reinterpret_cast<uint64_t*>(smem + pl.beam_off);
-    bits = kBits ? a.bits + slot * a.bits_words : nullptr;
     const int lane = lane_id();
 #pragma unroll
     for (int j = 0; j < NPL; j++)  // slots >= max_m are masked by the degree
@@ -297,16 +285,6 @@ struct Query {
     // when a candidate wins.
     const bool spec = PF == 1 && u < sz;
 
-    // Beam membership of each neighbour from the bitmap.  The bitmap updates
-    // of the previous hop were issued before this hop's record arrived;
-    // waiting for every outstanding vector memory operation here (the record
-    // is complete by now) orders them before these reads, which bypass the
-    // vector L1.
-    uint32_t bword = 0;
-    if constexpr (kBits) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      bword = __hip_atomic_load(bits + (nbr >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
     // ADC gather-sum over the neighbour's code row (LUT in LDS); the code rows
     // are in flight while the exact distance of v is computed.  Lanes without
     // a neighbour read code row 0 and discard the sum.
@@ -356,9 +334,8 @@ struct Query {
       exact_and_topk(v, xv, rec, lane);
     }
     const uint64_t nkey = has ? make_key(d, nbr, false) : sentinel_key(lane);
-    const bool fresh = kBits ? has && !((bword >> (nbr & 31)) & 1u) : has;
     bool hit = false;
-    const int32_t nx = merge_select<true, PF == 1>(nkey, fresh, lane, nr, spec, bu, hit);
+    const int32_t nx = merge_select<true, PF == 1>(nkey, has, lane, nr, spec, bu, hit);
     if constexpr (PF == 1 && MC > 0 && MC % 16 == 0) {
       if (blk && !hit && nx >= 0) adc_load<MC>(cr, block_row(nx));
       have = hit || (blk && nx >= 0);
@@ -388,12 +365,6 @@ struct Query {
     const uint8_t* rec = kD == 0 && a.dim > 32 * kVecPre ? record(v) : nullptr;
     const bool spec = PF && u < sz;
     const uint64_t spec_key = bu;
-    uint32_t bw0 = 0, bw1 = 0;
-    if constexpr (kBits) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      bw0 = __hip_atomic_load(bits + (nbr0 >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      bw1 = __hip_atomic_load(bits + (nbr1 >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
     float d0, d1;
     if constexpr (MC > 0 && MC % 16 == 0) {
       CodeRow<MC> c0, c1;
@@ -416,22 +387,18 @@ struct Query {
     }
     const uint64_t k0 = has0 ? make_key(d0, nbr0, false) : sentinel_key(lane);
     const uint64_t k1 = has1 ? make_key(d1, nbr1, false) : sentinel_key(lane + kWave);
-    const bool f0 = kBits ? has0 && !((bw0 >> (nbr0 & 31)) & 1u) : has0;
-    const bool f1 = kBits ? has1 && !((bw1 >> (nbr1 & 31)) & 1u) : has1;
     bool hit = false;
-    merge_select<false, false>(k0, f0, lane, nr, false, spec_key, hit);
-    return merge_select<true, PF>(k1, f1, lane, nr, spec, spec_key, hit);
+    merge_select<false, false>(k0, has0, lane, nr, false, spec_key, hit);
+    return merge_select<true, PF>(k1, has1, lane, nr, spec, spec_key, hit);
   }
 
-  // Without the bitmap, every LDS beam position from sz to cap holds kPadKey
-  // (above every key): set once per query; merges only write below the new
-  // sz, which never shrinks.  The rank search then needs no bounds test.
+  // Every LDS beam position from sz to cap holds kPadKey (above every key):
+  // set once per query; merges only write below the new sz, which never
+  // shrinks.  The rank search then needs no bounds test.
   __device__ __forceinline__ void pad_beam(int lane) {
-    if constexpr (!kBits) {
 #pragma unroll
-      for (int k = 0; k < Q; k++)
-        if (k * kWave + lane < cap) beam[k * kWave + lane] = kPadKey;
-    }
+    for (int k = 0; k < Q; k++)
+      if (k * kWave + lane < cap) beam[k * kWave + lane] = kPadKey;
   }
 
   // Beam position P from the register copy (kPadKey past it), wave-uniform.
@@ -481,11 +448,11 @@ struct Query {
   // most sz <= ef entries are compacted away.  So the new beam is the first ef
   // entries of  beam  U  {candidates whose id is not in the beam}, in key
   // order, and its first unvisited entry is taken and marked visited.
-  // fresh: lane holds a neighbour, not in the beam by the bitmap (kBits).
+  // has: the lane holds a neighbour.
   //
-  // Without the bitmap: a neighbour whose id is in the beam has that entry's
-  // key (the ADC of one code row against one query is one value), visited
-  // bit aside.  So the lower bound r of (c & ~1) in the sorted beam is both
+  // Membership: a neighbour whose id is in the beam has that entry's key
+  // (the ADC of one code row against one query is one value), visited bit
+  // aside.  So the lower bound r of (c & ~1) in the sorted beam is both
   // the candidate's rank and its membership test: c is in the beam iff
   // beam[r] and c differ only in the visited bit.  Only neighbours below the
   // end of a full beam need it.
@@ -499,15 +466,15 @@ struct Query {
   // record the hop requested at its start.  SEL = false merges without a
   // selection (the first batch of a two-slot hop) and returns -1.
   template <bool SEL, bool PF>
-  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool fresh, int lane, Rec& nr, bool spec,
+  __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool has, int lane, Rec& nr, bool spec,
                                                   uint64_t spec_key, bool& hit) {
     const int ef = a.ef;
     // Candidates at or above the last entry of a full beam end beyond ef.
     const uint64_t last = sz >= ef ? beam[ef - 1] : ~0ull;
-    const bool below = fresh && nkey < last;
+    const bool below = has && nkey < last;
     int r = 0;  // rank in the beam (valid lanes)
     bool valid = below;
-    if constexpr (!kBits) {
+    {
       if (__ballot(below)) {
         // r = #{beam entries e : e < (nkey & ~1)} by a 4-ary search over the
         // LDS beam: sorted, kPadKey from sz to its capacity cap (>= ef), so
@@ -558,22 +525,13 @@ struct Query {
       if (vm == 0) return -1;
     } else {
     if (vm == 0 && u >= sz) return -1;
-    // Smallest surviving candidate and its rank in the beam (with the bitmap:
-    // entries below it by ballots against the register beam, visited bit
-    // ignored: e < c iff e < (c & ~1)).
+    // Smallest surviving candidate and its rank in the beam.
     selpos = u;
     selkey = bu;
     if (vm != 0) {
       const uint64_t kv0 = wave_min_u64(valid ? nkey : ~0ull);
       if (kv0 < bu) {
-        if constexpr (kBits) {
-          int r0 = 0;
-#pragma unroll
-          for (int k = 0; k < Q; k++) r0 += __popcll(__ballot(ck[k] < (kv0 & ~1ull)));
-          selpos = r0;
-        } else {
-          selpos = read_lane_i32(r, __ffsll((long long)__ballot(valid && nkey == kv0)) - 1);
-        }
+        selpos = read_lane_i32(r, __ffsll((long long)__ballot(valid && nkey == kv0)) - 1);
         selkey = kv0;
       }
     }
@@ -599,43 +557,21 @@ struct Query {
     for (uint64_t rest = vm; rest; rest &= rest - 1) {
       const int l = __ffsll((long long)rest) - 1;
       const uint64_t c = read_lane_u64(nkey, l);
-      int rc;
-      if constexpr (kBits) {
-        rc = 0;
-#pragma unroll
-        for (int k = 0; k < Q; k++) rc += __popcll(__ballot(ck[k] < (c & ~1ull)));
-        if (lane == l) r = rc;
-      } else {
-        rc = read_lane_i32(r, l);
-      }
+      const int rc = read_lane_i32(r, l);
       t += c < nkey ? 1 : 0;
 #pragma unroll
       for (int k = 0; k < Q; k++) sh[k] += lane * Q + k >= rc ? 1u : 0u;
     }
 
-    // Scatter in place; entries pushed to ef or beyond drop out (and leave
-    // the bitmap), inserted candidates join it.
+    // Scatter in place; entries pushed to ef or beyond drop out.
 #pragma unroll
     for (int k = 0; k < Q; k++) {
       const int pos = lane * Q + k;
       const int g = pos + (int)sh[k];
-      if (pos < sz) {
-        if (g < ef) {
-          beam[g] = g == selpos ? (ck[k] & ~1ull) : ck[k];
-        } else if constexpr (kBits) {
-          const uint32_t id = key_id(ck[k]);
-          atomicAnd(bits + (id >> 5), ~(1u << (id & 31)));
-        }
-      }
+      if (pos < sz && g < ef) beam[g] = g == selpos ? (ck[k] & ~1ull) : ck[k];
     }
     const int f = r + t;
-    if (valid && f < ef) {
-      beam[f] = f == selpos ? (nkey & ~1ull) : nkey;
-      if constexpr (kBits) {
-        const uint32_t id = key_id(nkey);
-        atomicOr(bits + (id >> 5), 1u << (id & 31));
-      }
-    }
+    if (valid && f < ef) beam[f] = f == selpos ? (nkey & ~1ull) : nkey;
     sz = min(sz + (int)__popcll(vm), ef);
     // Register copy of the new beam (the wave's LDS accesses complete in order).
 #pragma unroll
@@ -645,20 +581,6 @@ struct Query {
     }
     find_unvisited(lane);
     return SEL ? (int32_t)key_id(selkey) : -1;
-  }
-
-  // Clears the bitmap bits of the final beam (bitmaps are zero between queries).
-  __device__ __forceinline__ void clear_bits(int lane) {
-    if constexpr (kBits) {
-#pragma unroll
-      for (int k = 0; k < Q; k++) {
-        const int pos = lane * Q + k;
-        if (pos < sz) {
-          const uint32_t id = key_id(ck[k]);
-          atomicAnd(bits + (id >> 5), ~(1u << (id & 31)));
-        }
-      }
-    }
   }
 
   // persistent_select_next_no_compact (kernel_helpers.cuh:491-518): the first
@@ -691,9 +613,9 @@ __device__ __forceinline__ void query_sync() {
 }
 
 // The persistent query loop of one wave: smem is its LDS area, piv the
-// shared pivots (SC > 0), slot its bitmap index (SC == 0).
+// shared pivots (SC > 0).
 template <class T, int Q, int MC, int SC, int NPL>
-__device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, const float* piv, int64_t slot) {
+__device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, const float* piv) {
   const int lane = lane_id();
 
   while (true) {
@@ -727,7 +649,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     if (qid < 0) break;
     if (a.t_start && lane == 0) a.t_start[qid] = wall_ticks();
 
-    Query<T, Q, MC, SC, NPL> Qy(a, smem, piv, slot);
+    Query<T, Q, MC, SC, NPL> Qy(a, smem, piv);
     const float* q = a.queries + (int64_t)qid * a.dim;
     // ---- entry node: the nav-graph search on the raw query when a nav graph is
     // loaded (kernel_q1.cuh:148-174, 199-206), else the medoid.
@@ -903,7 +825,6 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
         a.sr_hits[qid] = sr_h;
       }
     }
-    Qy.clear_bits(lane);
     if (lane < a.topk) {
       a.out_ids[(int64_t)qid * a.topk + lane] = Qy.ti;
       a.out_dists[(int64_t)qid * a.topk + lane] = Qy.td;
@@ -928,7 +849,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
 template <class T, int Q, int MC, int NPL>
 __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
   extern __shared__ __align__(16) char smem[];
-  run_queries<T, Q, MC, 0, NPL>(a, smem, nullptr, blockIdx.x);
+  run_queries<T, Q, MC, 0, NPL>(a, smem, nullptr);
 }
 
 // One workgroup per CU, one query per wave: the workgroup holds the pivots
@@ -950,7 +871,7 @@ __global__ __launch_bounds__(kWave * sp_max_waves(Q, NPL)) void search_kernel_sp
   __syncthreads();
   const int w = threadIdx.x / kWave;
   const LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, false, a.ef);
-  run_queries<T, Q, MC, SC, NPL>(a, smem + piv_bytes(a.dim) + w * pl.total, piv, 0);
+  run_queries<T, Q, MC, SC, NPL>(a, smem + piv_bytes(a.dim) + w * pl.total, piv);
 }
 
 }  // namespace

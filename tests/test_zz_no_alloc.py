@@ -5,8 +5,8 @@ Each case runs qv_search on device buffers with every query admitted at
 launch, then qv_search_noalloc twice in a row -- the full input, then a
 smaller one -- and requires ids, distances, found counts and the hop and
 evaluation totals to equal qv_search's for the same queries (integer and
-index work: bit-exact).  Also: the per-query-LUT kernel capped to the query
-slots whose bitmaps fit the fixed scratch, and the entry's argument limits.
+index work: bit-exact).  Also: a 600k-point index with 1024 query slots of
+either kernel, and the entry's argument limits.
 """
 from __future__ import annotations
 
@@ -117,11 +117,10 @@ def test_noalloc_equals_search_float(lib, small_f32_index):
         lib.load().qv_index_close(h)
 
 
-def test_noalloc_lut_slots_capped_by_scratch(lib):
-    """600k points: a slot's bitmap is 75 KB, so the 24 MB bitmap region holds
-    fewer slots than the 1024 requested; the forced per-query-LUT kernel runs
-    with that many, the automatic choice switches to shared pivots, and both
-    still equal qv_search."""
+def test_noalloc_many_slots_on_a_larger_index(lib):
+    """600k points and 1024 requested query slots: each kernel launches all of
+    them (the scratch holds only counts, nothing per slot or per point) and
+    equals qv_search."""
     import quiver  # noqa: F401
 
     L = lib.load()
@@ -139,18 +138,12 @@ def test_noalloc_lut_slots_capped_by_scratch(lib):
     lib.check(L.qv_mixture_fill_host(C.byref(mix), 1 << 40, q.shape[0], q.ctypes.data))
     dev = _Dev(lib, q.astype(np.float32))
     try:
-        words = ((n + 31) // 32 + 15) // 16 * 16
-        fit = (lib.QV_NOALLOC_SCRATCH_BYTES - (256 + 8 * lib.QV_NOALLOC_MAX_QUERIES)) // (4 * words)
-        assert 1 <= fit < 1024
         for n_q in (3000, 1500):
-            _say(f"[gpu] noalloc LUT kernel capped to {fit} slots, n={n_q}")
-            want, got, r0, r1 = _pair(lib, h, dev, n_q, 64, "lut", num_blocks=1024)
-            _check(want, got, r0, r1, f"lut capped n={n_q}")
-            assert r0.num_blocks == 1024 and r1.num_blocks == fit
-            want, got, r0, r1 = _pair(lib, h, dev, n_q, 64, "auto", num_blocks=1024)
-            for a, b in zip(want, got):
-                np.testing.assert_array_equal(b, a)
-            assert r1.kernel == lib.QV_KERNEL_SHARED_PIVOTS
+            for kernel in ("lut", "shared-pivots"):
+                _say(f"[gpu] noalloc 600k points kernel={kernel} 1024 slots n={n_q}")
+                want, got, r0, r1 = _pair(lib, h, dev, n_q, 64, kernel, num_blocks=1024)
+                _check(want, got, r0, r1, f"{kernel} 1024 slots n={n_q}")
+                assert r0.num_blocks == r1.num_blocks == 1024
     finally:
         L.qv_index_close(h)
 
