@@ -350,12 +350,10 @@ def main() -> int:
         result["adc"] = adc_leg(_lib, L, args.adc_codes, log)
 
     # The search kernel is bound by random accesses, not by HBM bytes: one code
-    # row per neighbour evaluation (plus one beam-membership bitmap word with
-    # the per-query-LUT kernel) and the 64-byte lines of each expanded record,
-    # against the rate the gather-alone kernel reaches for random rows in the
-    # same run.
-    per_eval = 2 if last.kernel == _lib.QV_KERNEL_LUT else 1
-    acc = per_eval * last.total_evals + last.total_hops * ((info.node_size + 63) // 64)
+    # row per neighbour evaluation and the 64-byte lines of each expanded
+    # record, against the rate the gather-alone kernel reaches for random rows
+    # in the same run.
+    acc = last.total_evals + last.total_hops * ((info.node_size + 63) // 64)
     rate = acc / (kernel_ms * 1e-3)
     ceil_rate = result.get("adc", {}).get("gather_alone_rows_per_s")
     if "adc" in result:
