@@ -6,8 +6,8 @@ Workload (default): 100M uint8 vectors of dimension 128 from the seeded
 Gaussian mixture (65536 centres uniform in [32, 224], sigma 20, clipped), a
 Vamana graph R=64 / L=100 / alpha=1.2 and PQ 32x256 built on the GPU, 10k
 queries from the same mixture, top-10.  Setup (data, build, ground truth, the
-ef/early-exit sweep) is untimed; a step is one search of all queries with the
-queries resident in HBM.  Beside it: the same steps with the queries and
+sweep over ef, early exit and pipe width) is untimed; a step is one search of
+all queries with the queries resident in HBM.  Beside it: the same steps with the queries and
 results in host memory (transfers inside each step), the latency mode
 (open-loop batches of 1, 16 and 256 queries at Recall@10 0.90 and 0.95), the
 PQ-ADC microbenchmark and the CPU oracle on the same index.  Prints one JSON
@@ -63,6 +63,9 @@ def main() -> int:
     ap.add_argument("--ef", type=int, default=0, help="time this ef_search and skip the sweep")
     ap.add_argument("--policy", default="none", choices=("none", "gpruning"),
                     help="early-exit policy used with --ef")
+    ap.add_argument("--pipe", type=int, default=1, help="pipe width used with --ef")
+    ap.add_argument("--pipe-widths", default="1,2",
+                    help="pipe widths the sweep tries with early exit off (the reference's default is 2)")
     ap.add_argument("--latency-batches", default="1,16,256",
                     help="comma-separated batch sizes for the latency leg; empty: off")
     ap.add_argument("--adc-only", action="store_true",
@@ -197,25 +200,29 @@ def main() -> int:
         hits = sum(len(set(ids[i]) & set(gt[i])) for i in range(nq))
         return hits / (nq * 10.0)
 
-    # ---- sweep (untimed): the fastest (ef, policy) with recall >= target (and >= 0.95)
+    # ---- sweep (untimed): the fastest (ef, policy, pipe width) with recall >=
+    # target (and >= 0.95).  Pipe widths above 1 are the reference's own
+    # schedule (its default is 2): the same beam search expanding the pipe
+    # lanes' nodes in turn, with results of its own that the oracle reproduces.
     sweep = []
     best = None
     targets = sorted({args.target_recall, 0.95})
-    points = []  # (ef, policy, qps, pname, recall, p99)
-    plan = ((_lib.QV_EXIT_GPRUNING, "gpruning"), (_lib.QV_EXIT_NONE, "none"))
+    points = []  # (ef, policy, qps, pname, recall, p99, pipe)
+    pipes = [int(x) for x in args.pipe_widths.split(",") if x]
+    plan = [(_lib.QV_EXIT_GPRUNING, "gpruning", 1)] + [(_lib.QV_EXIT_NONE, "none", pw) for pw in pipes]
     if args.ef:
         pol = _lib.QV_EXIT_GPRUNING if args.policy == "gpruning" else _lib.QV_EXIT_NONE
-        best = (args.ef, pol, 0.0, args.policy)
-        plan = ()
-    for policy, pname in plan:
+        best = (args.ef, pol, 0.0, args.policy, args.pipe)
+        plan = []
+    for policy, pname, pw in plan:
         for ef in w["efs"]:
-            rep = run(ef, policy)
+            rep = run(ef, policy, pw)
             r = recall_of()
-            sweep.append({"ef": ef, "early_exit": pname, "recall": round(r, 4), "qps": round(rep.qps),
-                          "p99_ms": round(rep.lat_p99_ms, 3), "hops": round(rep.avg_hops, 1)})
-            log(f"sweep ef={ef:3d} {pname:8s} recall={r:.4f} qps={rep.qps:10.0f} "
+            sweep.append({"ef": ef, "early_exit": pname, "pipe_width": pw, "recall": round(r, 4),
+                          "qps": round(rep.qps), "p99_ms": round(rep.lat_p99_ms, 3), "hops": round(rep.avg_hops, 1)})
+            log(f"sweep ef={ef:3d} {pname:8s} W={pw} recall={r:.4f} qps={rep.qps:10.0f} "
                 f"p50={rep.lat_p50_ms:.3f} p99={rep.lat_p99_ms:.3f} hops={rep.avg_hops:.1f}")
-            points.append((ef, policy, rep.qps, pname, r, rep.lat_p99_ms))
+            points.append((ef, policy, rep.qps, pname, r, rep.lat_p99_ms, pw))
             if r >= targets[-1]:
                 break
 
@@ -225,12 +232,12 @@ def main() -> int:
 
     if not args.ef:
         b = fastest(args.target_recall)
-        best = b[:4] if b else None
+        best = (b[0], b[1], b[2], b[3], b[6]) if b else None
     if best is None:
-        ef, policy, pname = w["efs"][-1], _lib.QV_EXIT_NONE, "none"
+        ef, policy, pname, pipe = w["efs"][-1], _lib.QV_EXIT_NONE, "none", 1
         log(f"no sweep point reached recall {args.target_recall}; timing ef={ef} none")
     else:
-        ef, policy, _, pname = best
+        ef, policy, _, pname, pipe = best
     at_095 = fastest(0.95)
 
     # ---- optional calibration copy: a kernel of known traffic for the counters
@@ -245,11 +252,11 @@ def main() -> int:
 
     # ---- warmup + timed steps ------------------------------------------------
     for _ in range(args.warmup):
-        run(ef, policy)
+        run(ef, policy, pipe)
     reps = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        reps.append(run(ef, policy))
+        reps.append(run(ef, policy, pipe))
     t1 = time.perf_counter()
     elapsed = t1 - t0
     recall = recall_of()
@@ -259,7 +266,7 @@ def main() -> int:
     p99 = float(np.median([r.lat_p99_ms for r in reps]))
     p50 = float(np.median([r.lat_p50_ms for r in reps]))
     last = reps[-1]
-    log(f"timed: ef={ef} {pname} steps={args.steps} qps={qps:.0f} recall={recall:.4f} p50={p50:.3f} p99={p99:.3f}")
+    log(f"timed: ef={ef} {pname} W={pipe} steps={args.steps} qps={qps:.0f} recall={recall:.4f} p50={p50:.3f} p99={p99:.3f}")
 
     # the same steps with the queries and results in host memory: the query
     # upload and the result download fall inside each step, as in the
@@ -269,7 +276,7 @@ def main() -> int:
     h_dists = np.empty((nq, 10), np.float32)
     ho = _lib.default_search_opts()
     ho.early_exit = policy
-    ho.pipe_width = 1
+    ho.pipe_width = pipe
     ho.kernel = _lib.KERNEL_NAMES[args.search_kernel]
     ho.admission = _lib.QV_ADMIT_STREAMING
     _lib.check(L.qv_search(h, qf.ctypes.data, nq, dim, 10, ef, C.byref(ho), h_ids.ctypes.data,
@@ -288,7 +295,7 @@ def main() -> int:
     # with a nav graph: the same steps from the medoid, to price the nav search
     medoid_entry = None
     if info.nav_nodes > 0:
-        mreps = [run(ef, policy, skip_nav=1) for _ in range(args.steps)]
+        mreps = [run(ef, policy, pipe, skip_nav=1) for _ in range(args.steps)]
         medoid_entry = {"kernel_ms": round(float(np.median([r.kernel_ms for r in mreps])), 3),
                         "recall_at_10": round(recall_of(), 4), "avg_hops": round(mreps[-1].avg_hops, 2)}
         log(f"medoid entry, same steps: {medoid_entry}")
@@ -304,7 +311,8 @@ def main() -> int:
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic(args.workload, ef, pname,
-                                              kname + (" neighbour-codes" if nbr_codes else ""), log),
+                                              kname + (" neighbour-codes" if nbr_codes else "")
+                                              + (f" pipe={pipe}" if pipe != 1 else ""), log),
                 "kernel": kname, "kernel_ms": round(kernel_ms, 3),
                 "bytes_per_launch": int(alg_bytes),
                 "bytes_per_launch_without_lut": int(alg_bytes - nq * info.num_chunks * 256 * 4),
@@ -318,7 +326,7 @@ def main() -> int:
         "data": "synthetic: seeded Gaussian mixture generated on the GPU; index built on the GPU",
         "config": {"workload": f"{args.workload}: {n} x {dim} {w['dtype']} mixture ({w['centers']} centres), "
                                f"Vamana R={w['R']} L={w['L']} alpha=1.2, PQ {w['M']}x256, {nq} queries, top-10",
-                   "ef_search": ef, "early_exit": pname, "pipe_width": 1, "num_blocks": last.num_blocks,
+                   "ef_search": ef, "early_exit": pname, "pipe_width": pipe, "num_blocks": last.num_blocks,
                    "graph_placement": args.graph_placement, "nav_nodes": int(info.nav_nodes),
                    "neighbour_codes": nbr_codes,
                    "admission": "streaming (window = num_blocks)", "recall_at_10": round(recall, 4),
@@ -332,14 +340,15 @@ def main() -> int:
 
     # ---- latency mode: batches of B queries, one search call per batch -----
     if args.latency_batches:
-        lat_points = [("0.90", ef, policy, pname)]
+        lat_points = [("0.90", ef, policy, pname, pipe)]
         if at_095 is not None:
-            lat_points.append(("0.95", at_095[0], at_095[1], at_095[3]))
+            lat_points.append(("0.95", at_095[0], at_095[1], at_095[3], at_095[6]))
         result["latency_mode"] = latency_leg(_lib, L, h, d_q, dim, nq, gt, d_ids, d_dists, lat_points,
                                              [int(b) for b in args.latency_batches.split(",") if b],
                                              _lib.KERNEL_NAMES[args.search_kernel], log)
     if at_095 is not None:
         result["config"]["at_recall_0.95"] = {"ef_search": at_095[0], "early_exit": at_095[3],
+                                              "pipe_width": at_095[6],
                                               "recall_at_10": round(at_095[4], 4), "qps": round(at_095[2], 1),
                                               "p99_ms": round(at_095[5], 3)}
 
@@ -365,8 +374,8 @@ def main() -> int:
 
     # ---- CPU baseline: the oracle (CPU restatement) on a bounded sample -------
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_leg(_lib, L, h, info, qf, ef, policy, pname, timed_ids, timed_dists, nq,
-                                         args.cpu_seconds)
+        result["cpu_baseline"] = cpu_leg(_lib, L, h, info, qf, ef, policy, pname, pipe, timed_ids, timed_dists,
+                                         nq, args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
     L.qv_index_close(h)
@@ -381,14 +390,14 @@ def latency_leg(_lib, L, h, d_q, dim, nq, gt, d_ids, d_dists, points, batches, k
     all calls of that batch size, launches included.  B=1 covers the first 1000
     queries, larger batches all of them."""
     out = []
-    for tag, ef, policy, pname in points:
+    for tag, ef, policy, pname, pipe in points:
         for b in batches:
             n = min(nq, 1000) if b == 1 else nq
             lat = []
             ids = np.empty((n, 10), np.int32)
             o = _lib.default_search_opts()
             o.early_exit = policy
-            o.pipe_width = 1
+            o.pipe_width = pipe
             o.kernel = kernel
             o.device_buffers = 1
             o.admission = _lib.QV_ADMIT_STREAMING
@@ -405,11 +414,11 @@ def latency_leg(_lib, L, h, d_q, dim, nq, gt, d_ids, d_dists, points, batches, k
             ids[:] = d_ids.download(np.int32, (nq, 10))[:n]
             hits = sum(len(set(ids[i]) & set(gt[i])) for i in range(n))
             lat = np.sort(np.asarray(lat))
-            row = {"target": tag, "batch": b, "ef_search": ef, "early_exit": pname, "queries": n,
+            row = {"target": tag, "batch": b, "ef_search": ef, "early_exit": pname, "pipe_width": pipe, "queries": n,
                    "recall_at_10": round(hits / (n * 10.0), 4), "qps": round(n / wall, 1),
                    "p50_ms": round(float(np.percentile(lat, 50)), 3),
                    "p99_ms": round(float(np.percentile(lat, 99)), 3)}
-            log(f"latency R@10>={tag} batch={b:4d} ef={ef} {pname}: qps={row['qps']:.0f} "
+            log(f"latency R@10>={tag} batch={b:4d} ef={ef} {pname} W={pipe}: qps={row['qps']:.0f} "
                 f"p50={row['p50_ms']:.3f} p99={row['p99_ms']:.3f} recall={row['recall_at_10']:.4f}")
             out.append(row)
     return out
@@ -526,7 +535,8 @@ def adc_leg(_lib, L, ncodes: int, log) -> dict:
             "physical_frac_of_random_read_peak": round(phys_gbs / random_peak, 4)}
 
 
-def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, gpu_ids_all, gpu_dists_all, nq, seconds: float) -> dict:
+def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, pipe, gpu_ids_all, gpu_dists_all, nq,
+            seconds: float) -> dict:
     sys.path.insert(0, str(ROOT / "oracle"))
     import qv_oracle as O
 
@@ -543,17 +553,18 @@ def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, gpu_ids_all, gpu_dists_all,
     early = O.EXIT_GPRUNING if pname == "gpruning" else O.EXIT_NONE
     # calibrate on a small slice, then size the sample to about `seconds`
     t = time.time()
-    O.search(host, qf[:threads * 4], 10, ef, early_exit=early, threads=threads)
+    O.search(host, qf[:threads * 4], 10, ef, pipe_width=pipe, early_exit=early, threads=threads)
     per_q = (time.time() - t) / (threads * 4)
     sample = int(max(threads * 8, min(nq, seconds / max(per_q, 1e-9))))
     secs = np.zeros(sample, np.float64)
     t = time.time()
-    ids, dists, _, _ = O.search(host, qf[:sample], 10, ef, early_exit=early, threads=threads, seconds=secs)
+    ids, dists, _, _ = O.search(host, qf[:sample], 10, ef, pipe_width=pipe, early_exit=early, threads=threads,
+                                seconds=secs)
     el = time.time() - t
     same = bool(np.array_equal(ids, gpu_ids_all[:sample]))
     same_d = bool(np.array_equal(dists, gpu_dists_all[:sample]))
     return {"value": round(sample / el, 1), "unit": "queries/s", "cores": threads, "kind": "port",
-            "sample": f"first {sample} of the {nq} queries, same index, ef={ef}, {pname}, "
+            "sample": f"first {sample} of the {nq} queries, same index, ef={ef}, {pname}, pipe width {pipe}, "
                       f"{el:.1f}s wall on {threads} threads (OpenMP over queries)",
             "p50_ms": round(float(np.percentile(secs, 50)) * 1e3, 3),
             "p99_ms": round(float(np.percentile(secs, 99)) * 1e3, 3),
