@@ -165,6 +165,37 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t x) {
   return read_lane_u64(umin64(((uint64_t)qh[0] << 32) | ql[0], ((uint64_t)qh[1] << 32) | ql[1]), 0);
 }
 
+// Minimum of one 32-bit value per lane, returned to every lane (uniform):
+// DPP steps inside each 16-lane row (quad_perm swaps, then rotations by 4 and
+// 8), then the permlane swaps across rows; VALU only, no LDS.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+  x = min(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, true));   // quad_perm [1,0,3,2]
+  x = min(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, true));   // quad_perm [2,3,0,1]
+  x = min(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x124, 0xF, 0xF, true));  // row_ror:4
+  x = min(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, true));  // row_ror:8
+  const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = min(p[0], p[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return read_lane_u32(min(q[0], q[1]), 0);
+}
+
+// The smallest key among the lanes where `valid` holds (at least one), and a
+// lane holding it (*at).  Keys order by their distance word first, so the
+// minimum distance word and one ballot usually settle it; only equal distance
+// words in two or more valid lanes take the full 64-bit minimum.
+__device__ __forceinline__ uint64_t wave_min_key(uint64_t key, bool valid, int* at) {
+  const uint32_t hi = (uint32_t)(key >> 32);
+  const uint32_t m = wave_min_u32(valid ? hi : 0xffffffffu);
+  const uint64_t b = __ballot(valid && hi == m);
+  if ((b & (b - 1)) == 0) {
+    *at = __ffsll((long long)b) - 1;
+    return read_lane_u64(key, *at);
+  }
+  const uint64_t kv = wave_min_u64(valid ? key : ~0ull);
+  *at = __ffsll((long long)__ballot(valid && key == kv)) - 1;
+  return kv;
+}
+
 // Per-query LUT in LDS: PQSearchData::init_query (src/shared/index/
 // pq_device.cuh:9-36).  Chunks are contiguous dimension ranges, so each
 // (chunk, pivot) cell accumulates its dimensions in ascending order, exactly as

@@ -529,9 +529,10 @@ struct Query {
     selpos = u;
     selkey = bu;
     if (vm != 0) {
-      const uint64_t kv0 = wave_min_u64(valid ? nkey : ~0ull);
+      int at;
+      const uint64_t kv0 = wave_min_key(nkey, valid, &at);
       if (kv0 < bu) {
-        selpos = read_lane_i32(r, __ffsll((long long)__ballot(valid && nkey == kv0)) - 1);
+        selpos = read_lane_i32(r, at);
         selkey = kv0;
       }
     }
