@@ -182,6 +182,11 @@ struct Query {
   int fc;        // found count
   int evals;     // ADC evaluations so far
   float last_e;  // exact distance of the node expanded by the last hop
+  // The beam's entry at ef - 1 when the beam is full (~0 before): candidates
+  // at or above it cannot enter.  Only merges change it; marking an entry
+  // visited does not matter here (a candidate's key equals an entry's only
+  // with the same id, which is not below it either way).
+  uint64_t lastk;
 
   // The shared-pivot kernels serve dim = MC SC only (uniform chunks).
   static constexpr int kD = SC > 0 ? MC * SC : 0;
@@ -193,7 +198,7 @@ struct Query {
   // smem: this query's LDS area.
   __device__ Query(const SearchArgs& args, char* smem, const float* pivots_lds)
       : a(args), piv(pivots_lds), sz(0), u(INT32_MAX), bu(~0ull), td(__int_as_float(0x7f800000)), ti(-1), fc(0),
-        evals(0) {
+        evals(0), lastk(~0ull) {
 #pragma unroll
     for (int k = 0; k < Q; k++) ck[k] = kPadKey;
     LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, SC == 0, a.ef);
@@ -469,8 +474,9 @@ struct Query {
   __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool has, int lane, Rec& nr, bool spec,
                                                   uint64_t spec_key, bool& hit) {
     const int ef = a.ef;
-    // Candidates at or above the last entry of a full beam end beyond ef.
-    const uint64_t last = sz >= ef ? beam[ef - 1] : ~0ull;
+    // Candidates at or above the last entry of a full beam end beyond ef
+    // (lastk: read with the previous merge's register reload).
+    const uint64_t last = lastk;
     const bool below = has && nkey < last;
     int r = 0;  // rank in the beam (valid lanes)
     bool valid = below;
@@ -510,7 +516,10 @@ struct Query {
         const uint64_t e0 = beam[min(r, top)];
         const uint64_t e1 = beam[min(r + 1, top)];
         const uint64_t e2 = beam[min(r + 2, top)];
-        const uint64_t e3 = beam[min(r + 3, top)];
+        uint64_t e3 = beam[min(r + 3, top)];
+        // e3 is only selected when n == 3; without this the compiler moves its
+        // read into that branch, a fourth dependent LDS round trip.
+        asm volatile("" : "+v"(e3));
         const int n = (e0 < c0 ? 1 : 0) + (e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0);
         r += n;
         const uint64_t at = n == 0 ? e0 : (n == 1 ? e1 : (n == 2 ? e2 : e3));
@@ -574,12 +583,15 @@ struct Query {
     const int f = r + t;
     if (valid && f < ef) beam[f] = f == selpos ? (nkey & ~1ull) : nkey;
     sz = min(sz + (int)__popcll(vm), ef);
-    // Register copy of the new beam (the wave's LDS accesses complete in order).
+    // Register copy of the new beam (the wave's LDS accesses complete in
+    // order), and its entry at ef - 1 for the next merge, read in the same
+    // round trip.
 #pragma unroll
     for (int k = 0; k < Q; k++) {
       const int pos = lane * Q + k;
       ck[k] = pos < sz ? beam[pos] : kPadKey;
     }
+    lastk = sz >= ef ? beam[ef - 1] : ~0ull;
     find_unvisited(lane);
     return SEL ? (int32_t)key_id(selkey) : -1;
   }
