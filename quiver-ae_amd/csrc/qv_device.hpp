@@ -244,6 +244,30 @@ __device__ __forceinline__ void adc_load(CodeRow<MC>& cr, const uint8_t* __restr
   }
 }
 
+// A raw buffer descriptor for the `bytes` bytes at p, a wave-uniform
+// address: loads through it take the base in scalar registers and a 32-bit
+// offset per lane, so no 64-bit vector address is formed or held while they
+// are in flight, and a load past `bytes` returns zero.  Word 3 is the gfx9
+// raw-buffer data format (32-bit).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_at(const void* p, int bytes = 0x7fffffff) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// A code row of MC bytes at byte off of the buffer r.
+template <int MC>
+__device__ __forceinline__ void adc_load(CodeRow<MC>& cr, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+#pragma unroll
+  for (int t = 0; t < MC / 16; t++) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off + 16u * t), 0, 0);
+    cr.w[4 * t + 0] = v.x;
+    cr.w[4 * t + 1] = v.y;
+    cr.w[4 * t + 2] = v.z;
+    cr.w[4 * t + 3] = v.w;
+  }
+}
+
 // The same from a row address (a row of the neighbour-code table).
 template <int MC>
 __device__ __forceinline__ void adc_load(CodeRow<MC>& cr, const uint8_t* __restrict__ row) {
@@ -569,23 +593,39 @@ __device__ __forceinline__ float raw_to_float(uint32_t r) {
   else return (float)(T)(uint8_t)r;
 }
 
-template <class T>
+template <class T, class R>
 __device__ __forceinline__ void load_vec_pre(const uint8_t* __restrict__ rec, int dim, int lane,
-                                             uint32_t (&x)[kVecPre]) {
+                                             R (&x)[kVecPre]) {
 #pragma unroll
-  for (int k = 0; k < kVecPre; k++) x[k] = elem_raw<T>(rec, min((lane & 31) + 32 * k, dim - 1));
+  for (int k = 0; k < kVecPre; k++) x[k] = (R)elem_raw<T>(rec, min((lane & 31) + 32 * k, dim - 1));
 }
 
 // load_vec_pre for a dim KD known at compile time (a multiple of 32 up to
 // 32 kVecPre): element (lane & 31) + 32 k for each k with 32 k < KD, at the
 // lane's loop-invariant byte offset off = (lane & 31) sizeof(T) plus an
 // immediate, so a request costs no address arithmetic.
-template <class T, int KD>
+template <class T, int KD, class R>
 __device__ __forceinline__ void load_vec_pre_fixed(const uint8_t* __restrict__ rec, uint32_t off,
-                                                   uint32_t (&x)[kVecPre]) {
+                                                   R (&x)[kVecPre]) {
   static_assert(KD % 32 == 0 && KD <= 32 * kVecPre, "whole 32-element rows");
 #pragma unroll
-  for (int k = 0; k < kVecPre; k++) x[k] = 32 * k < KD ? elem_raw<T>(rec + off, 32 * k) : 0u;
+  for (int k = 0; k < kVecPre; k++) x[k] = 32 * k < KD ? (R)elem_raw<T>(rec + off, 32 * k) : (R)0;
+}
+
+// load_vec_pre_fixed from the buffer r (a record), off = (lane & 31) sizeof(T).
+template <class T, int KD, class R>
+__device__ __forceinline__ void load_vec_pre_buf(__amdgpu_buffer_rsrc_t r, uint32_t off, R (&x)[kVecPre]) {
+  static_assert(KD % 32 == 0 && KD <= 32 * kVecPre, "whole 32-element rows");
+#pragma unroll
+  for (int k = 0; k < kVecPre; k++) {
+    const int o = (int)(off + 32u * k * (uint32_t)sizeof(T));
+    if (32 * k >= KD)
+      x[k] = (R)0;
+    else if constexpr (sizeof(T) == 1)
+      x[k] = (R)__builtin_amdgcn_raw_buffer_load_b8(r, o, 0, 0);
+    else
+      x[k] = (R)__builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0);
+  }
 }
 
 // Query elements lane + 32k (k < kVecPre) of the first 32 lanes, kept in
@@ -600,27 +640,10 @@ __device__ __forceinline__ void load_query_pre(const float* __restrict__ qu_lds,
   }
 }
 
-// exact_l2_ref with the first kVecPre elements of each lane taken from x and
-// the matching query elements from qv.  Elements past dim contribute
-// fma(0, 0, val) = val, so the sum is the reference's bit for bit.
-template <class T>
-__device__ __forceinline__ float exact_l2_pre(const uint32_t (&x)[kVecPre], const float (&qv)[kVecPre],
-                                              const uint8_t* __restrict__ rec, const float* __restrict__ qu_lds,
-                                              int dim, int lane) {
-  float val = 0.f;
-  const bool lo = lane < 32;
-#pragma unroll
-  for (int k = 0; k < kVecPre; k++) {
-    const int i = lane + 32 * k;
-    const float diff = lo && i < dim ? qv[k] - raw_to_float<T>(x[k]) : 0.f;
-    val = __fmaf_rn(diff, diff, val);
-  }
-  if (lo) {
-    for (int i = lane + 32 * kVecPre; i < dim; i += 32) {
-      const float diff = qu_lds[i] - elem_to_float<T>(rec, i);
-      val = __fmaf_rn(diff, diff, val);
-    }
-  }
+// The wave reduction of the exact distance over the lanes' sums (lanes < 32
+// hold them): an exchange of lanes 16 apart inside each 32-lane half, then
+// four row shifts, leave their total in lane 0 in exact_l2_ref's order.
+__device__ __forceinline__ float exact_reduce(float val, int lane) {
   val += __uint_as_float(xor_lane32<16>(__float_as_uint(val), lane));
   val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x108, 0xF, 0xF, false));
   val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x104, 0xF, 0xF, false));
@@ -629,15 +652,45 @@ __device__ __forceinline__ float exact_l2_pre(const uint32_t (&x)[kVecPre], cons
   return read_lane_f32(val, 0);
 }
 
-// exact_l2_pre for a dim KD known at compile time (a multiple of 32 up to
-// 32 kVecPre): lanes < 32 accumulate the same chain as exact_l2_pre without
-// its per-element tests (terms past KD would add fma(0, 0, val) = val), and
-// lanes >= 32 compute values that no step of the reduction carries into
-// lanes < 32 (the swizzle stays inside 32-lane halves, the row shifts inside
-// 16-lane rows), so lane 0 ends with the same sum bit for bit.
-template <class T, int KD>
-__device__ __forceinline__ float exact_l2_pre_fixed(const uint32_t (&x)[kVecPre], const float (&qv)[kVecPre],
-                                                    int lane) {
+// exact_l2_ref with the first kVecPre elements of each lane taken from x and
+// the matching query elements from qv.  Elements past dim contribute
+// fma(0, 0, val) = val, so the sum is the reference's bit for bit.  Split in
+// two: the lane's sum over its first kVecPre elements (exact_lane_pre), then
+// the rest of its elements and the wave reduction (exact_l2_rest).
+template <class T, class R>
+__device__ __forceinline__ float exact_lane_pre(const R (&x)[kVecPre], const float (&qv)[kVecPre], int dim,
+                                                int lane) {
+  float val = 0.f;
+  const bool lo = lane < 32;
+#pragma unroll
+  for (int k = 0; k < kVecPre; k++) {
+    const int i = lane + 32 * k;
+    const float diff = lo && i < dim ? qv[k] - raw_to_float<T>(x[k]) : 0.f;
+    val = __fmaf_rn(diff, diff, val);
+  }
+  return val;
+}
+
+template <class T>
+__device__ __forceinline__ float exact_l2_rest(float val, const uint8_t* __restrict__ rec,
+                                               const float* __restrict__ qu_lds, int dim, int lane) {
+  if (lane < 32) {
+    for (int i = lane + 32 * kVecPre; i < dim; i += 32) {
+      const float diff = qu_lds[i] - elem_to_float<T>(rec, i);
+      val = __fmaf_rn(diff, diff, val);
+    }
+  }
+  return exact_reduce(val, lane);
+}
+
+// exact_lane_pre for a dim KD known at compile time (a multiple of 32 up to
+// 32 kVecPre): lanes < 32 accumulate the same chain as exact_lane_pre
+// without its per-element tests (terms past KD would add fma(0, 0, val) =
+// val), and lanes >= 32 compute values that no step of exact_reduce carries
+// into lanes < 32 (the exchange stays inside 32-lane halves, the row shifts
+// inside 16-lane rows), so lane 0 ends with the same sum bit for bit.
+template <class T, int KD, class R>
+__device__ __forceinline__ float exact_lane_fixed(const R (&x)[kVecPre], const float (&qv)[kVecPre]) {
   static_assert(KD % 32 == 0 && KD <= 32 * kVecPre, "whole 32-element rows");
   float val = 0.f;
 #pragma unroll
@@ -647,12 +700,7 @@ __device__ __forceinline__ float exact_l2_pre_fixed(const uint32_t (&x)[kVecPre]
       val = __fmaf_rn(diff, diff, val);
     }
   }
-  val += __uint_as_float(xor_lane32<16>(__float_as_uint(val), lane));
-  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x108, 0xF, 0xF, false));
-  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x104, 0xF, 0xF, false));
-  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x102, 0xF, 0xF, false));
-  val += __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(val), 0x101, 0xF, 0xF, false));
-  return read_lane_f32(val, 0);
+  return val;
 }
 
 // Stable top-k insert (retset_push_topk_le32, kernel_helpers.cuh:65-104,

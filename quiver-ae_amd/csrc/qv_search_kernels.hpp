@@ -10,6 +10,8 @@
 #include "qv_common.hpp"
 #include "qv_device.hpp"
 
+#include <type_traits>
+
 namespace qv {
 namespace sk {
 
@@ -144,11 +146,25 @@ using namespace qv::sk;
 
 // Registers holding the start of a node record (see Query::fetch): NPL
 // neighbour slots per lane (lane l holds neighbours l and l + 64).
-template <int NPL>
+template <class T, int NPL>
 struct NodeRec {
+  // raw vector elements (load_vec_pre); bytes stay 8-bit values, so where two
+  // loads of them meet, the registers join without a zero-extension
+  using Raw = std::conditional_t<sizeof(T) == 1, uint8_t, uint32_t>;
   int deg;
   uint32_t nbr[NPL];
-  uint32_t xv[kVecPre];  // raw vector elements (load_vec_pre)
+  Raw xv[kVecPre];
+};
+
+// What a hop reads of its node's record, taken out of the registers the
+// record's loads wrote (Query::take) once they have arrived: the degree, this
+// lane's neighbour ids (0 past the degree) and this lane's sum over its
+// first vector elements for the exact distance.
+template <int NPL>
+struct Taken {
+  int deg;
+  uint32_t nbr[NPL];
+  float part;
 };
 
 // SC = 0: per-query LUT in LDS; SC > 0: LUT entries recomputed from the
@@ -157,7 +173,8 @@ struct NodeRec {
 template <class T, int Q, int MC, int SC, int NPL>
 struct Query {
   static_assert(NPL == 1 || NPL == 2, "one or two neighbours per lane");
-  using Rec = NodeRec<NPL>;
+  using Rec = NodeRec<T, NPL>;
+  using Tk = Taken<NPL>;
   const SearchArgs& a;
   float* lut;
   const float* piv;  // shared pivots (SC > 0)
@@ -215,9 +232,9 @@ struct Query {
     off_blk = (uint32_t)(min(lane, a.max_m - 1) * a.num_chunks);
   }
 
-  // This lane's code row in node v's neighbour-code block.
-  __device__ __forceinline__ const uint8_t* block_row(int32_t v) const {
-    return a.nbr_codes + (int64_t)v * (a.max_m * a.num_chunks) + off_blk;
+  // Node v's neighbour-code block (this lane's row at off_blk).
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t block(int32_t v) const {
+    return buf_at(a.nbr_codes + (int64_t)v * (a.max_m * a.num_chunks));
   }
 
   __device__ __forceinline__ const uint8_t* record(int32_t v) const {
@@ -231,26 +248,42 @@ struct Query {
   // loads are used, so waits on LDS traffic never wait for these.
   __device__ __forceinline__ void fetch(int32_t v, int lane, Rec& nr) const {
     const uint8_t* rec = record(v);
-    const uint8_t* nb = rec + a.data_size;
-    uint32_t z = 0;
-    asm volatile("" : "+v"(z));  // per-lane address: a vector load of the degree
-    nr.deg = *reinterpret_cast<const int*>(nb + z);
+    const __amdgpu_buffer_rsrc_t r = buf_at(rec);
+    const int ds = (int)a.data_size;  // a record is under 4 KB
+    nr.deg = (int)__builtin_amdgcn_raw_buffer_load_b32(r, 0, ds, 0);
 #pragma unroll
-    for (int j = 0; j < NPL; j++) nr.nbr[j] = *reinterpret_cast<const uint32_t*>(nb + off_nbr[j]);
+    for (int j = 0; j < NPL; j++) nr.nbr[j] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off_nbr[j], ds, 0);
     if constexpr (kD > 0)
-      load_vec_pre_fixed<T, kD>(rec, off_x, nr.xv);
+      load_vec_pre_buf<T, kD>(r, off_x, nr.xv);
     else
       load_vec_pre<T>(rec, a.dim, lane, nr.xv);
   }
 
-  // Exact distance of v and the top-k insert (the reference's second warp).
-  __device__ __forceinline__ void exact_and_topk(int32_t v, const uint32_t (&xv)[kVecPre], const uint8_t* rec,
-                                                 int lane) {
+  // The values a hop reads first from the record in nr.  Taken at the end
+  // of the hop that requested the record, they leave nr free for the next
+  // request: a record still in nr when the next one is requested into other
+  // registers has to be copied over at the end of the loop, and the copy
+  // waits for every load requested before it, the next code rows included.
+  __device__ __forceinline__ void take(const Rec& nr, Tk& tk, int lane) const {
+    // every load of the record is issued before the first wait for one
+    __builtin_amdgcn_sched_barrier(0);
+    tk.deg = read_lane_i32(nr.deg, 0);
+#pragma unroll
+    for (int j = 0; j < NPL; j++) tk.nbr[j] = lane + kWave * j < tk.deg ? nr.nbr[j] : 0u;
+    if constexpr (kD > 0)
+      tk.part = exact_lane_fixed<T, kD>(nr.xv, quv);
+    else
+      tk.part = exact_lane_pre<T>(nr.xv, quv, a.dim, lane);
+  }
+
+  // Exact distance of v from its lanes' sums (part) and the top-k insert
+  // (the reference's second warp).
+  __device__ __forceinline__ void exact_and_topk(int32_t v, float part, const uint8_t* rec, int lane) {
     float e;
     if constexpr (kD > 0)
-      e = exact_l2_pre_fixed<T, kD>(xv, quv, lane);
+      e = exact_reduce(part, lane);
     else
-      e = exact_l2_pre<T>(xv, quv, rec, qu, a.dim, lane);
+      e = exact_l2_rest<T>(part, rec, qu, a.dim, lane);
     last_e = e;
     const float dlast = read_lane_f32(td, a.topk - 1);
     if (fc < a.topk || e < dlast) topk_insert(td, ti, fc, a.topk, e, v);
@@ -258,11 +291,12 @@ struct Query {
 
   // One expansion of node v: persistent_merge_data (kernel_helpers.cuh:232-357)
   // followed by persistent_visit_select_dualwarp (kernel_helpers.cuh:422-489).
-  // nr holds v's record (fetch).  Returns the selected node or -1.  PF says
-  // which node's record the hop requests into nr once it has read v's: 0 none,
-  // 1 the speculated successor (below; with PF = 1 the selected node's record
-  // is also requested as soon as the merge knows it, when the guess missed),
-  // 2 the caller's nxt (the pipe lanes' next expansion; -1: not known).
+  // tk holds what was taken from v's record (fetch, take).  Returns the
+  // selected node or -1.  PF says which node's record the hop requests into
+  // nr and takes into tk at its end: 0 none, 1 the speculated successor
+  // (below; with PF = 1 the selected node's record is also requested as soon
+  // as the merge knows it, when the guess missed), 2 the caller's nxt (the
+  // pipe lanes' next expansion; -1: not known, v's record again).
   //
   // With PF, cr carries code rows from one hop to the next: when `have`, cr
   // holds (or is loading) v's neighbours' rows, requested by the previous hop.
@@ -272,17 +306,17 @@ struct Query {
   // through this hop's merge; `have` is set when the guess was the node
   // selected.  PF = 2 does the same for nxt, and `have` says nxt's rows are
   // in cr.  Only loads move: every result is the same.
+  static constexpr bool kRows = MC > 0 && MC % 16 == 0;  // code rows in registers (adc_load)
+
   template <int PF>
-  __device__ __forceinline__ int32_t hop(int32_t v, Rec& nr, CodeRow<MC>& cr, bool& have, int32_t nxt = -1) {
-    if constexpr (NPL == 2) return hop2<PF == 1>(v, nr);
+  __device__ __forceinline__ int32_t hop(int32_t v, Tk& tk, Rec& nr, CodeRow<MC>& cr, bool& have,
+                                         int32_t nxt = -1) {
+    if constexpr (NPL == 2) return hop2<PF == 1>(v, tk, nr);
     const int lane = opaque_lane();
-    const int deg = read_lane_i32(nr.deg, 0);
+    const int deg = tk.deg;
     evals += deg;
     const bool has = lane < deg;
-    const uint32_t nbr = has ? nr.nbr[0] : 0u;
-    uint32_t xv[kVecPre];
-#pragma unroll
-    for (int k = 0; k < kVecPre; k++) xv[k] = nr.xv[k];
+    const uint32_t nbr = tk.nbr[0];
     const uint8_t* rec = kD == 0 && a.dim > 32 * kVecPre ? record(v) : nullptr;
     // With PF, the next node is most often the beam's first unvisited entry
     // (whenever no new candidate beats it), so its record is requested right
@@ -299,22 +333,21 @@ struct Query {
     // are requested without waiting for its record, and after a wrong guess
     // the chosen node's rows follow its record at once.
     const bool blk = a.nbr_codes != nullptr;
-    if constexpr (MC > 0 && MC % 16 == 0) {
+    if constexpr (kRows) {
       if (!(PF != 0 && have)) {
         if (blk)
-          adc_load<MC>(cr, block_row(v));
+          adc_load<MC>(cr, block(v), off_blk);
         else
           adc_load<MC>(cr, a.codes, nbr);
       }
-      // Issued on every hop (v's own record when there is no unvisited entry
-      // to guess), so every path reaches the ADC with the same loads in
-      // flight and the compiler's wait for the code rows can leave the
-      // record outstanding.
+      // Issued on every hop (v's own record when there is no node to
+      // request), as are the rows below, so every path reaches each wait with
+      // the same loads in flight: the compiler's wait for the code rows then
+      // leaves the record outstanding, and the take's for the record leaves
+      // the next rows.
       if constexpr (PF == 1) fetch(spec ? (int32_t)key_id(bu) : v, lane, nr);
-      if constexpr (PF == 2) {
-        if (nxt >= 0) fetch(nxt, lane, nr);
-      }
-      exact_and_topk(v, xv, rec, lane);
+      if constexpr (PF == 2) fetch(nxt >= 0 ? nxt : v, lane, nr);
+      exact_and_topk(v, tk.part, rec, lane);
       if constexpr (SC > 0)
         d = adc_recompute<MC, SC, kQd>(cr, qd);
       else
@@ -323,29 +356,25 @@ struct Query {
       // guessed successor's (PF = 1) or nxt's (PF = 2)
       if constexpr (PF != 0) {
         const bool go = PF == 1 ? spec : nxt >= 0;
-        if (go) {
-          if (blk) {
-            adc_load<MC>(cr, block_row(PF == 1 ? (int32_t)key_id(bu) : nxt));
-          } else {
-            const int ndeg = read_lane_i32(nr.deg, 0);
-            adc_load<MC>(cr, a.codes, lane < ndeg ? nr.nbr[0] : 0u);
-          }
+        if (blk) {
+          adc_load<MC>(cr, block(go ? (PF == 1 ? (int32_t)key_id(bu) : nxt) : v), off_blk);
+        } else {
+          const int ndeg = read_lane_i32(nr.deg, 0);
+          adc_load<MC>(cr, a.codes, lane < ndeg ? nr.nbr[0] : 0u);
         }
       }
     } else {
       if (PF == 1 && spec) fetch((int32_t)key_id(bu), lane, nr);
       if (PF == 2 && nxt >= 0) fetch(nxt, lane, nr);
       d = adc_row<MC>(a.codes + (int64_t)nbr * a.num_chunks, lut, a.num_chunks);
-      exact_and_topk(v, xv, rec, lane);
+      exact_and_topk(v, tk.part, rec, lane);
     }
     const uint64_t nkey = has ? make_key(d, nbr, false) : sentinel_key(lane);
     bool hit = false;
-    const int32_t nx = merge_select<true, PF == 1>(nkey, has, lane, nr, spec, bu, hit);
-    if constexpr (PF == 1 && MC > 0 && MC % 16 == 0) {
-      if (blk && !hit && nx >= 0) adc_load<MC>(cr, block_row(nx));
-      have = hit || (blk && nx >= 0);
-    }
-    if constexpr (PF == 2 && MC > 0 && MC % 16 == 0) have = nxt >= 0;
+    const int32_t nx = merge_select<true, PF == 1, kRows>(nkey, has, lane, nr, spec, bu, hit, &cr);
+    if constexpr (PF == 1 && kRows) have = hit || (blk && nx >= 0);
+    if constexpr (PF == 2 && kRows) have = nxt >= 0;
+    if constexpr (PF != 0) take(nr, tk, lane);
     return nx;
   }
 
@@ -358,15 +387,12 @@ struct Query {
   // guessed successor is the first unvisited entry before A (its record is
   // requested at the start), compared by key after B.
   template <bool PF>
-  __device__ __forceinline__ int32_t hop2(int32_t v, Rec& nr) {
+  __device__ __forceinline__ int32_t hop2(int32_t v, Tk& tk, Rec& nr) {
     const int lane = opaque_lane();
-    const int deg = read_lane_i32(nr.deg, 0);
+    const int deg = tk.deg;
     evals += deg;
     const bool has0 = lane < deg, has1 = lane + kWave < deg;
-    const uint32_t nbr0 = has0 ? nr.nbr[0] : 0u, nbr1 = has1 ? nr.nbr[1] : 0u;
-    uint32_t xv[kVecPre];
-#pragma unroll
-    for (int k = 0; k < kVecPre; k++) xv[k] = nr.xv[k];
+    const uint32_t nbr0 = tk.nbr[0], nbr1 = tk.nbr[1];
     const uint8_t* rec = kD == 0 && a.dim > 32 * kVecPre ? record(v) : nullptr;
     const bool spec = PF && u < sz;
     const uint64_t spec_key = bu;
@@ -376,7 +402,7 @@ struct Query {
       adc_load<MC>(c0, a.codes, nbr0);
       adc_load<MC>(c1, a.codes, nbr1);
       if constexpr (PF) fetch(spec ? (int32_t)key_id(bu) : v, lane, nr);
-      exact_and_topk(v, xv, rec, lane);
+      exact_and_topk(v, tk.part, rec, lane);
       if constexpr (SC > 0) {
         d0 = adc_recompute<MC, SC, kQd>(c0, qd);
         d1 = adc_recompute<MC, SC, kQd>(c1, qd);
@@ -388,13 +414,15 @@ struct Query {
       if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
       d0 = adc_row<MC>(a.codes + (int64_t)nbr0 * a.num_chunks, lut, a.num_chunks);
       d1 = adc_row<MC>(a.codes + (int64_t)nbr1 * a.num_chunks, lut, a.num_chunks);
-      exact_and_topk(v, xv, rec, lane);
+      exact_and_topk(v, tk.part, rec, lane);
     }
     const uint64_t k0 = has0 ? make_key(d0, nbr0, false) : sentinel_key(lane);
     const uint64_t k1 = has1 ? make_key(d1, nbr1, false) : sentinel_key(lane + kWave);
     bool hit = false;
     merge_select<false, false>(k0, has0, lane, nr, false, spec_key, hit);
-    return merge_select<true, PF>(k1, has1, lane, nr, spec, spec_key, hit);
+    const int32_t nx = merge_select<true, PF>(k1, has1, lane, nr, spec, spec_key, hit);
+    if constexpr (PF) take(nr, tk, lane);
+    return nx;
   }
 
   // Every LDS beam position from sz to cap holds kPadKey (above every key):
@@ -470,9 +498,9 @@ struct Query {
   // hit: (PF) the selected node is the guessed one (key spec_key), whose
   // record the hop requested at its start.  SEL = false merges without a
   // selection (the first batch of a two-slot hop) and returns -1.
-  template <bool SEL, bool PF>
+  template <bool SEL, bool PF, bool ROWS = false>
   __device__ __forceinline__ int32_t merge_select(uint64_t nkey, bool has, int lane, Rec& nr, bool spec,
-                                                  uint64_t spec_key, bool& hit) {
+                                                  uint64_t spec_key, bool& hit, CodeRow<MC>* cr = nullptr) {
     const int ef = a.ef;
     // Candidates at or above the last entry of a full beam end beyond ef
     // (lastk: read with the previous merge's register reload).
@@ -548,7 +576,17 @@ struct Query {
     if constexpr (PF) {
       // (the key test, not the position: a winning candidate lands at u too)
       hit = spec && selkey == spec_key;
-      if (!hit) fetch((int32_t)key_id(selkey), lane, nr);
+      if (!hit) {
+        fetch((int32_t)key_id(selkey), lane, nr);
+        // ROWS: the selected node's code rows too, right behind its record
+        // (without the table, rows of the codes' first nodes, which only
+        // keep every path ending with rows requested after the record)
+        if constexpr (ROWS) {
+          const int code_bytes = (int)min(a.num_points * a.num_chunks, (int64_t)0x7fffffff);
+          adc_load<MC>(*cr, a.nbr_codes != nullptr ? block((int32_t)key_id(selkey)) : buf_at(a.codes, code_bytes),
+                       off_blk);
+        }
+      }
     }
     if (vm == 0) {
       mark_visited(selpos, selkey, lane);
@@ -731,7 +769,8 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       }
     };
 
-    NodeRec<NPL> nr;
+    NodeRec<T, NPL> nr;
+    Taken<NPL> tk;
     CodeRow<MC> cr;
     bool have = false;
     // Expansion for the pipe lanes: nxt is the expansion expected next (-1:
@@ -741,9 +780,10 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     auto expand = [&](int32_t v, int32_t nxt) -> int32_t {
       if (v != pf) {
         Qy.fetch(v, lane, nr);
+        Qy.take(nr, tk, lane);
         have = false;
       }
-      const int32_t nx = Qy.template hop<2>(v, nr, cr, have, nxt);
+      const int32_t nx = Qy.template hop<2>(v, tk, nr, cr, have, nxt);
       pf = NPL == 1 ? nxt : -1;
       return nx;
     };
@@ -753,9 +793,10 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       // hop selects is the next one expanded, so its record is requested while
       // the hop finishes.
       Qy.fetch(entry, lane, nr);
+      Qy.take(nr, tk, lane);
       int32_t v = entry;
       while (true) {
-        const int32_t nx = Qy.template hop<1>(v, nr, cr, have);
+        const int32_t nx = Qy.template hop<1>(v, tk, nr, cr, have);
         log_hop(v);
         ++step;
         if (gpr && check()) {
