@@ -698,6 +698,14 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     }
     qid = read_lane_i32(qid, 0);
     if (qid < 0) break;
+    // Later tickets issue first: the last-admitted queries set the end of the
+    // launch, the earlier ones have time to spare.
+    switch ((int)(((int64_t)qid * 4) / a.nq)) {
+      case 0: __builtin_amdgcn_s_setprio(0); break;
+      case 1: __builtin_amdgcn_s_setprio(1); break;
+      case 2: __builtin_amdgcn_s_setprio(2); break;
+      default: __builtin_amdgcn_s_setprio(3); break;
+    }
     if (a.t_start && lane == 0) a.t_start[qid] = wall_ticks();
 
     Query<T, Q, MC, SC, NPL> Qy(a, smem, piv);
