@@ -1089,7 +1089,13 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     if (st != hipErrorNotReady) HIP_OK(st);
     if (has_deadline && !timed_out && clock::now() > deadline) timed_out = true;
     if (timed_out) __atomic_store_n(ix->h_ctrl + 1, 1, __ATOMIC_RELEASE);
-    std::this_thread::sleep_for(std::chrono::microseconds(streaming ? 5 : 50));
+    // Streaming: every completion is in, the launch is draining its last
+    // waves; a short sleep request is rounded up to tens of microseconds, so
+    // the host keeps polling instead.
+    if (streaming)
+      std::this_thread::yield();
+    else
+      std::this_thread::sleep_for(std::chrono::microseconds(50));
   }
   if (!o.device_buffers) {
     HIP_OK(hipMemcpyAsync(ids, d_ids, sizeof(int32_t) * (size_t)nq * topk, hipMemcpyDeviceToHost, ix->stream));
