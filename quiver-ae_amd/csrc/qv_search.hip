@@ -934,7 +934,9 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   int32_t* d_found = (o.device_buffers && found) ? found : ix->d_found;
 
   HIP_OK(hipMemsetAsync(ix->d_counters, 0, 64, ix->stream));
-  HIP_OK(hipStreamSynchronize(ix->stream));
+  // (queries from host memory: uploaded before the clock starts; device
+  // buffers need no wait, the stream orders the clear before the launch)
+  if (!o.device_buffers) HIP_OK(hipStreamSynchronize(ix->stream));
   // Static batches (StaticDispatch, search.cu:1703-1796): sequential batches of
   // num_blocks x queries_per_block queries, each admitted once the previous
   // one has completed; served by the same persistent launch, the host gating
