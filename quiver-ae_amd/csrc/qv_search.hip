@@ -324,7 +324,10 @@ static void ensure_scratch(qv_index* ix, int64_t nq, int k) {
   HIP_OK(hipMalloc(&ix->d_tend, sizeof(uint64_t) * (size_t)cq));
   HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_ring), sizeof(int32_t) * (size_t)cq,
                        hipHostMallocCoherent));
-  HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_stage), sizeof(int32_t) * (size_t)(4 + 3 * cq)));
+  // coherent: the search kernel writes the per-query hop, stop and evaluation
+  // counts straight into it
+  HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_stage), sizeof(int32_t) * (size_t)(4 + 3 * cq),
+                       hipHostMallocCoherent));
   ix->cap_q = cq;
   ix->cap_k = ck;
 }
@@ -968,9 +971,14 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   a.out_ids = d_ids;
   a.out_dists = d_dists;
   a.out_found = d_found;
-  a.out_hops = ix->d_hops;
-  a.out_stopped = ix->d_stopped;
-  a.out_evals = ix->d_evals;
+  // per-query counts into the pinned staging buffer (no copies after the launch)
+  {
+    int32_t* dev_stage = nullptr;
+    HIP_OK(hipHostGetDevicePointer(reinterpret_cast<void**>(&dev_stage), ix->h_stage, 0));
+    a.out_hops = dev_stage + 4;
+    a.out_stopped = dev_stage + 4 + ix->cap_q;
+    a.out_evals = dev_stage + 4 + 2 * (size_t)ix->cap_q;
+  }
   a.t_start = ix->d_tstart;
   a.t_end = ix->d_tend;
   a.counters = ix->d_counters;
@@ -1108,19 +1116,13 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   }
   const auto t1 = clock::now();
 
-  // Counters, hop counts, stop flags and evaluation counts in one round trip
-  // through the pinned staging buffer.
+  // The counters through the pinned staging buffer; the kernel wrote the hop
+  // counts, stop flags and evaluation counts into it directly.
   int32_t* const st_counters = ix->h_stage;
   int32_t* const st_hops = ix->h_stage + 4;
   int32_t* const st_stopped = st_hops + ix->cap_q;
   int32_t* const st_evals = st_stopped + ix->cap_q;
-  const size_t qbytes = sizeof(int32_t) * (size_t)nq;
   HIP_OK(hipMemcpyAsync(st_counters, ix->d_counters, 4 * sizeof(int32_t), hipMemcpyDeviceToHost, ix->stream));
-  HIP_OK(hipMemcpyAsync(st_hops, ix->d_hops, qbytes, hipMemcpyDeviceToHost, ix->stream));
-  if (rep) {
-    HIP_OK(hipMemcpyAsync(st_stopped, ix->d_stopped, qbytes, hipMemcpyDeviceToHost, ix->stream));
-    HIP_OK(hipMemcpyAsync(st_evals, ix->d_evals, qbytes, hipMemcpyDeviceToHost, ix->stream));
-  }
   HIP_OK(hipStreamSynchronize(ix->stream));
   int32_t counters[4];
   std::memcpy(counters, st_counters, sizeof(counters));
