@@ -162,8 +162,9 @@ int qv_index_load_nav(qv_index* index, const char* nav_dir);
  * (kernel_helpers.cuh:271-287).  With it a hop reads its node's rows as one
  * block whose address needs no neighbour ids, so the next node's rows are
  * requested together with its record; results are unchanged.  Needs
- * num_chunks a multiple of 16 and max_m <= 64; QV_ENOMEM when the device
- * lacks the room (plus 1 GiB). */
+ * num_chunks 32 or 48 (the chunk counts whose hop reads the table) and
+ * max_m <= 64 (QV_EUNSUPPORTED otherwise); QV_ENOMEM when the device lacks
+ * the room (plus 1 GiB). */
 int qv_index_neighbour_codes(qv_index* index, int32_t enable);
 
 /* ---- Host-only pieces of the setup path (no GPU needed) ---------------------
@@ -214,6 +215,16 @@ typedef struct {
   float step_recall_threshold;  /* (0, 1]; --recall-threshold, 0.9 by default */
   int32_t* step_recall_step;
   int32_t* step_recall_hits;
+  /* Open-loop arrival (streaming admission only; no counterpart in the
+   * reference, whose admission loop refills a window as queries complete,
+   * search.cu:983-1051): with arrival_qps > 0, queries arrive in groups of
+   * arrival_batch at a fixed rate, group j at t0 + j * arrival_batch /
+   * arrival_qps, and each group is admitted on its clock however many queries
+   * are still in flight.  A query's latency runs from its group's scheduled
+   * arrival.  0 (default): the reference's closed window. */
+  double arrival_qps;
+  int32_t arrival_batch;     /* queries per arrival, >= 1 (default 1) */
+  int32_t reserved0;
 } qv_search_opts;
 
 /* shared::RunReport (src/shared/common/run_report.hpp:32-56) for one search. */
@@ -243,20 +254,23 @@ int qv_search(qv_index* index, const float* queries, int64_t nq, int32_t dim,
               int32_t topk, int32_t ef_search, const qv_search_opts* opts,
               int32_t* ids, float* dists, int32_t* found, qv_search_report* report);
 
-/* No counterpart in the reference.  For callers that cannot allocate (code
- * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc): qv_search with every query admitted at launch, all of
- * d_queries / d_ids / d_dists / d_found (may be NULL) device pointers, and
- * the search's scratch (dispatch counters, per-query hop and evaluation
- * counts) taken from one fixed device array of QV_NOALLOC_SCRATCH_BYTES per
- * GPU, held until the process ends.  It calls no hipMalloc, hipHostMalloc,
- * hipFree or memset.  Limits: 1..QV_NOALLOC_MAX_QUERIES queries per call
- * (QV_EINVAL beyond); opts->timeout_s must be 0 (no deadline).  Results equal
- * qv_search's.  Calls share the GPU's array: calls from one process are
- * serialised; work captured from it and replayed concurrently on one GPU
- * races.  Blocking; the report has no latency percentiles (queries are not
- * stamped). */
-#define QV_NOALLOC_SCRATCH_BYTES (8 * 1024 * 1024 + 256)
+/* No counterpart in the reference.  For callers that cannot allocate (tight
+ * serving loops, harnesses that forbid hipMalloc): qv_search with every query
+ * admitted at launch, all of d_queries / d_ids / d_dists / d_found (may be
+ * NULL) device pointers, and the search's scratch (dispatch counters,
+ * per-query hop, evaluation and early-exit counts) taken from one fixed
+ * device array of QV_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends.  It calls no hipMalloc, hipHostMalloc, hipFree or memset of any kind.
+ * It is synchronous: it runs on the handle's own stream and returns once the
+ * results are in the caller's device buffers, so it cannot be captured into
+ * a caller's HIP graph.  Limits: 1..QV_NOALLOC_MAX_QUERIES queries per call
+ * (QV_EINVAL beyond); opts->timeout_s must be 0 (no deadline); no per-step
+ * recall or open-loop arrival.  Results (ids, distances, found counts, hop
+ * and evaluation totals, early exits) equal qv_search's.  All calls on one
+ * GPU share its array and are serialised by a lock per GPU; calls on
+ * different GPUs run independently.  The report has no latency percentiles
+ * (queries are not stamped). */
+#define QV_NOALLOC_SCRATCH_BYTES (12 * 1024 * 1024 + 256)
 #define QV_NOALLOC_MAX_QUERIES (1024 * 1024)
 int qv_search_noalloc(qv_index* index, const float* d_queries, int64_t nq, int32_t dim,
                       int32_t topk, int32_t ef_search, const qv_search_opts* opts,
@@ -286,6 +300,8 @@ int qv_device_info(int device, char* name, int32_t name_len, int32_t* num_cus,
  * library's HIP runtime.  kind: 0 host->device, 1 device->host, 2 device->device
  * (one GPU, 16-byte aligned: a grid-stride copy kernel, else hipMemcpy). */
 int qv_device_count(int32_t* count);
+/* Free and total device memory of `device` (hipMemGetInfo). */
+int qv_device_mem_info(int device, int64_t* free_bytes, int64_t* total_bytes);
 int qv_dev_alloc(int device, int64_t bytes, void** out);
 int qv_dev_free(void* ptr);
 int qv_dev_copy(void* dst, const void* src, int64_t bytes, int32_t kind);

@@ -354,12 +354,17 @@ int main(int argc, char** argv) {
     o.gpruning_patience = 8;
     o.skip_nav = f["--skip-nav"].used ? 1 : 0;
     o.kernel = kernel;
-    if (f["--static-batches"].used) {  // run_static_batch_search (search.cu:1703-1796)
+    const bool static_batches = f["--static-batches"].used;
+    if (static_batches) {  // run_static_batch_search (search.cu:1703-1796)
       o.admission = QV_ADMIT_STATIC;
-      const int64_t stride = (int64_t)nb * qpb;
-      std::cout << "[Quiver] StaticBatch: " << (nq + stride - 1) / stride << " batches of " << nb
-                << " blocks x Q=" << qpb << " = " << stride << " queries per batch, total " << nq << " queries"
-                << std::endl;
+      // With --num-blocks unset (0) the library fills the GPU with slots; the
+      // batch line then follows the search, from the slots it launched.
+      if (nb > 0) {
+        const int64_t stride = (int64_t)nb * qpb;
+        std::cout << "[Quiver] StaticBatch: " << (nq + stride - 1) / stride << " batches of " << nb
+                  << " blocks x Q=" << qpb << " = " << stride << " queries per batch, total " << nq << " queries"
+                  << std::endl;
+      }
     }
     if (const char* e = std::getenv("QUIVER_PREFEED")) o.prefeed = std::atoi(e);
     if (const char* e = std::getenv("QUIVER_ADMIT_MIN_BATCH")) o.admit_min_batch = std::max(1, std::atoi(e));
@@ -381,6 +386,13 @@ int main(int argc, char** argv) {
       return 1;
     }
     qv_last_hops(ix, hops.data(), nq);
+    if (static_batches && nb <= 0) {
+      // max_inflight of a static search is its batch size: min(nq, slots)
+      const int64_t stride = std::max<int64_t>(1, rep.max_inflight);
+      std::cout << "[Quiver] StaticBatch: " << (nq + stride - 1) / stride << " batches of " << stride
+                << " queries (query slots filling the GPU, Q=" << qpb << "), total " << nq << " queries"
+                << std::endl;
+    }
     if (step_recall && !write_step_recall(step_csv, sr_step, sr_hits, topk, recall_threshold)) {
       qv_index_close(ix);
       return 1;

@@ -576,6 +576,19 @@ int qv_device_info(int device, char* name, int32_t name_len, int32_t* num_cus, i
   });
 }
 
+int qv_device_mem_info(int device, int64_t* free_bytes, int64_t* total_bytes) {
+  return qv::guard([&] {
+    int n = 0;
+    HIP_OK(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) qv::fail(QV_EINVAL, "device not present");
+    HIP_OK(hipSetDevice(device));
+    size_t f = 0, t = 0;
+    HIP_OK(hipMemGetInfo(&f, &t));
+    if (free_bytes) *free_bytes = (int64_t)f;
+    if (total_bytes) *total_bytes = (int64_t)t;
+  });
+}
+
 int qv_device_count(int32_t* count) {
   return qv::guard([&] {
     if (!count) qv::fail(QV_EINVAL, "null argument");

@@ -241,37 +241,44 @@ LaunchShape shape_launch(const LaunchPlan& lp, int64_t slots, int num_cus) {
 //   [0, 256)                     dispatch counters (ticket, done, error bits)
 //   [256, +4 kNoAllocMaxQueries) per-query hop counts
 //   [.., +4 kNoAllocMaxQueries)  per-query ADC evaluation counts
+//   [.., +4 kNoAllocMaxQueries)  per-query early-exit flags
 // Host code never uses the symbol's name as an address: each device's copy is
 // looked up once with hipGetSymbolAddress.
 constexpr int64_t kNoAllocBytes = QV_NOALLOC_SCRATCH_BYTES;
 constexpr int64_t kNoAllocMaxQueries = QV_NOALLOC_MAX_QUERIES;
 constexpr int64_t kNoAllocHopsOff = 256;
 constexpr int64_t kNoAllocEvalsOff = kNoAllocHopsOff + 4 * kNoAllocMaxQueries;
-static_assert(kNoAllocEvalsOff + 4 * kNoAllocMaxQueries <= kNoAllocBytes, "scratch holds every count");
+constexpr int64_t kNoAllocStoppedOff = kNoAllocEvalsOff + 4 * kNoAllocMaxQueries;
+static_assert(kNoAllocStoppedOff + 4 * kNoAllocMaxQueries <= kNoAllocBytes, "scratch holds every count");
 __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
 
-// Zero fill by vector stores (no hipMemsetAsync: a caller may capture the
-// stream into a graph, where memset nodes are avoided).
+// Zero fill by vector stores: the allocation-free entry point calls no
+// memset of any kind.
 __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t words) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (int64_t)gridDim.x * blockDim.x)
     p[i] = 0u;
 }
 
-// totals[0] += sum of hops, totals[1] += sum of evals (64-bit).
-__global__ __launch_bounds__(256) void sum_counts_kernel(const int32_t* hops, const int32_t* evals, int64_t n,
+// totals[0] += sum of hops, totals[1] += sum of evals, totals[2] += early
+// exits (64-bit).
+__global__ __launch_bounds__(256) void sum_counts_kernel(const int32_t* hops, const int32_t* evals,
+                                                         const int32_t* stopped, int64_t n,
                                                          unsigned long long* totals) {
-  unsigned long long h = 0, e = 0;
+  unsigned long long h = 0, e = 0, s = 0;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     h += (unsigned long long)hops[i];
     e += (unsigned long long)evals[i];
+    s += (unsigned long long)stopped[i];
   }
   for (int off = 32; off > 0; off >>= 1) {
     h += shfl_xor64(h, off);
     e += shfl_xor64(e, off);
+    s += shfl_xor64(s, off);
   }
   if ((threadIdx.x & 63) == 0) {
     atomicAdd(&totals[0], h);
     atomicAdd(&totals[1], e);
+    atomicAdd(&totals[2], s);
   }
 }
 
@@ -602,7 +609,9 @@ void set_neighbour_codes(qv_index* ix, bool enable) {
   }
   if (ix->d_nbr_codes) return;
   const Layout& L = ix->lay;
-  if (ix->M % 16 != 0) fail(QV_EUNSUPPORTED, "the neighbour code table needs M a multiple of 16");
+  // Only the 32- and 48-chunk hops read code rows from the table (kRows);
+  // any other M would hold its bytes and change nothing.
+  if (ix->M != 32 && ix->M != 48) fail(QV_EUNSUPPORTED, "the neighbour code table needs M = 32 or 48");
   if (L.max_m0 > kWave) fail(QV_EUNSUPPORTED, "the neighbour code table needs R <= 64");
   const int64_t bytes = L.num_data * L.max_m0 * ix->M;
   size_t free_b = 0, total_b = 0;
@@ -903,10 +912,24 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
       fail(QV_EUNSUPPORTED, "per-step recall ground truth wider than 256 ids");
   }
 
+  const bool open_loop = o.arrival_qps > 0.0;
+  if (open_loop) {
+    if (o.admission != QV_ADMIT_STREAMING)
+      fail(QV_EINVAL, "open-loop arrival (arrival_qps > 0) needs QV_ADMIT_STREAMING admission");
+    if (o.arrival_batch < 1) fail(QV_EINVAL, "arrival_batch must be at least 1");
+    if (step_recall) fail(QV_EINVAL, "open-loop arrival does not take per-step recall");
+    if (!(o.arrival_qps < 1e12) || (double)nq / o.arrival_qps > 3600.0)
+      fail(QV_EINVAL, "open-loop arrival must offer its queries within an hour");
+  }
+
   HIP_OK(hipSetDevice(ix->device));
   ensure_scratch(ix, nq, topk);
   const int64_t requested = o.num_blocks > 0 ? (int64_t)o.num_blocks * o.queries_per_block : INT64_MAX;
-  const LaunchPlan lp = launch_plan(ix, ef, o.kernel, std::min<int64_t>(nq, requested));
+  // Queries the call can have in flight.  Open loop: by Little's law, the
+  // offered rate times a nominal 2 ms in the system, plus one arrival.
+  int64_t need = std::min<int64_t>(nq, requested);
+  if (open_loop) need = std::min<int64_t>(need, (int64_t)std::ceil(o.arrival_qps * 2e-3) + o.arrival_batch);
+  const LaunchPlan lp = launch_plan(ix, ef, o.kernel, need);
   const int spc = lp.slots_per_cu;
   if (spc <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
   // Query slots (search.cu:393-399): num_blocks x queries_per_block.  Each slot
@@ -923,23 +946,18 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   const int num_blocks = grid * ls.waves;  // query slots (waves) launched
   if (o.admission != QV_ADMIT_STREAMING && o.admission != QV_ADMIT_BATCH && o.admission != QV_ADMIT_STATIC)
     fail(QV_EINVAL, "admission must be QV_ADMIT_STREAMING, QV_ADMIT_BATCH or QV_ADMIT_STATIC");
-  const int max_inflight = (int)std::min<int64_t>(
-      nq, o.admission == QV_ADMIT_STATIC ? slots : slots + std::max(0, o.prefeed));
+  // Open loop: every arrival is admitted on its clock, however many queries
+  // are still in flight.
+  const int max_inflight = open_loop ? (int)nq
+                                     : (int)std::min<int64_t>(
+                                           nq, o.admission == QV_ADMIT_STATIC ? slots : slots + std::max(0, o.prefeed));
 
-  const float* d_q = queries;
-  if (!o.device_buffers) {
-    HIP_OK(hipMemcpyAsync(ix->d_queries, queries, sizeof(float) * (size_t)nq * dim,
-                          hipMemcpyHostToDevice, ix->stream));
-    d_q = ix->d_queries;
-  }
+  const float* d_q = o.device_buffers ? queries : ix->d_queries;
   int32_t* d_ids = o.device_buffers ? ids : ix->d_ids;
   float* d_dists = o.device_buffers ? dists : ix->d_dists;
   int32_t* d_found = (o.device_buffers && found) ? found : ix->d_found;
 
   HIP_OK(hipMemsetAsync(ix->d_counters, 0, 64, ix->stream));
-  // (queries from host memory: uploaded before the clock starts; device
-  // buffers need no wait, the stream orders the clear before the launch)
-  if (!o.device_buffers) HIP_OK(hipStreamSynchronize(ix->stream));
   // Static batches (StaticDispatch, search.cu:1703-1796): sequential batches of
   // num_blocks x queries_per_block queries, each admitted once the previous
   // one has completed; served by the same persistent launch, the host gating
@@ -986,8 +1004,10 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   a.terminate = dev_ctrl + 1;
   a.ring = dev_ring;
   // Feed waits end on their own after this long even if the host never
-  // admits more work, so a lost host thread cannot leave the kernel spinning.
-  const double spin_s = o.timeout_s > 0 ? o.timeout_s + 5.0 : 60.0;
+  // admits more work, so a lost host thread cannot leave the kernel spinning
+  // (open loop: the arrivals' own span on top).
+  const double spin_s =
+      (o.timeout_s > 0 ? o.timeout_s + 5.0 : 60.0) + (open_loop ? (double)nq / o.arrival_qps : 0.0);
   a.spin_limit_ticks = (uint64_t)(spin_s * 1e8);
   a.rec_ids = nullptr;
   a.rec_dists = nullptr;
@@ -1015,12 +1035,19 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   }
 
   using clock = std::chrono::steady_clock;
+  // The clock starts before the queries leave host memory and before the
+  // launch: the reference takes t0 ahead of H2D_initial and stamps the whole
+  // initial window with it (search.cu:865-877).  The upload and the launch
+  // share the stream, so the kernel starts once its queries are in HBM.
+  const auto t0 = clock::now();
+  if (!o.device_buffers)
+    HIP_OK(hipMemcpyAsync(ix->d_queries, queries, sizeof(float) * (size_t)nq * dim, hipMemcpyHostToDevice,
+                          ix->stream));
   HIP_OK(hipEventRecord(ix->ev0, ix->stream));
   hipLaunchKernelGGL(lp.kern, dim3(grid), dim3(kWave * ls.waves), (size_t)ls.lds, ix->stream, a);
   HIP_OK(hipGetLastError());
   HIP_OK(hipEventRecord(ix->ev1, ix->stream));
 
-  const auto t0 = clock::now();
   const bool has_deadline = o.timeout_s > 0;
   const auto deadline = t0 + std::chrono::duration_cast<clock::duration>(
                                  std::chrono::duration<double>(has_deadline ? o.timeout_s : 0.0));
@@ -1032,7 +1059,15 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     std::vector<clock::time_point> admit((size_t)nq);
     lat_ms.assign((size_t)nq, 0.0);
     const int64_t stride = static_batches ? std::min<int64_t>(nq, slots) : 0;
-    int64_t fed = static_batches ? stride : max_inflight;
+    // Open loop: arrival j brings queries [j B, (j + 1) B) at t0 + j B / rate,
+    // and each query's latency runs from its arrival's scheduled time, so a
+    // late admission by the host counts against the search.
+    const int64_t arr_b = open_loop ? o.arrival_batch : 1;
+    const double arr_gap = open_loop ? (double)arr_b / o.arrival_qps : 0.0;
+    auto arrival_time = [&](int64_t j) {
+      return t0 + std::chrono::duration_cast<clock::duration>(std::chrono::duration<double>((double)j * arr_gap));
+    };
+    int64_t fed = static_batches ? stride : (open_loop ? std::min<int64_t>(nq, arr_b) : max_inflight);
     int64_t batch_begin = 0;  // static batches: the batch in flight is [batch_begin, fed)
     auto batch_t = t0;
     // a static batch's queries all take its wall time as their latency (search.cu:1783-1788)
@@ -1055,7 +1090,23 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
         progressed = true;
       }
       const int64_t target = std::min<int64_t>(nq, done + max_inflight);
-      if (static_batches) {
+      if (open_loop) {
+        if (fed < nq) {
+          const auto now = clock::now();
+          int64_t to = fed;
+          while (to < nq && arrival_time(to / arr_b) <= now) {
+            const int64_t end = std::min<int64_t>(nq, to + arr_b);
+            const auto at = arrival_time(to / arr_b);
+            for (int64_t i = to; i < end; i++) admit[(size_t)i] = at;
+            to = end;
+          }
+          if (to > fed) {
+            fed = to;
+            __atomic_store_n(ix->h_ctrl, (int32_t)fed, __ATOMIC_RELEASE);
+            progressed = true;
+          }
+        }
+      } else if (static_batches) {
         if (done == fed && fed < nq) {
           const auto now = clock::now();
           close_batch(now);
@@ -1193,14 +1244,18 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
 // Per device: the address of its copy of `scratch` (hipGetSymbolAddress, once,
 // with the device current).
 struct NoAllocDevice {
+  std::mutex mu;  // one array per device: calls on one GPU are serialised by it
   uint8_t* ptr = nullptr;
 };
-static std::mutex g_noalloc_mu;
+static std::mutex g_noalloc_lookup_mu;  // guards only the one-time address lookups
 static NoAllocDevice g_noalloc[64];
 
+// The device's entry with its array's address looked up (the device must be
+// current).
 static NoAllocDevice& noalloc_device(int device) {
   if (device < 0 || device >= 64) fail(QV_EINVAL, "device out of range");
   NoAllocDevice& nd = g_noalloc[device];
+  std::lock_guard<std::mutex> lk(g_noalloc_lookup_mu);
   if (!nd.ptr) {
     void* p = nullptr;
     HIP_OK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
@@ -1243,9 +1298,9 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
   if (o.step_recall_gt) fail(QV_EINVAL, "qv_search_noalloc does not take per-step recall");
   if (!d_queries || !d_ids || !d_dists) fail(QV_EINVAL, "null argument");
 
-  std::lock_guard<std::mutex> dlk(g_noalloc_mu);  // one device array: calls on one GPU are serialised here
   HIP_OK(hipSetDevice(ix->device));
   NoAllocDevice& nd = noalloc_device(ix->device);
+  std::lock_guard<std::mutex> dlk(nd.mu);  // calls on one GPU share its array
   uint8_t* const base = nd.ptr;
   const int64_t requested = o.num_blocks > 0 ? (int64_t)o.num_blocks * o.queries_per_block : INT64_MAX;
   const LaunchPlan lp = launch_plan(ix, ef, o.kernel, std::min<int64_t>(nq, requested));
@@ -1257,6 +1312,7 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
   int32_t* const counters = reinterpret_cast<int32_t*>(base);
   int32_t* const hops = reinterpret_cast<int32_t*>(base + kNoAllocHopsOff);
   int32_t* const evals = reinterpret_cast<int32_t*>(base + kNoAllocEvalsOff);
+  int32_t* const stopped = reinterpret_cast<int32_t*>(base + kNoAllocStoppedOff);
   zero_words(base, kNoAllocHopsOff, ix->stream);  // counters and the 64-bit totals
 
   SearchArgs a = base_args(ix);
@@ -1273,7 +1329,7 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
   a.out_dists = d_dists;
   a.out_found = d_found;
   a.out_hops = hops;
-  a.out_stopped = nullptr;
+  a.out_stopped = stopped;
   a.out_evals = evals;
   a.t_start = nullptr;
   a.t_end = nullptr;
@@ -1293,12 +1349,12 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
   HIP_OK(hipEventRecord(ix->ev1, ix->stream));
   unsigned long long* const totals = reinterpret_cast<unsigned long long*>(base + 64);
   hipLaunchKernelGGL(sum_counts_kernel, dim3((unsigned)std::min<int64_t>((nq + 255) / 256, 1024)), dim3(256), 0,
-                     ix->stream, hops, evals, nq, totals);
+                     ix->stream, hops, evals, stopped, nq, totals);
   HIP_OK(hipGetLastError());
   HIP_OK(hipStreamSynchronize(ix->stream));
   const auto t1 = std::chrono::steady_clock::now();
   int32_t c[4] = {0, 0, 0, 0};
-  unsigned long long tot[2] = {0, 0};
+  unsigned long long tot[3] = {0, 0, 0};
   HIP_OK(hipMemcpy(c, counters, sizeof(c), hipMemcpyDeviceToHost));
   HIP_OK(hipMemcpy(tot, totals, sizeof(tot), hipMemcpyDeviceToHost));
   if (c[1] != nq)
@@ -1316,6 +1372,7 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
     rep->total_hops = (double)tot[0];
     rep->total_evals = (double)tot[1];
     rep->avg_hops = (double)tot[0] / (double)nq;
+    rep->early_stopped = (int32_t)tot[2];
   }
 }
 
@@ -1343,6 +1400,8 @@ void qv_search_opts_default(qv_search_opts* o) {
   o->kernel = QV_KERNEL_AUTO;
   o->step_recall_gt = nullptr;
   o->step_recall_threshold = 0.9f;
+  o->arrival_qps = 0.0;
+  o->arrival_batch = 1;
 }
 
 int qv_index_open(const char* index_dir, const char* data_type, const char* memory_backend,

@@ -34,7 +34,7 @@ QV_ADMIT_STATIC = 2
 QV_GRAPH_HBM = 0
 QV_GRAPH_HOST = 1
 QV_STREAM_READ_BLOCKS = 4096
-QV_NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024 + 256
+QV_NOALLOC_SCRATCH_BYTES = 12 * 1024 * 1024 + 256
 QV_NOALLOC_MAX_QUERIES = 1024 * 1024
 QV_KERNEL_AUTO = 0
 QV_KERNEL_LUT = 1
@@ -88,6 +88,9 @@ class SearchOpts(C.Structure):
         ("step_recall_threshold", C.c_float),
         ("step_recall_step", C.c_void_p),
         ("step_recall_hits", C.c_void_p),
+        ("arrival_qps", C.c_double),
+        ("arrival_batch", C.c_int32),
+        ("reserved0", C.c_int32),
     ]
 
 
@@ -181,6 +184,7 @@ SIGNATURES = {
     "qv_mixture_fill_host": (_I32, [C.POINTER(Mixture), _I64, _I64, _P]),
     "qv_mixture_fill_device": (_I32, [C.POINTER(Mixture), _I64, _I64, _P, C.c_int]),
     "qv_device_count": (_I32, [C.POINTER(_I32)]),
+    "qv_device_mem_info": (_I32, [C.c_int, C.POINTER(_I64), C.POINTER(_I64)]),
     "qv_build_index_gpu": (_I32, [_P, _I32, _I64, _I32, C.POINTER(BuildParams), C.c_int, C.POINTER(_P)]),
     "qv_index_save": (_I32, [_P, C.c_char_p]),
     "qv_index_copy_out": (_I32, [_P, _P, _P, _P, _P, _P]),

@@ -159,3 +159,33 @@ def test_cli_default_slots_fill_the_gpu(small_u8_index, tmp_path):
     a = np.fromfile(tmp_path / "a_ids.bin", dtype="<i4")
     b = np.fromfile(tmp_path / "b_ids.bin", dtype="<i4")
     np.testing.assert_array_equal(a, b)
+
+
+def test_static_batches_without_num_blocks_parses(tmp_path):
+    """--static-batches with --num-blocks unset is accepted by the parser and
+    reaches the index (an ordinary error for a missing one, not a signal)."""
+    r = run("--index-dir", tmp_path / "none", "--query", "q.u8bin", "--data-type", "uint8", "--static-batches")
+    assert r.returncode == 1 and "does not exist" in r.stderr
+
+
+@pytest.mark.gpu
+def test_cli_static_batches_fill_the_gpu(small_u8_index, tmp_path):
+    """--static-batches without --num-blocks: batches of the slots that fill
+    the GPU, reported after the search; ids equal the oracle's."""
+    import qv_oracle as O
+
+    ix = small_u8_index
+    q = ix["queries"][:300]
+    qf = tmp_path / "q.u8bin"
+    qf.write_bytes(struct.pack("<ii", *q.shape) + q.tobytes())
+    print("[gpu] CLI --static-batches without --num-blocks", flush=True)
+    r = run("--index-dir", ix["dir"], "--query", qf, "--data-type", "uint8", "--ef-search", "64", "--repeat", "1",
+            "--pipe-width", "1", "--early-exit-policy", "none", "--static-batches",
+            "--result-prefix", tmp_path / "s")
+    assert r.returncode == 0, r.stderr
+    line = [s for s in r.stdout.splitlines() if s.startswith("[Quiver] StaticBatch:")]
+    assert line and "total 300 queries" in line[0], r.stdout
+    ids = np.fromfile(tmp_path / "s_ids.bin", dtype="<i4")[2:].reshape(300, 10)
+    host = O.HostIndex.from_files(ix["dir"], "uint8")
+    oids, _, _, _ = O.search(host, q.astype(np.float32), 10, 64, early_exit=O.EXIT_NONE)
+    np.testing.assert_array_equal(ids, oids)

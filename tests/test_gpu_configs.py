@@ -75,11 +75,11 @@ def c1():
     L.qv_index_close(h)
 
 
-def _search(c, queries, ef, policy, kernel="auto", pipe=1, num_blocks=0, timeout=0.0):
+def _search(c, queries, ef, policy, kernel="auto", pipe=1, num_blocks=0, timeout=0.0, k=K):
     lib, L = c["lib"], c["L"]
     n = queries.shape[0]
-    ids = np.empty((n, K), np.int32)
-    dists = np.empty((n, K), np.float32)
+    ids = np.empty((n, k), np.int32)
+    dists = np.empty((n, k), np.float32)
     found = np.empty(n, np.int32)
     o = lib.default_search_opts()
     o.early_exit = lib.QV_EXIT_GPRUNING if policy == "gpruning" else lib.QV_EXIT_NONE
@@ -89,7 +89,7 @@ def _search(c, queries, ef, policy, kernel="auto", pipe=1, num_blocks=0, timeout
     o.timeout_s = timeout
     rep = lib.SearchReport()
     q = np.ascontiguousarray(queries, np.float32)
-    rc = L.qv_search(c["h"], q.ctypes.data, n, DIM, K, ef, C.byref(o), ids.ctypes.data, dists.ctypes.data,
+    rc = L.qv_search(c["h"], q.ctypes.data, n, DIM, k, ef, C.byref(o), ids.ctypes.data, dists.ctypes.data,
                      found.ctypes.data, C.byref(rep))
     if rc != 0:
         return rc, None
@@ -98,12 +98,27 @@ def _search(c, queries, ef, policy, kernel="auto", pipe=1, num_blocks=0, timeout
     return rc, (ids, dists, found, hops, rep)
 
 
-def _oracle(c, ef, policy, pipe=1, n=NQ):
-    key = (ef, policy, pipe, n)
+def _oracle(c, ef, policy, pipe=1, n=NQ, k=K):
+    key = (ef, policy, pipe, n, k)
     if key not in c["cache"]:
-        c["cache"][key] = O.search(c["host"], c["q"][:n], K, ef, pipe_width=pipe,
+        c["cache"][key] = O.search(c["host"], c["q"][:n], k, ef, pipe_width=pipe,
                                    early_exit=O.EXIT_GPRUNING if policy == "gpruning" else O.EXIT_NONE)
     return c["cache"][key]
+
+
+class _CodeTable:
+    """The neighbour code table on the C1 handle for the duration of a test."""
+
+    def __init__(self, c):
+        self.c = c
+
+    def __enter__(self):
+        self.c["lib"].check(self.c["L"].qv_index_neighbour_codes(self.c["h"], 1))
+        return self
+
+    def __exit__(self, *exc):
+        self.c["lib"].check(self.c["L"].qv_index_neighbour_codes(self.c["h"], 0))
+        return False
 
 
 def _same(got, want, what):
@@ -245,3 +260,76 @@ def test_c1_static_batches(c1, kernel):
     assert len(batches) == 16
     for bl in batches:
         assert bl.min() == bl.max() > 0  # one wall time per batch
+
+
+@pytest.mark.parametrize("pipe", [1, 2])
+@pytest.mark.parametrize("ef", [32, 288, 416])
+def test_c1_headline_path_with_code_table(c1, pipe, ef):
+    """The path the throughput benchmark times: uint8, R = 64, M = 32, the
+    neighbour code table (2 KB blocks of the 64 neighbours' code rows), the
+    shared-pivot kernel (forced, and picked by `auto` for 2000 queries), pipe
+    widths 1 and 2, both early-exit policies."""
+    with _CodeTable(c1):
+        for kernel in ("shared-pivots", "auto"):
+            for policy in ("none", "gpruning"):
+                _say(f"[gpu] C1 code table kernel={kernel} ef={ef} W={pipe} policy={policy}")
+                rc, got = _search(c1, c1["q"][:NQ], ef, policy, kernel, pipe=pipe)
+                assert rc == 0, c1["lib"].load().qv_last_error()
+                assert got[4].kernel == KERNEL["shared-pivots"]
+                want = _oracle(c1, ef, policy, pipe=pipe)
+                _same(got, want, f"table {kernel} ef={ef} W={pipe} {policy}")
+                assert abs(O.recall(got[0], c1["gt"], K) - O.recall(want[0], c1["gt"], K)) <= 0.002
+
+
+@pytest.mark.parametrize("k", [1, 20, 33, 64])
+def test_c1_topk_matches_oracle(c1, k):
+    """top-k other than 10: k = 1, k = 20 and 33 (the reference's k > 32
+    insert, gpu_primitives.cuh:99-138, has the same first-found-wins order)
+    and k = 64; both kernels, with and without the code table."""
+    n = 1000
+    want = _oracle(c1, 128, "none", n=n, k=k)
+    for table in (False, True):
+        for kernel in ("lut", "shared-pivots"):
+            _say(f"[gpu] C1 topk={k} kernel={kernel} table={table}")
+            if table:
+                with _CodeTable(c1):
+                    rc, got = _search(c1, c1["q"][:n], 128, "none", kernel, k=k)
+            else:
+                rc, got = _search(c1, c1["q"][:n], 128, "none", kernel, k=k)
+            assert rc == 0, c1["lib"].load().qv_last_error()
+            _same(got, want, f"topk={k} {kernel} table={table}")
+
+
+@pytest.mark.parametrize("batch,rate", [(1, 2e5), (16, 1e6), (256, 4e6)])
+def test_c1_open_loop_arrival(c1, batch, rate):
+    """Open-loop arrival into one launch: groups of `batch` queries admitted on
+    a fixed clock (arrival_qps), whatever is in flight.  Answers equal the
+    oracle's; the search lasts at least until the last group's scheduled
+    arrival; every latency is positive."""
+    lib, L = c1["lib"], c1["L"]
+    n = NQ
+    _say(f"[gpu] C1 open loop batch={batch} rate={rate:.0f}")
+    o = lib.default_search_opts()
+    o.early_exit = lib.QV_EXIT_NONE
+    o.arrival_qps = rate
+    o.arrival_batch = batch
+    q = np.ascontiguousarray(c1["q"][:n], np.float32)
+    ids = np.empty((n, K), np.int32)
+    dists = np.empty((n, K), np.float32)
+    found = np.empty(n, np.int32)
+    rep = lib.SearchReport()
+    lib.check(L.qv_search(c1["h"], q.ctypes.data, n, DIM, K, 128, C.byref(o), ids.ctypes.data,
+                          dists.ctypes.data, found.ctypes.data, C.byref(rep)))
+    hops = np.empty(n, np.int32)
+    lib.check(L.qv_last_hops(c1["h"], hops.ctypes.data, n))
+    _same((ids, dists, found, hops), _oracle(c1, 128, "none"), f"open loop batch={batch}")
+    last_arrival = ((n + batch - 1) // batch - 1) * batch / rate
+    assert rep.search_time_s >= last_arrival
+    lat = np.empty(n, np.float64)
+    lib.check(L.qv_last_latencies(c1["h"], lat.ctypes.data, n))
+    assert lat.min() > 0 and rep.lat_p99_ms > 0
+    # the static and batch admissions refuse an arrival rate
+    o.admission = lib.QV_ADMIT_STATIC
+    rc = L.qv_search(c1["h"], q.ctypes.data, 16, DIM, K, 128, C.byref(o), ids.ctypes.data, dists.ctypes.data,
+                     None, None)
+    assert rc == lib.QV_EINVAL and b"open-loop" in L.qv_last_error()

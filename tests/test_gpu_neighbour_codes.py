@@ -100,7 +100,8 @@ def test_float_index_with_neighbour_codes(small_f32_index, kernel):
         L.qv_index_close(h)
 
 
-@pytest.mark.parametrize("dim,R,msg", [(4, 8, "M a multiple of 16"), (16, 128, "R <= 64")])
+@pytest.mark.parametrize("dim,R,msg", [(4, 8, "M = 32 or 48"), (16, 8, "M = 32 or 48"), (64, 8, "M = 32 or 48"),
+                                       (32, 128, "R <= 64")])
 def test_unsupported_shapes_are_refused(tmp_path, dim, R, msg):
     from index_fixtures import exact_pq, write_index
     from quiver import _lib

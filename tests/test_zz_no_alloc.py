@@ -3,9 +3,11 @@ qv_search through the C ABI (runs on the MI355X).
 
 Each case runs qv_search on device buffers with every query admitted at
 launch, then qv_search_noalloc twice in a row -- the full input, then a
-smaller one -- and requires ids, distances, found counts and the hop and
-evaluation totals to equal qv_search's for the same queries (integer and
-index work: bit-exact).  Also: a 600k-point index with 1024 query slots of
+smaller one -- and requires ids, distances, found counts, the hop and
+evaluation totals and the early-exit count to equal qv_search's for the same
+queries (integer and index work: bit-exact), and the device's free memory to
+be the same before and after every call but the process's first (which may
+load the entry's kernels).  Also: a 600k-point index with 1024 query slots of
 either kernel, and the entry's argument limits.
 """
 from __future__ import annotations
@@ -19,6 +21,13 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 K = 10
+_WARM = {"calls": 0}  # noalloc calls made so far in this process
+
+
+def _free_bytes(lib) -> int:
+    free, total = C.c_int64(), C.c_int64()
+    lib.check(lib.load().qv_device_mem_info(0, C.byref(free), C.byref(total)))
+    return free.value
 
 
 def _say(msg: str) -> None:
@@ -72,8 +81,13 @@ def _pair(lib, h, dev, n, ef, kernel, num_blocks=0, policy="none"):
     dev.ids.clear()
     dev.dists.clear()
     dev.found.clear()
+    free0 = _free_bytes(lib)
     lib.check(L.qv_search_noalloc(h, dev.q.ptr, n, dev.dim, K, ef, C.byref(o), dev.ids.ptr, dev.dists.ptr,
                                   dev.found.ptr, C.byref(r1)))
+    free1 = _free_bytes(lib)
+    if _WARM["calls"] > 0:
+        assert free1 == free0, f"device memory changed across a warm qv_search_noalloc: {free0 - free1} bytes"
+    _WARM["calls"] += 1
     return want, dev.fetch(n), r0, r1
 
 
@@ -81,6 +95,7 @@ def _check(want, got, r0, r1, what):
     for a, b, name in zip(want, got, ("ids", "dists", "found")):
         np.testing.assert_array_equal(b, a, err_msg=f"{what}: {name}")
     assert (r1.total_hops, r1.total_evals) == (r0.total_hops, r0.total_evals), what
+    assert r1.early_stopped == r0.early_stopped, what
     assert r1.kernel == r0.kernel, what
 
 
@@ -97,9 +112,13 @@ def test_noalloc_equals_search_u8(lib, small_u8_index, kernel):
     h = _open_small(lib, ix)
     dev = _Dev(lib, ix["queries"].astype(np.float32))
     try:
+        stops = 0
         for n, ef, policy in ((dev.n, 128, "none"), (37, 64, "gpruning")):  # second call smaller
             _say(f"[gpu] noalloc u8 kernel={kernel} n={n} ef={ef} {policy}")
-            _check(*_pair(lib, h, dev, n, ef, kernel, policy=policy), f"u8 {kernel} n={n}")
+            want, got, r0, r1 = _pair(lib, h, dev, n, ef, kernel, policy=policy)
+            _check(want, got, r0, r1, f"u8 {kernel} n={n}")
+            stops += r1.early_stopped
+        assert stops > 0, "gpruning stopped no query: the early-exit count went untested"
     finally:
         lib.load().qv_index_close(h)
 
