@@ -7,11 +7,12 @@ Gaussian mixture (65536 centres uniform in [32, 224], sigma 20, clipped), a
 Vamana graph R=64 / L=100 / alpha=1.2 and PQ 32x256 built on the GPU, 10k
 queries from the same mixture, top-10.  Setup (data, build, ground truth, the
 sweep over ef, early exit and pipe width) is untimed; a step is one search of
-all queries with the queries resident in HBM.  Beside it: the same steps with the queries and
-results in host memory (transfers inside each step), the latency mode
-(open-loop batches of 1, 16 and 256 queries at Recall@10 0.90 and 0.95), the
-PQ-ADC microbenchmark and the CPU oracle on the same index.  Prints one JSON
-line.
+all queries with the queries and results in host memory, the transfers inside
+each step's clock as the reference times a search.  Beside it: the same steps
+with the queries resident in HBM, the latency mode (one search call per batch
+of 1, 16 and 256 queries at Recall@10 0.90 and 0.95), open-loop arrival
+(batches of 1, 16 and 256 offered at fixed rates into one launch), the PQ-ADC
+microbenchmark and the CPU oracle on the same index.  Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -68,6 +69,8 @@ def main() -> int:
                     help="pipe widths the sweep tries with early exit off (the reference's default is 2)")
     ap.add_argument("--latency-batches", default="1,16,256",
                     help="comma-separated batch sizes for the latency leg; empty: off")
+    ap.add_argument("--open-loop-batches", default="1,16,256",
+                    help="arrival batch sizes of the open-loop leg (queries offered at fixed rates); empty: off")
     ap.add_argument("--adc-only", action="store_true",
                     help="run only the ADC microbenchmark leg (prints its JSON object)")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -265,46 +268,58 @@ def main() -> int:
         log(f"calibration copy: {args.copy_mib} MiB read + {args.copy_mib} MiB written")
 
     # ---- warmup + timed steps ------------------------------------------------
+    # A step is one search of all queries with the queries and results in host
+    # memory: the clock of each call starts before the queries are uploaded and
+    # stops once the results are back in host memory, as the reference times a
+    # search (src/quiver/search.cu:865-877, 1121-1129, 1186).
+    h_ids = np.empty((nq, 10), np.int32)
+    h_dists = np.empty((nq, 10), np.float32)
+
+    def run_host(ef: int, policy: int, pipe: int = 1):
+        o = _lib.default_search_opts()
+        o.early_exit = policy
+        o.pipe_width = pipe
+        o.kernel = _lib.KERNEL_NAMES[args.search_kernel]
+        o.admission = _lib.QV_ADMIT_STREAMING
+        rep = _lib.SearchReport()
+        _lib.check(L.qv_search(h, qf.ctypes.data, nq, dim, 10, ef, C.byref(o), h_ids.ctypes.data,
+                               h_dists.ctypes.data, None, C.byref(rep)))
+        return rep
+
     for _ in range(args.warmup):
-        run(ef, policy, pipe)
+        run_host(ef, policy, pipe)
     reps = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        reps.append(run(ef, policy, pipe))
+        reps.append(run_host(ef, policy, pipe))
     t1 = time.perf_counter()
     elapsed = t1 - t0
-    recall = recall_of()
-    timed_ids = d_ids.download(np.int32, (nq, 10))  # the later legs reuse d_ids
-    timed_dists = d_dists.download(np.float32, (nq, 10))
+    timed_ids = h_ids.copy()
+    timed_dists = h_dists.copy()
+    recall = sum(len(set(timed_ids[i]) & set(gt[i])) for i in range(nq)) / (nq * 10.0)
     qps = args.steps * nq / elapsed
     p99 = float(np.median([r.lat_p99_ms for r in reps]))
     p50 = float(np.median([r.lat_p50_ms for r in reps]))
     last = reps[-1]
-    log(f"timed: ef={ef} {pname} W={pipe} steps={args.steps} qps={qps:.0f} recall={recall:.4f} p50={p50:.3f} p99={p99:.3f}")
+    log(f"timed (host buffers): ef={ef} {pname} W={pipe} steps={args.steps} qps={qps:.0f} recall={recall:.4f} "
+        f"p50={p50:.3f} p99={p99:.3f}")
 
-    # the same steps with the queries and results in host memory: the query
-    # upload and the result download fall inside each step, as in the
-    # reference's timing (src/quiver/search.cu:869, 1121-1129)
-    host_steps = max(1, min(args.steps, 10))
-    h_ids = np.empty((nq, 10), np.int32)
-    h_dists = np.empty((nq, 10), np.float32)
-    ho = _lib.default_search_opts()
-    ho.early_exit = policy
-    ho.pipe_width = pipe
-    ho.kernel = _lib.KERNEL_NAMES[args.search_kernel]
-    ho.admission = _lib.QV_ADMIT_STREAMING
-    _lib.check(L.qv_search(h, qf.ctypes.data, nq, dim, 10, ef, C.byref(ho), h_ids.ctypes.data,
-                           h_dists.ctypes.data, None, None))
-    t0h = time.perf_counter()
-    for _ in range(host_steps):
-        _lib.check(L.qv_search(h, qf.ctypes.data, nq, dim, 10, ef, C.byref(ho), h_ids.ctypes.data,
-                               h_dists.ctypes.data, None, None))
-    host_s = time.perf_counter() - t0h
-    host_buffers = {"value": round(host_steps * nq / host_s, 1), "unit": "queries/s", "steps": host_steps,
-                    "ms_per_step": round(host_s / host_steps * 1e3, 3),
-                    "same_results": bool(np.array_equal(h_ids, timed_ids) and np.array_equal(h_dists, timed_dists)),
-                    "note": "queries uploaded from and results copied to host memory inside each step"}
-    log(f"host buffers: {host_buffers['value']:.0f} queries/s ({host_buffers['ms_per_step']} ms per step)")
+    # the same steps with the queries already in HBM and the results left there
+    dev_steps = max(1, min(args.steps, 10))
+    run(ef, policy, pipe)
+    t0d = time.perf_counter()
+    dreps = [run(ef, policy, pipe) for _ in range(dev_steps)]
+    dev_s = time.perf_counter() - t0d
+    device_resident = {"value": round(dev_steps * nq / dev_s, 1), "unit": "queries/s", "steps": dev_steps,
+                       "ms_per_step": round(dev_s / dev_steps * 1e3, 3),
+                       "p50_ms": round(float(np.median([r.lat_p50_ms for r in dreps])), 3),
+                       "p99_ms": round(float(np.median([r.lat_p99_ms for r in dreps])), 3),
+                       "kernel_ms": round(float(np.median([r.kernel_ms for r in dreps])), 3),
+                       "same_results": bool(np.array_equal(d_ids.download(np.int32, (nq, 10)), timed_ids)
+                                            and np.array_equal(d_dists.download(np.float32, (nq, 10)),
+                                                               timed_dists)),
+                       "note": "queries resident in HBM and results left there; no host transfer in a step"}
+    log(f"device-resident: {device_resident['value']:.0f} queries/s ({device_resident['ms_per_step']} ms per step)")
 
     # with a nav graph: the same steps from the medoid, to price the nav search
     medoid_entry = None
@@ -343,12 +358,14 @@ def main() -> int:
                    "ef_search": ef, "early_exit": pname, "pipe_width": pipe, "num_blocks": last.num_blocks,
                    "graph_placement": args.graph_placement, "nav_nodes": int(info.nav_nodes),
                    "neighbour_codes": nbr_codes,
-                   "admission": "streaming (window = num_blocks)", "recall_at_10": round(recall, 4),
+                   "admission": "streaming (window = num_blocks)",
+                   "buffers": "queries and results in host memory; each step's clock includes their transfer",
+                   "recall_at_10": round(recall, 4),
                    "p50_ms": round(p50, 3), "p99_ms": round(p99, 3), "avg_hops": round(last.avg_hops, 2),
                    "build_s": round(build_s, 1),
                    **({"medoid_entry": medoid_entry} if medoid_entry else {})},
         "roofline": roofline,
-        "host_buffers": host_buffers,
+        "device_resident": device_resident,
         "sweep": sweep,
     }
 
@@ -360,6 +377,11 @@ def main() -> int:
         result["latency_mode"] = latency_leg(_lib, L, h, d_q, dim, nq, gt, d_ids, d_dists, lat_points,
                                              [int(b) for b in args.latency_batches.split(",") if b],
                                              _lib.KERNEL_NAMES[args.search_kernel], log)
+    if args.open_loop_batches:
+        result["open_loop"] = open_loop_leg(_lib, L, h, qf, dim, nq, timed_ids, ef, policy, pname, pipe,
+                                            device_resident["value"],
+                                            [int(b) for b in args.open_loop_batches.split(",") if b],
+                                            _lib.KERNEL_NAMES[args.search_kernel], log)
     if at_095 is not None:
         result["config"]["at_recall_0.95"] = {"ef_search": at_095[0], "early_exit": at_095[3],
                                               "pipe_width": at_095[6],
@@ -435,6 +457,61 @@ def latency_leg(_lib, L, h, d_q, dim, nq, gt, d_ids, d_dists, points, batches, k
             log(f"latency R@10>={tag} batch={b:4d} ef={ef} {pname} W={pipe}: qps={row['qps']:.0f} "
                 f"p50={row['p50_ms']:.3f} p99={row['p99_ms']:.3f} recall={row['recall_at_10']:.4f}")
             out.append(row)
+    return out
+
+
+def open_loop_leg(_lib, L, h, qf, dim, nq, ref_ids, ef, policy, pname, pipe, capacity, batches, kernel,
+                  log) -> dict:
+    """Open-loop arrival: queries arrive in groups of B at a fixed offered rate
+    into one persistent launch (the admission word is advanced on the clock,
+    whatever is still in flight), and each query's latency runs from its
+    group's scheduled arrival to the host seeing its completion.  The 10k
+    queries are offered thirty times over (300k arrivals, device-resident) at
+    fractions of the device-resident closed-loop rate, past it until the
+    backlog of a rate above what the launch sustains lifts P99 over 10 ms
+    (one launch has no per-batch drain, so it sustains more than the
+    closed loop's rate); reported per point: offered and
+    achieved QPS, P50/P99, the kernel `auto` took, and whether every answer
+    equals the closed-loop one.  Per batch size: the highest offered rate
+    whose P99 is at most 10 ms."""
+    reps_q = 30
+    n = nq * reps_q
+    q10 = np.ascontiguousarray(np.tile(qf, (reps_q, 1)), np.float32)
+    d_q10 = _lib.DeviceBuffer(q10.nbytes).upload(q10)
+    d_i10 = _lib.DeviceBuffer(n * 40)
+    d_d10 = _lib.DeviceBuffer(n * 40)
+    want = np.tile(ref_ids, (reps_q, 1))
+    fracs = (0.1, 0.25, 0.5, 0.75, 1.0, 1.1, 1.2, 1.3, 1.35, 1.4, 1.45, 1.5, 1.6)
+    out = {"ef_search": ef, "early_exit": pname, "pipe_width": pipe, "arrivals": n,
+           "closed_loop_qps": round(capacity, 1), "points": [], "max_offered_qps_p99_le_10ms": {}}
+    for b in batches:
+        best = None
+        for f in fracs:
+            rate = f * capacity
+            o = _lib.default_search_opts()
+            o.early_exit = policy
+            o.pipe_width = pipe
+            o.kernel = kernel
+            o.device_buffers = 1
+            o.admission = _lib.QV_ADMIT_STREAMING
+            o.arrival_qps = rate
+            o.arrival_batch = b
+            rep = _lib.SearchReport()
+            _lib.check(L.qv_search(h, d_q10.ptr, n, dim, 10, ef, C.byref(o), d_i10.ptr, d_d10.ptr, None,
+                                   C.byref(rep)))
+            same = bool(np.array_equal(d_i10.download(np.int32, (n, 10)), want))
+            row = {"batch": b, "offered_qps": round(rate, 1), "achieved_qps": round(rep.qps, 1),
+                   "p50_ms": round(rep.lat_p50_ms, 3), "p99_ms": round(rep.lat_p99_ms, 3),
+                   "kernel": "shared-pivots" if rep.kernel == _lib.QV_KERNEL_SHARED_PIVOTS else "lut",
+                   "ids_identical_to_closed_loop": same}
+            out["points"].append(row)
+            log(f"open loop batch={b:4d} offered={rate:10.0f} achieved={rep.qps:10.0f} p50={rep.lat_p50_ms:.3f} "
+                f"p99={rep.lat_p99_ms:.3f} kernel={row['kernel']} same={same}")
+            if rep.lat_p99_ms <= 10.0 and (best is None or rate > best["offered_qps"]):
+                best = row
+        out["max_offered_qps_p99_le_10ms"][str(b)] = best
+    for buf in (d_q10, d_i10, d_d10):
+        buf.close()
     return out
 
 

@@ -48,6 +48,8 @@ struct qv_index {
   uint64_t* d_tstart = nullptr;
   uint64_t* d_tend = nullptr;
   int32_t* d_counters = nullptr;
+  uint64_t* d_feed_mirror = nullptr;  // device copies of the feed word (search kernels' feed wait)
+  uint32_t feed_epoch = 0;            // epoch of the last search that used them
   int32_t* h_ctrl = nullptr;   // [0] feed_count, [1] terminate (host-coherent)
   int32_t* h_ring = nullptr;   // [cap_q] completion ring (host-coherent)
   int32_t* h_stage = nullptr;  // pinned: counters[4], hops, stopped, evals [cap_q each]

@@ -315,6 +315,12 @@ static void ensure_scratch(qv_index* ix, int64_t nq, int k) {
     HIP_OK(hipMalloc(&ix->d_counters, 64));
     HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_ctrl), 64, hipHostMallocCoherent));
   }
+  if (!ix->d_feed_mirror) {
+    HIP_OK(hipMalloc(&ix->d_feed_mirror, kFeedMirrorBytes));
+    HIP_OK(hipMemset(ix->d_feed_mirror, 0, kFeedMirrorBytes));
+    HIP_OK(hipDeviceSynchronize());
+    ix->feed_epoch = 0;
+  }
   if (nq <= ix->cap_q && k <= ix->cap_k) return;
   free_scratch(ix);
   const int64_t cq = std::max<int64_t>(nq, 1024);
@@ -344,6 +350,7 @@ void release_index(qv_index* ix) {
   hipSetDevice(ix->device);
   free_scratch(ix);
   hipFree(ix->d_counters);
+  hipFree(ix->d_feed_mirror);
   hipHostFree(ix->h_ctrl);
   hipFree(ix->d_nav_data);
   hipFree(ix->d_nav_graph);
@@ -926,9 +933,9 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   ensure_scratch(ix, nq, topk);
   const int64_t requested = o.num_blocks > 0 ? (int64_t)o.num_blocks * o.queries_per_block : INT64_MAX;
   // Queries the call can have in flight.  Open loop: by Little's law, the
-  // offered rate times a nominal 2 ms in the system, plus one arrival.
+  // offered rate times a nominal 1.5 ms in the system, plus one arrival.
   int64_t need = std::min<int64_t>(nq, requested);
-  if (open_loop) need = std::min<int64_t>(need, (int64_t)std::ceil(o.arrival_qps * 2e-3) + o.arrival_batch);
+  if (open_loop) need = std::min<int64_t>(need, (int64_t)std::ceil(o.arrival_qps * 1.5e-3) + o.arrival_batch);
   const LaunchPlan lp = launch_plan(ix, ef, o.kernel, need);
   const int spc = lp.slots_per_cu;
   if (spc <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
@@ -1003,6 +1010,14 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   a.feed_count = dev_ctrl;
   a.terminate = dev_ctrl + 1;
   a.ring = dev_ring;
+  // A new epoch per search makes the mirror words of earlier searches read as
+  // 0 without a clear; at the end of the epochs the words are cleared once.
+  if (ix->feed_epoch == UINT32_MAX) {
+    HIP_OK(hipMemsetAsync(ix->d_feed_mirror, 0, kFeedMirrorBytes, ix->stream));
+    ix->feed_epoch = 0;
+  }
+  a.feed_mirror = ix->d_feed_mirror;
+  a.feed_epoch = ++ix->feed_epoch;
   // Feed waits end on their own after this long even if the host never
   // admits more work, so a lost host thread cannot leave the kernel spinning
   // (open loop: the arrivals' own span on top).

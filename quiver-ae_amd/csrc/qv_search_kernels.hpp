@@ -58,6 +58,8 @@ struct SearchArgs {
   const int32_t* terminate;        // host-coherent, may be null
   int32_t* ring;                   // host-coherent completion ring, may be null
   uint64_t spin_limit_ticks;       // watchdog on feed waits (100 MHz ticks)
+  uint64_t* feed_mirror;           // kFeedLines words, kFeedStride apart: (epoch << 32) | feed
+  uint32_t feed_epoch;             // this search's epoch (a word of another epoch reads as 0)
   // navigation graph for the per-query entry node (nav_data null: the medoid)
   const uint8_t* nav_data;
   const int32_t* nav_graph;
@@ -84,6 +86,13 @@ struct SearchArgs {
 };
 
 enum : int32_t { kErrSpinTimeout = 1 };
+
+// Device copies of the host's feed word: one 8-byte word per line, the lines
+// 4352 bytes apart so that the waiting waves' reads spread over many memory
+// channels instead of queueing at one.
+constexpr int kFeedLines = 64;
+constexpr int64_t kFeedStride = 4352 / 8;  // in 8-byte words
+constexpr int64_t kFeedMirrorBytes = kFeedLines * kFeedStride * 8;
 
 // Dynamic LDS carve-up of one query (one wave), shared by the kernel and its
 // launcher.  Q = beam positions per lane: the register beam holds Q * 64 >= ef
@@ -680,9 +689,33 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
                  __hip_atomic_load(a.terminate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
         qid = -1;
       } else if (a.feed_count) {
+        // Only the wave holding the lowest unadmitted ticket reads the host's
+        // feed word; it publishes what it reads in the device mirror lines
+        // that every other waiting wave watches (each wave its own line).
+        // Thousands of waves reading host memory, or one device word, at once
+        // would crowd the fabric the running queries' loads go through.  Every
+        // access is relaxed: the queries are in HBM before the launch, so the
+        // feed word orders nothing, and an acquire or release at agent or
+        // system scope would invalidate or write back the L2 on each poll.
+        const int64_t line = ((int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave) & (kFeedLines - 1);
+        uint64_t* const mine = a.feed_mirror + line * kFeedStride;
         const uint64_t t0 = wall_ticks();
-        while (qid >= __hip_atomic_load(a.feed_count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM)) {
-          if (a.terminate &&
+        for (uint32_t nap = 0;; nap++) {
+          const uint64_t mv = __hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const int32_t seen = (uint32_t)(mv >> 32) == a.feed_epoch ? (int32_t)(uint32_t)mv : 0;
+          if (qid < seen) break;
+          const bool poller = qid == seen;
+          if (poller) {
+            const int32_t fed = __hip_atomic_load(a.feed_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (qid < fed) {
+              const uint64_t v = ((uint64_t)a.feed_epoch << 32) | (uint32_t)fed;
+              for (int l = 0; l < kFeedLines; l++)
+                __hip_atomic_fetch_max(a.feed_mirror + l * kFeedStride, v, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+              break;
+            }
+          }
+          if ((poller || (nap & 63) == 63) && a.terminate &&
               __hip_atomic_load(a.terminate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
             qid = -1;
             break;
@@ -692,7 +725,10 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
             qid = -1;
             break;
           }
-          __builtin_amdgcn_s_sleep(4);
+          if (poller)
+            __builtin_amdgcn_s_sleep(4);
+          else
+            __builtin_amdgcn_s_sleep(32);
         }
       }
     }
@@ -899,8 +935,10 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       if (a.t_end) a.t_end[qid] = wall_ticks();
       atomicAdd(&a.counters[1], 1);
       if (a.ring) {
+        // relaxed: the host takes the entry as the query's completion time
+        // only; it reads the results once the launch has ended
         const int32_t pos = atomicAdd(&a.counters[3], 1);
-        __hip_atomic_store(&a.ring[pos], qid + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(&a.ring[pos], qid + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       }
     }
     query_sync<SC>();
