@@ -337,11 +337,12 @@ def main() -> int:
     alg_bytes = (last.total_hops * info.node_size + last.total_evals * (info.num_chunks + 4)
                  + nq * (info.num_chunks * 256 * 4 + dim * 4 + 10 * 8))
     achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
+    traffic, traffic_pipe = measured_traffic(args.workload, ef, pname,
+                                             kname + (" neighbour-codes" if nbr_codes else ""), pipe, log)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic(args.workload, ef, pname,
-                                              kname + (" neighbour-codes" if nbr_codes else "")
-                                              + (f" pipe={pipe}" if pipe != 1 else ""), log),
+                "traffic": traffic,
+                "traffic_pipe_width": traffic_pipe,
                 "kernel": kname, "kernel_ms": round(kernel_ms, 3),
                 "bytes_per_launch": int(alg_bytes),
                 "bytes_per_launch_without_lut": int(alg_bytes - nq * info.num_chunks * 256 * 4),
@@ -515,19 +516,37 @@ def open_loop_leg(_lib, L, h, qf, dim, nq, ref_ids, ef, policy, pname, pipe, cap
     return out
 
 
-def measured_traffic(workload: str, ef: int, policy: str, kernel: str, log):
+def measured_traffic(workload: str, ef: int, policy: str, kernel: str, pipe: int, log):
     """HBM bytes per search-kernel launch for this configuration and kernel, as
     measured by the FETCH_SIZE and WRITE_SIZE counter runs summarised under
-    profiles/ (scaled by a copy kernel of known size); None when not measured."""
-    key = f"traffic_bytes_per_launch[{workload} ef={ef} {policy} {kernel}]"
+    profiles/ (scaled by a copy kernel of known size), and the pipe width it
+    was measured at: this one's if measured, else another's (the same nodes
+    and code blocks are read whatever the pipe width); (None, None) when not
+    measured."""
+    base = f"traffic_bytes_per_launch[{workload} ef={ef} {policy} {kernel}"
+    found = {}
     for f in sorted((Path(__file__).resolve().parent / "profiles").glob("*.md")):
         for line in f.read_text().splitlines():
-            if line.strip().startswith(key):
-                try:
-                    return int(line.split("=")[-1].strip().replace(",", ""))
-                except ValueError:
-                    log(f"unreadable traffic line in {f.name}: {line}")
-    return None
+            t = line.strip()
+            if not t.startswith(base):
+                continue
+            rest = t[len(base):]
+            if rest.startswith("]"):
+                w = 1
+            elif rest.startswith(" pipe=") and "]" in rest:
+                w = int(rest[len(" pipe="):rest.index("]")])
+            else:
+                continue
+            try:
+                found[w] = int(t.split("=")[-1].strip().replace(",", ""))
+            except ValueError:
+                log(f"unreadable traffic line in {f.name}: {line}")
+    if pipe in found:
+        return found[pipe], pipe
+    if found:
+        w = min(found)
+        return found[w], w
+    return None, None
 
 
 def adc_leg(_lib, L, ncodes: int, log) -> dict:
@@ -592,6 +611,7 @@ def adc_leg(_lib, L, ncodes: int, log) -> dict:
         log(f"random {wb:3d}-byte rows: {wms:.3f} ms, {evals / wms / 1e6:.1f} G rows/s, "
             f"{evals * wb / wms / 1e6:.0f} GB/s")
     fold.close()
+    matrix = access_matrix(_lib, L, codes, ncodes, M, ids, evals, log)
     rate32 = widths[32]["rows_per_s"]
     # the widest row read at (within 15 % of) the 32-byte row rate: what one
     # random 32-byte row occupies of the memory system
@@ -623,7 +643,47 @@ def adc_leg(_lib, L, ncodes: int, log) -> dict:
             "physical_bytes_per_launch": int(phys), "physical_gbs": round(phys_gbs, 1),
             "physical_frac": round(phys_gbs / HBM_PEAK_GBS, 4),
             "random_read_peak_gbs": random_peak,
+            "access_matrix": matrix,
             "physical_frac_of_random_read_peak": round(phys_gbs / random_peak, 4)}
+
+
+def access_matrix(_lib, L, codes, ncodes, M, ids, n, log) -> dict:
+    """The random row gather's rate over its shape: tables of 32 MB, 3.2 GB and
+    32 GB (prefixes of the code table), rows of 32-256 bytes, nontemporal or
+    default loads, 1, 2 or 4 rows in flight per lane group and 8, 16 or 32
+    waves per CU (the last two swept for 32-byte rows only).  The same n
+    uniform ids each time (mapped onto the table's rows); rows/s per cell,
+    the median of two timed launches after one untimed."""
+    fold = _lib.DeviceBuffer(4)
+    cells = []
+    for table in (32_000_000, 3_200_000_000, 32_000_000_000):
+        table = min(table, ncodes * M)
+        for row in (32, 64, 128, 256):
+            shapes = [(p, w) for p in (1, 2, 4) for w in (8, 16, 32)] if row == 32 else [(1, 32)]
+            for nt in (1, 0):
+                for per, waves in shapes:
+                    ts = []
+                    launched = C.c_int32()
+                    for _ in range(3):
+                        ms = C.c_float()
+                        _lib.check(L.qv_gather_sweep_bench(codes.ptr, table // row, row, ids.ptr, n, ncodes, per,
+                                                           waves, nt, fold.ptr, 0, C.byref(ms), C.byref(launched)))
+                        ts.append(ms.value)
+                    t = float(np.median(ts[1:]))
+                    cells.append({"table_bytes": table, "row_bytes": row, "nontemporal": bool(nt),
+                                  "rows_in_flight": per, "waves_per_cu": waves, "waves": launched.value,
+                                  "ms": round(t, 4), "rows_per_s": round(n / (t * 1e-3), 1),
+                                  "gb_per_s": round(n * row / (t * 1e-3) / 1e9, 1)})
+    fold.close()
+    best = max((c for c in cells if c["row_bytes"] == 32), key=lambda c: c["rows_per_s"])
+    log(f"access matrix: {len(cells)} cells; best 32-byte cell {best['rows_per_s'] / 1e9:.1f} G rows/s "
+        f"(table {best['table_bytes'] / 1e9:g} GB, nt={best['nontemporal']}, {best['rows_in_flight']} in flight, "
+        f"{best['waves_per_cu']} waves/CU)")
+    for c in cells:
+        log(f"  table={c['table_bytes'] / 1e9:7.3f} GB row={c['row_bytes']:3d} nt={int(c['nontemporal'])} "
+            f"per={c['rows_in_flight']} waves={c['waves_per_cu']:2d}: {c['rows_per_s'] / 1e9:6.1f} G rows/s "
+            f"{c['gb_per_s']:7.0f} GB/s")
+    return {"cells": cells, "best_32b": best}
 
 
 def cpu_leg(_lib, L, h, info, qf, ef, policy, pname, pipe, gpu_ids_all, gpu_dists_all, nq,

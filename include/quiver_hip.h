@@ -359,6 +359,24 @@ int qv_gather_rows_bench(const uint8_t* d_table, int64_t table_bytes, int32_t ro
                          const int32_t* d_ids, int64_t n, int32_t id_shift, uint32_t* d_fold,
                          int device, float* elapsed_ms);
 
+/* The random row gather in a configurable shape, for the access-rate matrix
+ * (no reference counterpart; a measurement aid): rows of row_bytes (32, 64,
+ * 128 or 256) from a table of table_rows rows, row i = (d_ids[i] * row_mul)
+ * >> 32 with row_mul = floor(table_rows * 2^32 / id_range), clamped to the
+ * last row (ids uniform over [0, id_range) land uniformly in the table;
+ * table_rows < 2^32, id_range <= 2^32); rows_in_flight (1, 2 or 4) rows
+ * requested per group of row_bytes / 16 lanes before any is used;
+ * waves_per_cu (8, 16 or 32) resident waves per CU (a persistent grid sized
+ * through its LDS); nontemporal != 0 for nontemporal loads.  The XOR of every
+ * 32-bit word read goes into d_fold[0] (XORed in: clear it first).
+ * elapsed_ms and waves_launched (may be NULL) receive the kernel time and the
+ * waves launched. */
+int qv_gather_sweep_bench(const uint8_t* d_table, int64_t table_rows, int32_t row_bytes,
+                          const int32_t* d_ids, int64_t n, int64_t id_range,
+                          int32_t rows_in_flight, int32_t waves_per_cu, int32_t nontemporal,
+                          uint32_t* d_fold, int device, float* elapsed_ms,
+                          int32_t* waves_launched);
+
 /* Sequential read of nbytes (a multiple of 16, 16-byte aligned) from d_src,
  * XOR-folded into d_fold[min(QV_STREAM_READ_BLOCKS, ceil(nbytes / 4096))] (no
  * reference counterpart; a measurement aid): the device's streaming read

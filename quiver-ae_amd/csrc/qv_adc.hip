@@ -10,6 +10,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "qv_common.hpp"
 #include "qv_device.hpp"
@@ -289,6 +290,39 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const uint8_t* __restr
 // Streaming read of nwords 16-byte words (grid-stride, four loads in flight
 // per thread), XOR-folded into one word per workgroup: the device's sequential
 // read bandwidth, the measured counterpart of the nominal HBM peak.
+// Random row gather of a configurable shape, for the access-rate matrix: rows
+// of ROW bytes (ROW / 16 lanes per row, 16 bytes each), PER rows requested per
+// lane group before any is used, nontemporal (NT) or default loads.  Row id i
+// is (ids[i] * row_mul) >> 32: ids uniform over [0, id_range) land uniformly
+// in the table's rows when row_mul = floor(rows * 2^32 / id_range).  The grid
+// is persistent (as many workgroups as are resident); each wave XOR-folds
+// what it read into fold[0].
+template <int ROW, int PER, bool NT>
+__global__ __launch_bounds__(256) void gather_sweep_kernel(const uint8_t* __restrict__ table, uint64_t row_mul,
+                                                           uint64_t last_row, const int32_t* __restrict__ ids,
+                                                           int64_t n, uint32_t* __restrict__ fold) {
+  constexpr int kLanes = ROW / 16;
+  constexpr int kGroups = 256 / kLanes;  // rows per workgroup per request round
+  const int g = (int)threadIdx.x / kLanes, part = (int)threadIdx.x % kLanes;
+  const int64_t rounds_stride = (int64_t)gridDim.x * kGroups;
+  uint32_t x = 0;
+  for (int64_t base = (int64_t)blockIdx.x * kGroups + g; base < n; base += rounds_stride * PER) {
+    u32x4 v[PER];
+#pragma unroll
+    for (int p = 0; p < PER; p++) {
+      const int64_t i = min(base + p * rounds_stride, n - 1);
+      const uint64_t row = min(((uint64_t)(uint32_t)ids[i] * row_mul) >> 32, last_row);
+      const u32x4* ptr = reinterpret_cast<const u32x4*>(table + row * ROW) + part;
+      v[p] = NT ? __builtin_nontemporal_load(ptr) : *ptr;
+    }
+#pragma unroll
+    for (int p = 0; p < PER; p++)
+      if (base + p * rounds_stride < n) x ^= v[p][0] ^ v[p][1] ^ v[p][2] ^ v[p][3];
+  }
+  for (int off = 32; off > 0; off >>= 1) x ^= (uint32_t)__shfl_xor((int)x, off);
+  if ((threadIdx.x & 63) == 0) atomicXor(fold, x);
+}
+
 __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ src, int64_t nwords,
                                                           uint32_t* __restrict__ fold) {
   __shared__ uint32_t part[4];
@@ -449,6 +483,73 @@ int qv_gather_bench(const uint8_t* d_rows, int64_t num_rows, const int32_t* d_id
     HIP_OK(hipEventCreate(&e1));
     HIP_OK(hipEventRecord(e0, 0));
     hipLaunchKernelGGL(gather_kernel, dim3((unsigned)blocks), dim3(256), 0, 0, d_rows, num_rows - 1, d_ids, n, d_fold);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipEventRecord(e1, 0));
+    HIP_OK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (elapsed_ms) *elapsed_ms = ms;
+  });
+}
+
+int qv_gather_sweep_bench(const uint8_t* d_table, int64_t table_rows, int32_t row_bytes, const int32_t* d_ids,
+                          int64_t n, int64_t id_range, int32_t rows_in_flight, int32_t waves_per_cu,
+                          int32_t nontemporal, uint32_t* d_fold, int device, float* elapsed_ms,
+                          int32_t* waves_launched) {
+  return qv::guard([&] {
+    if (!d_table || !d_ids || !d_fold || n <= 0 || n > ((int64_t)1 << 34) || table_rows < 1 ||
+        table_rows >= ((int64_t)1 << 32) || id_range < 1 || id_range > ((int64_t)1 << 32))
+      qv::fail(QV_EINVAL, "bad argument");
+    if (row_bytes != 32 && row_bytes != 64 && row_bytes != 128 && row_bytes != 256)
+      qv::fail(QV_EINVAL, "row_bytes must be 32, 64, 128 or 256");
+    if (rows_in_flight != 1 && rows_in_flight != 2 && rows_in_flight != 4)
+      qv::fail(QV_EINVAL, "rows_in_flight must be 1, 2 or 4");
+    if (waves_per_cu != 8 && waves_per_cu != 16 && waves_per_cu != 32)
+      qv::fail(QV_EINVAL, "waves_per_cu must be 8, 16 or 32");
+    if ((reinterpret_cast<uintptr_t>(d_table) & 15) != 0) qv::fail(QV_EINVAL, "table must be 16-byte aligned");
+    // row = (id * row_mul) >> 32 < table_rows for every id < id_range
+    const uint64_t row_mul = (uint64_t)(((unsigned __int128)table_rows << 32) / (unsigned __int128)id_range);
+    if (row_mul == 0) qv::fail(QV_EINVAL, "table has fewer rows than the id range can spread over");
+    HIP_OK(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    HIP_OK(hipGetDeviceProperties(&prop, device));
+    int lds_cu = 0;
+    HIP_OK(hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, device));
+    // waves per CU set through LDS: four-wave workgroups, waves_per_cu / 4 of
+    // them fit a CU's LDS
+    const int wgs = waves_per_cu / 4;
+    const size_t lds = (size_t)(lds_cu / wgs) & ~(size_t)255;
+    using Kern = void (*)(const uint8_t*, uint64_t, uint64_t, const int32_t*, int64_t, uint32_t*);
+    Kern kern = nullptr;
+    auto pick = [&](auto rowc, auto perc) {
+      constexpr int R = decltype(rowc)::value, P = decltype(perc)::value;
+      kern = nontemporal ? gather_sweep_kernel<R, P, true> : gather_sweep_kernel<R, P, false>;
+    };
+    auto by_per = [&](auto rowc) {
+      if (rows_in_flight == 1) pick(rowc, std::integral_constant<int, 1>{});
+      else if (rows_in_flight == 2) pick(rowc, std::integral_constant<int, 2>{});
+      else pick(rowc, std::integral_constant<int, 4>{});
+    };
+    if (row_bytes == 32) by_per(std::integral_constant<int, 32>{});
+    else if (row_bytes == 64) by_per(std::integral_constant<int, 64>{});
+    else if (row_bytes == 128) by_per(std::integral_constant<int, 128>{});
+    else by_per(std::integral_constant<int, 256>{});
+    HIP_OK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)lds));
+    int per_cu = 0;
+    HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kern), 256, lds));
+    if (per_cu < 1) qv::fail(QV_EHIP, "gather sweep kernel does not fit on a compute unit");
+    per_cu = std::min(per_cu, wgs);
+    const int grid = per_cu * prop.multiProcessorCount;
+    if (waves_launched) *waves_launched = grid * 4;
+    hipEvent_t e0, e1;
+    HIP_OK(hipEventCreate(&e0));
+    HIP_OK(hipEventCreate(&e1));
+    HIP_OK(hipEventRecord(e0, 0));
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, 0, d_table, row_mul, (uint64_t)(table_rows - 1), d_ids, n,
+                       d_fold);
     HIP_OK(hipGetLastError());
     HIP_OK(hipEventRecord(e1, 0));
     HIP_OK(hipEventSynchronize(e1));

@@ -581,14 +581,18 @@ __global__ __launch_bounds__(64) void reverse_insert_kernel(GLayout L, const uin
     uint32_t* nb = reinterpret_cast<uint32_t*>(node_rec(L, t) + L.data_size);
     const int cdeg = (int)nb[0];
     const int pc = pcnt[t];
-    const uint32_t mine = lane < cdeg ? nb[1 + lane] : ~0u;
+    // the list, two slots per lane (R <= 128), and the pending edges (P <= 64)
+    const uint32_t mine0 = lane < cdeg ? nb[1 + lane] : ~0u;
+    const uint32_t mine1 = lane + kWave < cdeg ? nb[1 + kWave + lane] : ~0u;
     const uint32_t pmine = lane < pc ? pend[(int64_t)t * P + lane] : ~0u;
+    const int c0 = min(cdeg, kWave);
     // new sources, counted over the whole run, 64 pairs at a time
     auto fresh = [&](int64_t q, uint32_t& src) -> bool {
       if (q >= npairs || (uint32_t)(pairs[q] >> 32) != t) return false;
       src = (uint32_t)pairs[q];
       bool dup = false;
-      for (int k = 0; k < cdeg; k++) dup |= src == (uint32_t)__builtin_amdgcn_readlane((int)mine, k);
+      for (int k = 0; k < c0; k++) dup |= src == (uint32_t)__builtin_amdgcn_readlane((int)mine0, k);
+      for (int k = kWave; k < cdeg; k++) dup |= src == (uint32_t)__builtin_amdgcn_readlane((int)mine1, k - kWave);
       for (int k = 0; k < pc; k++) dup |= src == (uint32_t)__builtin_amdgcn_readlane((int)pmine, k);
       return !dup;
     };
@@ -1352,7 +1356,7 @@ int qv_build_index_gpu(const void* d_base, int32_t data_type, int64_t n, int32_t
     qv_build_params p;
     qv_build_params_default(&p);
     if (params) p = *params;
-    if (p.R <= 0 || p.R > kMaxBuildDegree) qv::fail(QV_EINVAL, "R must be in [1, 64]");
+    if (p.R <= 0 || p.R > kMaxBuildDegree) qv::fail(QV_EINVAL, "R must be in [1, 128]");
     if (p.L < p.R) qv::fail(QV_EINVAL, "L must be >= R");
     HIP_OK(hipSetDevice(device));
     if (data_type == QV_UINT8)

@@ -14,7 +14,7 @@ namespace qv {
 constexpr int64_t kPageSize = 4096;   // shared::PAGE_SIZE (src/shared/io/loader.hpp:25)
 constexpr int kNumPivots = 256;       // PQSearchData::num_pivots (pq_search.hpp:14)
 constexpr int kMaxDegree = 128;       // two neighbour slots per wavefront lane
-constexpr int kMaxBuildDegree = 64;   // the GPU builder's prune: one lane per edge
+constexpr int kMaxBuildDegree = 128;  // the GPU builder: a list in two slots per lane
 constexpr int kMaxEf = 1024;          // 16 beam positions per lane
 constexpr int kMaxTopk = 64;          // one top-k entry per lane
 constexpr int kMaxPipeWidth = 16;     // bin/common/cli_validation.hpp:9

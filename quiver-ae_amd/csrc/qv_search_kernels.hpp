@@ -90,7 +90,7 @@ enum : int32_t { kErrSpinTimeout = 1 };
 // Device copies of the host's feed word: one 8-byte word per line, the lines
 // 4352 bytes apart so that the waiting waves' reads spread over many memory
 // channels instead of queueing at one.
-constexpr int kFeedLines = 64;
+constexpr int kFeedLines = 64;  // one per lane of the publishing wave
 constexpr int64_t kFeedStride = 4352 / 8;  // in 8-byte words
 constexpr int64_t kFeedMirrorBytes = kFeedLines * kFeedStride * 8;
 
@@ -681,6 +681,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
   while (true) {
     // ---- acquire (StreamingDispatch, src/quiver/kernel_core/policies/dispatch.cuh:39-79)
     int32_t qid = -1;
+    uint64_t pub = 0;  // the poller's new mirror value, published by the whole wave below
     if (lane == 0) {
       qid = atomicAdd(&a.counters[0], 1);
       if (qid >= a.nq) {
@@ -691,14 +692,15 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       } else if (a.feed_count) {
         // Only the wave holding the lowest unadmitted ticket reads the host's
         // feed word; it publishes what it reads in the device mirror lines
-        // that every other waiting wave watches (each wave its own line).
+        // that every other waiting wave watches (each ticket its own line;
+        // addresses from the ticket, never loop-invariant values the compiler
+        // would keep in registers through the hops).
         // Thousands of waves reading host memory, or one device word, at once
         // would crowd the fabric the running queries' loads go through.  Every
         // access is relaxed: the queries are in HBM before the launch, so the
         // feed word orders nothing, and an acquire or release at agent or
         // system scope would invalidate or write back the L2 on each poll.
-        const int64_t line = ((int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave) & (kFeedLines - 1);
-        uint64_t* const mine = a.feed_mirror + line * kFeedStride;
+        uint64_t* const mine = a.feed_mirror + (int64_t)(qid & (kFeedLines - 1)) * kFeedStride;
         const uint64_t t0 = wall_ticks();
         for (uint32_t nap = 0;; nap++) {
           const uint64_t mv = __hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -708,10 +710,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
           if (poller) {
             const int32_t fed = __hip_atomic_load(a.feed_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             if (qid < fed) {
-              const uint64_t v = ((uint64_t)a.feed_epoch << 32) | (uint32_t)fed;
-              for (int l = 0; l < kFeedLines; l++)
-                __hip_atomic_fetch_max(a.feed_mirror + l * kFeedStride, v, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+              pub = ((uint64_t)a.feed_epoch << 32) | (uint32_t)fed;
               break;
             }
           }
@@ -733,6 +732,11 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       }
     }
     qid = read_lane_i32(qid, 0);
+    // one mirror line per lane (kFeedLines == kWave), one instruction
+    pub = read_lane_u64(pub, 0);
+    if (pub != 0)
+      __hip_atomic_fetch_max(a.feed_mirror + (int64_t)opaque_lane() * kFeedStride, pub, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
     if (qid < 0) break;
     // Later tickets issue first: the last-admitted queries set the end of the
     // launch, the earlier ones have time to spare.

@@ -184,6 +184,8 @@ SIGNATURES = {
     "qv_mixture_fill_host": (_I32, [C.POINTER(Mixture), _I64, _I64, _P]),
     "qv_mixture_fill_device": (_I32, [C.POINTER(Mixture), _I64, _I64, _P, C.c_int]),
     "qv_device_count": (_I32, [C.POINTER(_I32)]),
+    "qv_gather_sweep_bench": (_I32, [_P, _I64, _I32, _P, _I64, _I64, _I32, _I32, _I32, _P, C.c_int,
+                                     C.POINTER(C.c_float), C.POINTER(_I32)]),
     "qv_device_mem_info": (_I32, [C.c_int, C.POINTER(_I64), C.POINTER(_I64)]),
     "qv_build_index_gpu": (_I32, [_P, _I32, _I64, _I32, C.POINTER(BuildParams), C.c_int, C.POINTER(_P)]),
     "qv_index_save": (_I32, [_P, C.c_char_p]),

@@ -237,7 +237,7 @@ class IndexQuiver:
     ``search_kernel`` ("auto", "lut" or "shared-pivots") and
     ``neighbour_codes`` (store each node's neighbours' PQ code rows as one
     block in device memory, n * R * M bytes: the same results with fewer
-    bytes read per hop; indexes with R <= 64 and M a multiple of 16).
+    bytes read per hop; indexes with R <= 64 and M = 32 or 48).
     ``num_blocks`` left unset fills the GPU with concurrent query slots (an
     external ``binary`` gets the reference's 756); a number given is the slot
     count, as in the reference.  Results do not depend on it.

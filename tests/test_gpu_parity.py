@@ -418,3 +418,32 @@ def test_mixture_device_matches_host(lib):
         _lib.check(_lib.load().qv_mixture_fill_device(C.byref(m), 12345, 3000, buf.ptr, 0))
         dev = buf.download(host.dtype, host.shape)
         np.testing.assert_array_equal(dev, host)
+
+
+@pytest.mark.parametrize("row", [32, 64, 128, 256])
+def test_gather_sweep_fold(lib, row):
+    """The access-rate matrix's gather: every shape reads exactly the rows its
+    ids map to (the XOR of all words read, against numpy)."""
+    from quiver import _lib
+
+    _say(f"[gpu] gather sweep fold row={row}")
+    rng = np.random.default_rng(row)
+    nrows, n, id_range = 3001, 64 * 500 + 29, 1_000_000
+    table = rng.integers(0, 2**32, (nrows, row // 4), dtype=np.uint32)
+    ids = rng.integers(0, id_range, n, dtype=np.int32)
+    mul = (nrows << 32) // id_range
+    rows = np.minimum((ids.astype(np.uint64) * np.uint64(mul)) >> np.uint64(32), nrows - 1).astype(np.int64)
+    want = np.bitwise_xor.reduce(table[rows].reshape(-1))
+    dt = _lib.DeviceBuffer(table.nbytes).upload(table)
+    di = _lib.DeviceBuffer(ids.nbytes).upload(ids)
+    df = _lib.DeviceBuffer(4)
+    L = _lib.load()
+    for per in (1, 2, 4):
+        for waves in (8, 16, 32):
+            for nt in (0, 1):
+                df.clear()
+                ms, launched = C.c_float(0), C.c_int32(0)
+                _lib.check(L.qv_gather_sweep_bench(dt.ptr, nrows, row, di.ptr, n, id_range, per, waves, nt, df.ptr,
+                                                   0, C.byref(ms), C.byref(launched)))
+                assert df.download(np.uint32, (1,))[0] == want, (per, waves, nt)
+                assert launched.value % 4 == 0 and launched.value <= 256 * waves
