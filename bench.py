@@ -593,25 +593,17 @@ def adc_leg(_lib, L, ncodes: int, log) -> dict:
     gms = float(np.median(gt[1:]))
     fold.close()
     log(f"gather alone: {gms:.3f} ms, {evals / gms / 1e6:.1f} G rows/s; ADC at {gms / ms:.1%} of that rate")
-    # the same number of uniformly random rows of 32, 64, 128 and 256 bytes from
-    # the same table: a rate that does not fall with the width means the gather
-    # pays per row, not per byte
-    fold = _lib.DeviceBuffer(evals * 16 // 256 * 4 + 4096)
-    widths = {}
-    for wb, sh in ((32, 0), (64, 1), (128, 2), (256, 3)):
-        ts = []
-        for _ in range(3):
-            wms = C.c_float()
-            _lib.check(L.qv_gather_rows_bench(codes.ptr, ncodes * M, wb, ids.ptr, evals, sh, fold.ptr, 0,
-                                              C.byref(wms)))
-            ts.append(wms.value)
-        wms = float(np.median(ts[1:]))
-        widths[wb] = {"ms": round(wms, 4), "rows_per_s": round(evals / (wms * 1e-3), 1),
-                      "gb_per_s": round(evals * wb / (wms * 1e-3) / 1e9, 1)}
-        log(f"random {wb:3d}-byte rows: {wms:.3f} ms, {evals / wms / 1e6:.1f} G rows/s, "
-            f"{evals * wb / wms / 1e6:.0f} GB/s")
-    fold.close()
+    # the access-rate matrix: the same ids over tables of 32 MB to 32 GB, rows
+    # of 32-256 bytes, both load types, 1-4 rows in flight, 8-32 waves per CU
     matrix = access_matrix(_lib, L, codes, ncodes, M, ids, evals, log)
+    # rows of 32, 64, 128 and 256 bytes from the whole table, as the ADC
+    # kernel reads (nontemporal, one row in flight, 32 waves per CU): a rate
+    # that does not fall with the width means the gather pays per row
+    widths = {}
+    for c in matrix["cells"]:
+        if (c["table_bytes"] == min(32_000_000_000, ncodes * M) and c["nontemporal"] and c["rows_in_flight"] == 1
+                and c["waves_per_cu"] == 32):
+            widths[c["row_bytes"]] = {"ms": c["ms"], "rows_per_s": c["rows_per_s"], "gb_per_s": c["gb_per_s"]}
     rate32 = widths[32]["rows_per_s"]
     # the widest row read at (within 15 % of) the 32-byte row rate: what one
     # random 32-byte row occupies of the memory system
