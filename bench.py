@@ -636,7 +636,7 @@ def adc_leg(_lib, L, ncodes: int, log) -> dict:
             "physical_frac": round(phys_gbs / HBM_PEAK_GBS, 4),
             "random_read_peak_gbs": random_peak,
             "access_matrix": matrix,
-            "physical_frac_of_random_read_peak": round(phys_gbs / random_peak, 4)}
+            "physical_frac_of_stream_read": round(phys_gbs / stream_gbs, 4)}
 
 
 def access_matrix(_lib, L, codes, ncodes, M, ids, n, log) -> dict:
