@@ -84,6 +84,22 @@ __device__ __forceinline__ uint64_t read_lane_u64(uint64_t v, int l) {
   return ((uint64_t)read_lane_u32((uint32_t)(v >> 32), l) << 32) | read_lane_u32((uint32_t)v, l);
 }
 
+// Sum of v over the lanes below this one: an inclusive scan within each row of
+// 16 lanes (DPP row_shr 1, 2, 4, 8; lanes shifted in from outside the row
+// read 0), then lane 15 of rows 0 and 2 added to rows 1 and 3 (row_bcast:15)
+// and lane 31 to rows 2 and 3 (row_bcast:31); rows a broadcast does not
+// write keep the 0 given as the old value.
+__device__ __forceinline__ uint32_t wave_excl_sum(uint32_t v) {
+  int x = (int)v;
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);
+  return (uint32_t)x - v;
+}
+
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
   uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
   lo = (uint32_t)__shfl_xor((int)lo, m);

@@ -103,13 +103,19 @@ constexpr int64_t kFeedMirrorBytes = kFeedLines * kFeedStride * 8;
 // are only read once, into registers (load_query_dpp, load_query_pre),
 // before the first hop.
 struct LdsPlan {
-  int lut_off, qc_off, qu_off, beam_off, total;
+  int lut_off, qc_off, qu_off, beam_off, count_off, total;
 };
 
 // LDS beam entries: Q * 64 with the per-query LUT (its table, not the beam,
 // limits the queries per CU); ef rounded up to 8 with shared pivots, where the
 // beam's LDS decides how many queries a CU holds.
 __host__ __device__ inline int beam_cap(int ef, int Q, bool lut) { return lut ? Q * kWave : (ef + 7) & ~7; }
+
+// Whether a merge counts its surviving candidates per beam rank in LDS (one
+// word per beam position, after the beam): the per-query-LUT kernel up to
+// Q = 7, where the counts still leave room for 4 queries of 32-chunk LUTs per
+// CU.  The other kernels add the candidates one at a time.
+__host__ __device__ constexpr bool rank_counts(bool lut, int Q) { return lut && Q <= 7; }
 
 __host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool lut, int ef) {
   LdsPlan p;
@@ -120,7 +126,9 @@ __host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool
   const bool overlay = !lut && dim <= 32 * kVecPre;
   p.beam_off = overlay ? p.qc_off : (p.qu_off + dpad * 4 + 15) & ~15;
   const int beam_bytes = beam_cap(ef, Q, lut) * 8;
-  p.total = p.beam_off + (overlay && 2 * dpad * 4 > beam_bytes ? 2 * dpad * 4 : beam_bytes);
+  p.count_off = p.beam_off + beam_bytes;  // (rank_counts: no overlay)
+  p.total = p.beam_off + (overlay && 2 * dpad * 4 > beam_bytes ? 2 * dpad * 4 : beam_bytes) +
+            (rank_counts(lut, Q) ? beam_cap(ef, Q, lut) * 4 : 0);
   return p;
 }
 
@@ -194,6 +202,12 @@ struct Query {
   static constexpr int kQd = SC > 0 ? (MC * SC + 15) / 16 : 1;
   float qd[kQd];
   uint64_t* beam;
+  // surviving candidates per beam rank (kCounts), zero between merges
+  uint32_t* rcount;
+  static constexpr bool kCounts = rank_counts(SC == 0, Q);
+  // 8-ary rank search (needs cap = 64 Q); at Q = 1 the 4-ary one also takes
+  // two LDS round trips, with fewer reads.
+  static constexpr bool kRank8 = kCounts && Q >= 2;
   int sz;        // beam size (ctx.size)
   int cap;       // LDS beam entries (beam_cap >= ef)
   // The beam in registers, chunk-major (lane l holds positions [l Q, l Q + Q),
@@ -213,6 +227,10 @@ struct Query {
   // visited does not matter here (a candidate's key equals an entry's only
   // with the same id, which is not below it either way).
   uint64_t lastk;
+  // (kRank8) the beam's entries at 64 j - 1, j = 1 .. Q - 1, from the
+  // register copy (kPadKey past sz), wave-uniform: the first level of the
+  // rank search, renewed whenever the beam changes.
+  uint64_t pk[Q > 1 ? Q - 1 : 1];
 
   // The shared-pivot kernels serve dim = MC SC only (uniform chunks).
   static constexpr int kD = SC > 0 ? MC * SC : 0;
@@ -227,12 +245,15 @@ struct Query {
         evals(0), lastk(~0ull) {
 #pragma unroll
     for (int k = 0; k < Q; k++) ck[k] = kPadKey;
+#pragma unroll
+    for (int j = 0; j < Q - 1; j++) pk[j] = kPadKey;
     LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, SC == 0, a.ef);
     cap = beam_cap(a.ef, Q, SC == 0);
     lut = reinterpret_cast<float*>(smem + pl.lut_off);
     qc = reinterpret_cast<float*>(smem + pl.qc_off);
     qu = reinterpret_cast<float*>(smem + pl.qu_off);
     beam = reinterpret_cast<uint64_t*>(smem + pl.beam_off);
+    rcount = reinterpret_cast<uint32_t*>(smem + pl.count_off);
     const int lane = lane_id();
 #pragma unroll
     for (int j = 0; j < NPL; j++)  // slots >= max_m are masked by the degree
@@ -436,11 +457,16 @@ struct Query {
 
   // Every LDS beam position from sz to cap holds kPadKey (above every key):
   // set once per query; merges only write below the new sz, which never
-  // shrinks.  The rank search then needs no bounds test.
+  // shrinks.  The rank search then needs no bounds test.  The rank counts
+  // start at zero, and every merge leaves them so.
   __device__ __forceinline__ void pad_beam(int lane) {
 #pragma unroll
     for (int k = 0; k < Q; k++)
       if (k * kWave + lane < cap) beam[k * kWave + lane] = kPadKey;
+    if constexpr (kCounts) {
+#pragma unroll
+      for (int k = 0; k < Q; k++) rcount[k * kWave + lane] = 0u;
+    }
   }
 
   // Beam position P from the register copy (kPadKey past it), wave-uniform.
@@ -452,24 +478,37 @@ struct Query {
       return kPadKey;
   }
 
-  // First unvisited entry of the beam from the register copy.
-  __device__ __forceinline__ void find_unvisited(int lane) {
-    int first = INT32_MAX;
+  // pk from the register copy.
+  __device__ __forceinline__ void block_keys() {
 #pragma unroll
-    for (int k = 0; k < Q; k++) {
-      const uint64_t m = __ballot(lane * Q + k < sz && key_unvisited(ck[k]));
-      if (m) first = min(first, (__ffsll((long long)m) - 1) * Q + k);
+    for (int j = 0; j < Q - 1; j++) {
+      constexpr int kQ = Q;
+      const int P = 64 * (j + 1) - 1;
+      pk[j] = read_lane_u64(ck[P % kQ], P / kQ);
     }
-    u = first;
-    // its key from the register copy: slot first % Q of lane first / Q
-    // (wave-uniform, so the next node's record address is scalar work)
-    if (first < sz) {
-      const int kk = first % Q;
+  }
+
+  // First unvisited entry of the beam from the register copy: the first lane
+  // L with an unvisited entry among its slots below sz (bit k of m: slot k),
+  // and its lowest such slot kk, position L Q + kk.
+  __device__ __forceinline__ void find_unvisited(int lane) {
+    const int nv = sz - lane * Q;
+    uint32_t m = 0;
+#pragma unroll
+    for (int k = 0; k < Q; k++) m |= k < nv && key_unvisited(ck[k]) ? 1u << k : 0u;
+    const uint64_t any = __ballot(m != 0);
+    if (any) {
+      const int L = __ffsll((long long)any) - 1;
+      const int kk = __builtin_ctz(read_lane_u32(m, L));
+      u = L * Q + kk;
+      // its key from the register copy (wave-uniform, so the next node's
+      // record address is scalar work)
       uint64_t e = ck[0];
 #pragma unroll
       for (int k = 1; k < Q; k++) e = kk == k ? ck[k] : e;
-      bu = read_lane_u64(e, first / Q);
+      bu = read_lane_u64(e, L);
     } else {
+      u = INT32_MAX;
       bu = ~0ull;
     }
   }
@@ -519,47 +558,83 @@ struct Query {
     bool valid = below;
     {
       if (__ballot(below)) {
-        // r = #{beam entries e : e < (nkey & ~1)} by a 4-ary search over the
-        // LDS beam: sorted, kPadKey from sz to its capacity cap (>= ef), so
-        // a read clamped to cap - 1 sees either a key of the beam or kPadKey
-        // (a below candidate is under the last key of a full beam, so even a
-        // full-capacity beam never lifts r past it).  A level of step s reads
-        // r + s - 1, r + 2 s - 1 and r + 3 s - 1 at once (one LDS round trip)
-        // and adds s per key below; steps 4^i from kTop cover 4 kTop - 1 >=
-        // 64 Q - 1 positions.  The last level (s = 1) also reads r + 3, so
-        // beam[r] for the membership test is one of its four keys.
-        //
-        // The first level (r = 0 in every lane) reads the same three positions
-        // for every lane, so it compares against the register beam's copies,
-        // read as wave-uniform values: the same keys, or kPadKey past sz where
-        // the LDS read would be clamped to cap - 1 -- equal for the
-        // comparison, since a below candidate is under the last key of a
-        // full beam.  Visited bits do not matter: e < c0 ignores them.
-        constexpr int kCap = Q * kWave;
-        constexpr int kTop = kCap <= 64 ? 16 : (kCap <= 256 ? 64 : 256);
-        const int top = cap - 1;
         const uint64_t c0 = nkey & ~1ull;
-        {
-          const uint64_t e1 = reg_pos<kTop - 1>(), e2 = reg_pos<2 * kTop - 1>(), e3 = reg_pos<3 * kTop - 1>();
-          r = ((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * kTop;
-        }
+        uint64_t at;
+        if constexpr (kRank8) {
+          // cap = 64 Q: r = #{beam entries e : e < c0} by an 8-ary search.
+          // Sorted, with kPadKey from sz to cap, the beam puts
+          // min(floor(r / 64), Q - 1) of the keys pk below c0, which gives
+          // r's 64-entry block at b0 = 64 n0 <= cap - 64 (beam[cap - 1] is
+          // kPadKey or, in a full beam of ef = cap, the last key, which a
+          // below candidate is under); then 7 keys at steps of 8 inside it
+          // and the 8 keys from there (beam[r] among them): every read lies
+          // in [b0, b0 + 63], inside the beam, whatever c0.  Two LDS round
+          // trips.  Visited bits do not matter: e < c0 ignores them.
+          int n0 = 0;
 #pragma unroll
-        for (int step = kTop / 4; step > 1; step >>= 2) {
-          const uint64_t e1 = beam[min(r + step - 1, top)];
-          const uint64_t e2 = beam[min(r + 2 * step - 1, top)];
-          const uint64_t e3 = beam[min(r + 3 * step - 1, top)];
-          r += ((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * step;
+          for (int j = 0; j < Q - 1; j++) n0 += pk[j] < c0 ? 1 : 0;
+          r = 64 * n0;
+          const uint64_t* const blk8 = beam + r;
+          int n1 = 0;
+#pragma unroll
+          for (int j = 1; j < 8; j++) n1 += blk8[8 * j - 1] < c0 ? 1 : 0;
+          r += 8 * n1;
+          const uint64_t* const last8 = beam + r;
+          uint64_t g[8];
+#pragma unroll
+          for (int j = 0; j < 8; j++) g[j] = last8[j];
+          // g[7] is only selected when n == 7; without this the compiler
+          // moves its read into that branch, a third dependent round trip.
+          asm volatile("" : "+v"(g[7]));
+          int n = 0;
+#pragma unroll
+          for (int j = 0; j < 7; j++) n += g[j] < c0 ? 1 : 0;
+          r += n;
+          at = g[7];
+#pragma unroll
+          for (int j = 6; j >= 0; j--) at = n == j ? g[j] : at;
+        } else {
+          // r = #{beam entries e : e < c0} by a 4-ary search over the
+          // LDS beam: sorted, kPadKey from sz to its capacity cap (>= ef), so
+          // a read clamped to cap - 1 sees either a key of the beam or kPadKey
+          // (a below candidate is under the last key of a full beam, so even a
+          // full-capacity beam never lifts r past it).  A level of step s reads
+          // r + s - 1, r + 2 s - 1 and r + 3 s - 1 at once (one LDS round trip)
+          // and adds s per key below; steps 4^i from kTop cover 4 kTop - 1 >=
+          // 64 Q - 1 positions.  The last level (s = 1) also reads r + 3, so
+          // beam[r] for the membership test is one of its four keys.
+          //
+          // The first level (r = 0 in every lane) reads the same three positions
+          // for every lane, so it compares against the register beam's copies,
+          // read as wave-uniform values: the same keys, or kPadKey past sz where
+          // the LDS read would be clamped to cap - 1 -- equal for the
+          // comparison, since a below candidate is under the last key of a
+          // full beam.  Visited bits do not matter: e < c0 ignores them.
+          constexpr int kCap = Q * kWave;
+          constexpr int kTop = kCap <= 64 ? 16 : (kCap <= 256 ? 64 : 256);
+          const int top = cap - 1;
+          {
+            const uint64_t e1 = reg_pos<kTop - 1>(), e2 = reg_pos<2 * kTop - 1>(), e3 = reg_pos<3 * kTop - 1>();
+            r = ((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * kTop;
+          }
+#pragma unroll
+          for (int step = kTop / 4; step > 1; step >>= 2) {
+            const uint64_t e1 = beam[min(r + step - 1, top)];
+            const uint64_t e2 = beam[min(r + 2 * step - 1, top)];
+            const uint64_t e3 = beam[min(r + 3 * step - 1, top)];
+            r += ((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * step;
+          }
+          const uint64_t e0 = beam[min(r, top)];
+          const uint64_t e1 = beam[min(r + 1, top)];
+          const uint64_t e2 = beam[min(r + 2, top)];
+          uint64_t e3 = beam[min(r + 3, top)];
+          // e3 is only selected when n == 3; without this the compiler moves its
+          // read into that branch, a fourth dependent LDS round trip.
+          asm volatile("" : "+v"(e3));
+          const int n = (e0 < c0 ? 1 : 0) + (e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0);
+          r += n;
+          at = n == 0 ? e0 : (n == 1 ? e1 : (n == 2 ? e2 : e3));
         }
-        const uint64_t e0 = beam[min(r, top)];
-        const uint64_t e1 = beam[min(r + 1, top)];
-        const uint64_t e2 = beam[min(r + 2, top)];
-        uint64_t e3 = beam[min(r + 3, top)];
-        // e3 is only selected when n == 3; without this the compiler moves its
-        // read into that branch, a fourth dependent LDS round trip.
-        asm volatile("" : "+v"(e3));
-        const int n = (e0 < c0 ? 1 : 0) + (e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0);
-        r += n;
-        const uint64_t at = n == 0 ? e0 : (n == 1 ? e1 : (n == 2 ? e2 : e3));
         valid = below && (at >> 1) != (nkey >> 1);
       }
     }
@@ -604,20 +679,26 @@ struct Query {
     }
     }
 
-    // For each surviving candidate c (few per hop: most neighbours below the
-    // beam's end are already in it): its rank t among the candidates and the
-    // shift of every old entry at or above its rank in the beam.
+    // Each surviving candidate's rank t among the candidates, and the shift
+    // sh of every old entry: the number of candidates whose rank is at or
+    // below its position.
     int t = 0;
     uint32_t sh[Q];
+    if (kCounts && __popcll(vm) > kCountMin) {
+      count_shifts(valid, nkey, r, lane, t, sh);
+    } else {
+      // one candidate at a time (few per hop: most neighbours below the
+      // beam's end are already in it)
 #pragma unroll
-    for (int k = 0; k < Q; k++) sh[k] = 0u;
-    for (uint64_t rest = vm; rest; rest &= rest - 1) {
-      const int l = __ffsll((long long)rest) - 1;
-      const uint64_t c = read_lane_u64(nkey, l);
-      const int rc = read_lane_i32(r, l);
-      t += c < nkey ? 1 : 0;
+      for (int k = 0; k < Q; k++) sh[k] = 0u;
+      for (uint64_t rest = vm; rest; rest &= rest - 1) {
+        const int l = __ffsll((long long)rest) - 1;
+        const uint64_t c = read_lane_u64(nkey, l);
+        const int rc = read_lane_i32(r, l);
+        t += c < nkey ? 1 : 0;
 #pragma unroll
-      for (int k = 0; k < Q; k++) sh[k] += lane * Q + k >= rc ? 1u : 0u;
+        for (int k = 0; k < Q; k++) sh[k] += lane * Q + k >= rc ? 1u : 0u;
+      }
     }
 
     // Scatter in place; entries pushed to ef or beyond drop out.
@@ -639,8 +720,52 @@ struct Query {
       ck[k] = pos < sz ? beam[pos] : kPadKey;
     }
     lastk = sz >= ef ? beam[ef - 1] : ~0ull;
+    if constexpr (kRank8) block_keys();
     find_unvisited(lane);
     return SEL ? (int32_t)key_id(selkey) : -1;
+  }
+
+  // Survivors above which a merge counts them per rank instead of one at a
+  // time (kCounts).
+  static constexpr int kCountMin = 2;
+
+  // sh and t by counting: rcount[x] = surviving candidates of rank x (LDS
+  // adds), replaced by its inclusive prefix over the beam positions (lane l
+  // owns positions [l Q, l Q + Q): a running sum over its Q counts, plus the
+  // sum of the lanes below).  A candidate of rank r comes after every
+  // candidate of a lower rank (a beam entry lies between them) and before
+  // every one of a higher rank, so t = prefix(r - 1) plus the candidates of
+  // rank r with a smaller key, counted one at a time where a rank holds
+  // several.  rcount is zero again on return.
+  __device__ __forceinline__ void count_shifts(bool valid, uint64_t nkey, int r, int lane, int& t,
+                                               uint32_t (&sh)[Q]) {
+    if (valid) __hip_atomic_fetch_add(rcount + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+    uint32_t* const own = rcount + lane * Q;
+    uint32_t run = 0;
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      run += own[k];
+      sh[k] = run;
+    }
+    const uint32_t lower = wave_excl_sum(run);
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      sh[k] += lower;
+      own[k] = sh[k];
+    }
+    // prefix(r) and prefix(r - 1) (at r = 0 the word before the counts, the
+    // beam's last, is read and not used)
+    const uint32_t* const at = rcount + min(r, cap - 1);
+    const uint32_t upto = at[0];
+    const uint32_t before = r > 0 ? at[-1] : 0u;
+#pragma unroll
+    for (int k = 0; k < Q; k++) own[k] = 0u;
+    t = (int)before;
+    for (uint64_t rest = __ballot(valid && upto - before > 1u); rest; rest &= rest - 1) {
+      const int l = __ffsll((long long)rest) - 1;
+      const uint64_t c = read_lane_u64(nkey, l);
+      t += read_lane_i32(r, l) == r && c < nkey ? 1 : 0;
+    }
   }
 
   // persistent_select_next_no_compact (kernel_helpers.cuh:491-518): the first
