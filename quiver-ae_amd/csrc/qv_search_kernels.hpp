@@ -686,6 +686,8 @@ struct Query {
     uint32_t sh[Q];
     if (kCounts && __popcll(vm) > kCountMin) {
       count_shifts(valid, nkey, r, lane, t, sh);
+    } else if (kPacked && __popcll(vm) > kPackedMin && ~vm != 0) {
+      packed_shifts(vm, valid, nkey, r, lane, t, sh);
     } else {
       // one candidate at a time (few per hop: most neighbours below the
       // beam's end are already in it)
@@ -762,6 +764,70 @@ struct Query {
     for (int k = 0; k < Q; k++) own[k] = 0u;
     t = (int)before;
     for (uint64_t rest = __ballot(valid && upto - before > 1u); rest; rest &= rest - 1) {
+      const int l = __ffsll((long long)rest) - 1;
+      const uint64_t c = read_lane_u64(nkey, l);
+      t += read_lane_i32(r, l) == r && c < nkey ? 1 : 0;
+    }
+  }
+
+  // The same in registers (the kernels without the LDS counts, at Q = 4 and
+  // 5, where the loop's Q compares per survivor cost the most and one word
+  // holds a lane's counts): lane l's counts of surviving candidates per rank, for
+  // its positions l Q + k, as 6-bit fields (field k at bit 6 (k % 5) of word
+  // k / 5), each survivor adding one to the field of its rank's owner; with
+  // at most 63 survivors neither a count nor a prefix leaves its field.
+  static constexpr bool kPacked = !kCounts && (Q == 4 || Q == 5);
+  static constexpr int kPW = (Q + 4) / 5;
+  static constexpr int kPackedMin = 4;
+
+  // sh and t from the packed counts: the prefix over each lane's fields plus
+  // the sum of the lanes below gives sh; a candidate of rank r reads the
+  // prefix and the count at r from the lane that owns r (ds_bpermute), and
+  // t = prefix(r) - count(r), plus the smaller keys of its rank where the
+  // count is above one.
+  __device__ __forceinline__ void packed_shifts(uint64_t vm, bool valid, uint64_t nkey, int r, int lane, int& t,
+                                                uint32_t (&sh)[Q]) {
+    uint32_t cw[kPW];
+#pragma unroll
+    for (int w = 0; w < kPW; w++) cw[w] = 0u;
+    for (uint64_t rest = vm; rest; rest &= rest - 1) {
+      const int l = __ffsll((long long)rest) - 1;
+      const uint32_t rc = (uint32_t)read_lane_i32(r, l);
+      const uint32_t owner = rc / Q, f = rc - owner * Q;
+      const uint32_t inc = 1u << (6 * (kPW == 1 ? f : f % 5));
+#pragma unroll
+      for (int w = 0; w < kPW; w++) cw[w] += (uint32_t)lane == owner && (kPW == 1 || f / 5 == (uint32_t)w) ? inc : 0u;
+    }
+    uint32_t run = 0;
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      run += (cw[k / 5] >> (6 * (k % 5))) & 63u;
+      sh[k] = run;
+    }
+    const uint32_t lower = wave_excl_sum(run);
+    uint32_t pw[kPW];
+#pragma unroll
+    for (int w = 0; w < kPW; w++) pw[w] = 0u;
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      sh[k] += lower;
+      pw[k / 5] |= sh[k] << (6 * (k % 5));
+    }
+    const uint32_t rr = (uint32_t)min(r, Q * kWave - 1);
+    const uint32_t owner = rr / Q, f = rr - owner * Q;
+    const int at = (int)(owner << 2);
+    uint32_t pv = (uint32_t)__builtin_amdgcn_ds_bpermute(at, (int)pw[0]);
+    uint32_t cv = (uint32_t)__builtin_amdgcn_ds_bpermute(at, (int)cw[0]);
+    if constexpr (kPW > 1) {
+      const uint32_t pv1 = (uint32_t)__builtin_amdgcn_ds_bpermute(at, (int)pw[1]);
+      const uint32_t cv1 = (uint32_t)__builtin_amdgcn_ds_bpermute(at, (int)cw[1]);
+      pv = f >= 5 ? pv1 : pv;
+      cv = f >= 5 ? cv1 : cv;
+    }
+    const uint32_t sf = 6u * (kPW == 1 ? f : f % 5);
+    const uint32_t upto = (pv >> sf) & 63u, here = (cv >> sf) & 63u;
+    t = (int)(upto - here);
+    for (uint64_t rest = __ballot(valid && here > 1u); rest; rest &= rest - 1) {
       const int l = __ffsll((long long)rest) - 1;
       const uint64_t c = read_lane_u64(nkey, l);
       t += read_lane_i32(r, l) == r && c < nkey ? 1 : 0;
