@@ -84,6 +84,18 @@ __device__ __forceinline__ uint64_t read_lane_u64(uint64_t v, int l) {
   return ((uint64_t)read_lane_u32((uint32_t)(v >> 32), l) << 32) | read_lane_u32((uint32_t)v, l);
 }
 
+// LDS byte address of a pointer into the dynamic LDS area, and the 8-byte
+// word at byte address min(a, lim) + 8 OFF: one v_min against a wave-uniform
+// bound, the offset in the instruction (min(x + k, t) = min(x, t - k) + k).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+template <int OFF>
+__device__ __forceinline__ uint64_t lds_u64_min(uint32_t a, uint32_t lim) {
+  const uint32_t m = min(a, lim);
+  return ((const __attribute__((address_space(3))) uint64_t*)(uintptr_t)m)[OFF];
+}
+
 // Sum of v over the lanes below this one: an inclusive scan within each row of
 // 16 lanes (DPP row_shr 1, 2, 4, 8; lanes shifted in from outside the row
 // read 0), then lane 15 of rows 0 and 2 added to rows 1 and 3 (row_bcast:15)

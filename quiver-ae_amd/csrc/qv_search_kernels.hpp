@@ -213,8 +213,12 @@ struct Query {
   // The beam in registers, chunk-major (lane l holds positions [l Q, l Q + Q),
   // kPadKey at and beyond sz), and its first unvisited entry u with key bu
   // (INT32_MAX and ~0 when every entry is visited).  LDS holds the same beam
-  // for the scatter of each merge.
+  // for the scatter of each merge.  Which entries are unvisited is um's to
+  // say (bit k: slot k of this lane, below sz): marking an entry visited
+  // clears its bit only, and the visited bits of ck are brought up to date
+  // from um when a merge writes the beam back.
   uint64_t ck[Q];
+  uint32_t um;
   int u;
   uint64_t bu;
   float td;      // top-k entry of this lane
@@ -241,7 +245,7 @@ struct Query {
 
   // smem: this query's LDS area.
   __device__ Query(const SearchArgs& args, char* smem, const float* pivots_lds)
-      : a(args), piv(pivots_lds), sz(0), u(INT32_MAX), bu(~0ull), td(__int_as_float(0x7f800000)), ti(-1), fc(0),
+      : a(args), piv(pivots_lds), sz(0), um(0), u(INT32_MAX), bu(~0ull), td(__int_as_float(0x7f800000)), ti(-1), fc(0),
         evals(0), lastk(~0ull) {
 #pragma unroll
     for (int k = 0; k < Q; k++) ck[k] = kPadKey;
@@ -478,6 +482,18 @@ struct Query {
       return kPadKey;
   }
 
+  // The 4-ary search's LDS levels of steps S, S / 4, .. 4 (rank_levels).
+  template <int S>
+  __device__ __forceinline__ void rank_levels(uint32_t& rb, uint32_t top8, uint64_t c0) const {
+    if constexpr (S > 1) {
+      const uint64_t e1 = lds_u64_min<S - 1>(rb, top8 - 8u * (S - 1));
+      const uint64_t e2 = lds_u64_min<2 * S - 1>(rb, top8 - 8u * (2 * S - 1));
+      const uint64_t e3 = lds_u64_min<3 * S - 1>(rb, top8 - 8u * (3 * S - 1));
+      rb += 8u * (uint32_t)(((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * S);
+      rank_levels<S / 4>(rb, top8, c0);
+    }
+  }
+
   // pk from the register copy.
   __device__ __forceinline__ void block_keys() {
 #pragma unroll
@@ -488,24 +504,34 @@ struct Query {
     }
   }
 
-  // First unvisited entry of the beam from the register copy: the first lane
-  // L with an unvisited entry among its slots below sz (bit k of m: slot k),
-  // and its lowest such slot kk, position L Q + kk.
-  __device__ __forceinline__ void find_unvisited(int lane) {
+  // um from the register copy (after a merge reloads it).
+  __device__ __forceinline__ void unvisited_mask(int lane) {
     const int nv = sz - lane * Q;
     uint32_t m = 0;
 #pragma unroll
     for (int k = 0; k < Q; k++) m |= k < nv && key_unvisited(ck[k]) ? 1u << k : 0u;
-    const uint64_t any = __ballot(m != 0);
+    um = m;
+  }
+
+  // First unvisited entry of the beam: the first lane L with a bit in um, and
+  // its lowest such slot kk, position L Q + kk.
+  __device__ __forceinline__ void find_unvisited(int lane) {
+    const uint64_t any = __ballot(um != 0);
     if (any) {
       const int L = __ffsll((long long)any) - 1;
-      const int kk = __builtin_ctz(read_lane_u32(m, L));
+      const int kk = __builtin_ctz(read_lane_u32(um, L));
       u = L * Q + kk;
       // its key from the register copy (wave-uniform, so the next node's
-      // record address is scalar work)
+      // record address is scalar work), selected among values: opaque, so
+      // the select is not turned into one of addresses into ck, an index the
+      // compiler can only serve from memory
       uint64_t e = ck[0];
 #pragma unroll
-      for (int k = 1; k < Q; k++) e = kk == k ? ck[k] : e;
+      for (int k = 1; k < Q; k++) {
+        uint64_t ek = ck[k];
+        asm volatile("" : "+v"(ek));
+        e = kk == k ? ek : e;
+      }
       bu = read_lane_u64(e, L);
     } else {
       u = INT32_MAX;
@@ -513,11 +539,12 @@ struct Query {
     }
   }
 
-  // Marks the entry at position pos visited (LDS and registers).
+  // Marks the entry at position pos (wave-uniform) visited: in LDS, and in
+  // um (bit pos % Q of lane pos / Q).
   __device__ __forceinline__ void mark_visited(int pos, uint64_t key, int lane) {
     if (lane == 0) beam[pos] = key & ~1ull;
-#pragma unroll
-    for (int k = 0; k < Q; k++) ck[k] &= lane * Q + k == pos ? ~1ull : ~0ull;
+    const uint32_t owner = (uint32_t)pos / Q, bit = 1u << ((uint32_t)pos - owner * Q);
+    um &= (uint32_t)lane == owner ? ~bit : ~0u;
   }
 
   // persistent_merge_data's result after persistent_visit_select_dualwarp's
@@ -612,27 +639,31 @@ struct Query {
           // full beam.  Visited bits do not matter: e < c0 ignores them.
           constexpr int kCap = Q * kWave;
           constexpr int kTop = kCap <= 64 ? 16 : (kCap <= 256 ? 64 : 256);
-          const int top = cap - 1;
           {
             const uint64_t e1 = reg_pos<kTop - 1>(), e2 = reg_pos<2 * kTop - 1>(), e3 = reg_pos<3 * kTop - 1>();
             r = ((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * kTop;
           }
-#pragma unroll
-          for (int step = kTop / 4; step > 1; step >>= 2) {
-            const uint64_t e1 = beam[min(r + step - 1, top)];
-            const uint64_t e2 = beam[min(r + 2 * step - 1, top)];
-            const uint64_t e3 = beam[min(r + 3 * step - 1, top)];
-            r += ((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * step;
-          }
-          const uint64_t e0 = beam[min(r, top)];
-          const uint64_t e1 = beam[min(r + 1, top)];
-          const uint64_t e2 = beam[min(r + 2, top)];
-          uint64_t e3 = beam[min(r + 3, top)];
+          // LDS byte addresses: rb = beam + 8 r, and the read of position
+          // min(r + k, cap - 1) at min(rb, top8 - 8 k) + 8 k, the 8 k in the
+          // instruction (every beam lies past the LUT or the pivot table, at
+          // least 8 KB in, so top8 - 8 k stays above 0 for k < 3 kTop).  The
+          // address is wave-uniform: held in a scalar register, opaque, so the
+          // bounds are scalar work of each merge rather than vector registers
+          // held across the loop.
+          uint32_t b0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_addr(beam));
+          asm volatile("" : "+s"(b0));
+          const uint32_t top8 = b0 + 8u * (uint32_t)(cap - 1);
+          uint32_t rb = b0 + 8u * (uint32_t)r;
+          rank_levels<kTop / 4>(rb, top8, c0);
+          const uint64_t e0 = lds_u64_min<0>(rb, top8);
+          const uint64_t e1 = lds_u64_min<1>(rb, top8 - 8u);
+          const uint64_t e2 = lds_u64_min<2>(rb, top8 - 16u);
+          uint64_t e3 = lds_u64_min<3>(rb, top8 - 24u);
           // e3 is only selected when n == 3; without this the compiler moves its
           // read into that branch, a fourth dependent LDS round trip.
           asm volatile("" : "+v"(e3));
           const int n = (e0 < c0 ? 1 : 0) + (e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0);
-          r += n;
+          r = (int)((rb - b0) >> 3) + n;
           at = n == 0 ? e0 : (n == 1 ? e1 : (n == 2 ? e2 : e3));
         }
         valid = below && (at >> 1) != (nkey >> 1);
@@ -708,7 +739,8 @@ struct Query {
     for (int k = 0; k < Q; k++) {
       const int pos = lane * Q + k;
       const int g = pos + (int)sh[k];
-      if (pos < sz && g < ef) beam[g] = g == selpos ? (ck[k] & ~1ull) : ck[k];
+      const uint64_t e = (ck[k] & ~1ull) | ((um >> k) & 1u);
+      if (pos < sz && g < ef) beam[g] = g == selpos ? (e & ~1ull) : e;
     }
     const int f = r + t;
     if (valid && f < ef) beam[f] = f == selpos ? (nkey & ~1ull) : nkey;
@@ -723,6 +755,7 @@ struct Query {
     }
     lastk = sz >= ef ? beam[ef - 1] : ~0ull;
     if constexpr (kRank8) block_keys();
+    unvisited_mask(lane);
     find_unvisited(lane);
     return SEL ? (int32_t)key_id(selkey) : -1;
   }
