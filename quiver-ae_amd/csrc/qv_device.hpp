@@ -318,6 +318,22 @@ __device__ __forceinline__ float adc_sum(const CodeRow<MC>& cr, const float* __r
   return dist;
 }
 
+// adc_sum for a LUT at LDS address 0 (the first bytes of the dynamic LDS
+// area, with no static LDS before it): entry (m, c) is at byte 1024 m + 4 c,
+// so its address is one shift of the code byte (an SDWA source selects the
+// byte) and the chunk's 1024 m is the instruction's offset.
+template <int MC>
+__device__ __forceinline__ float adc_sum_at0(const CodeRow<MC>& cr) {
+  typedef const __attribute__((address_space(3))) float lds_f32;
+  float dist = 0.f;
+#pragma unroll
+  for (int j = 0; j < MC; j++) {
+    const uint32_t c = (cr.w[j >> 2] >> ((j & 3) * 8)) & 0xffu;
+    dist += ((lds_f32*)(uintptr_t)(c << 2))[j * kPivots];
+  }
+  return dist;
+}
+
 typedef float qv_float4 __attribute__((ext_vector_type(4)));
 typedef float qv_float2 __attribute__((ext_vector_type(2)));
 
@@ -653,6 +669,21 @@ __device__ __forceinline__ void load_vec_pre_buf(__amdgpu_buffer_rsrc_t r, uint3
       x[k] = (R)__builtin_amdgcn_raw_buffer_load_b8(r, o, 0, 0);
     else
       x[k] = (R)__builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0);
+  }
+}
+
+// load_vec_pre from the buffer r (a record) for a dim known only at run time:
+// the lane's byte offsets off[k] of elements min((lane & 31) + 32 k, dim - 1),
+// computed once per query, so a request costs no address arithmetic.
+template <class T, class R>
+__device__ __forceinline__ void load_vec_pre_offs(__amdgpu_buffer_rsrc_t r, const uint32_t (&off)[kVecPre],
+                                                  R (&x)[kVecPre]) {
+#pragma unroll
+  for (int k = 0; k < kVecPre; k++) {
+    if constexpr (sizeof(T) == 1)
+      x[k] = (R)__builtin_amdgcn_raw_buffer_load_b8(r, (int)off[k], 0, 0);
+    else
+      x[k] = (R)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off[k], 0, 0);
   }
 }
 

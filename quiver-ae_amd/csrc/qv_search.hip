@@ -726,11 +726,12 @@ static int occupancy(int device, int lds_cu, KernelFn k, int waves, int lds) {
   const auto any = cache.lower_bound(std::make_tuple(device, f, INT32_MIN, INT32_MIN));
   if (any == cache.end() || std::get<0>(any->first) != device || std::get<1>(any->first) != f) {
     HIP_OK(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, std::max(lds_cu, 65536)));
-    // The shared-pivot ADC addresses the pivot table at LDS address 0: the
-    // search kernels keep all their LDS dynamic, so it starts there.
+    // The ADC addresses the per-query LUT or the shared pivot table at LDS
+    // address 0: the search kernels keep all their LDS dynamic, so the area
+    // starts there.
     hipFuncAttributes fa{};
     HIP_OK(hipFuncGetAttributes(&fa, f));
-    if (fa.sharedSizeBytes != 0) fail(QV_EHIP, "search kernel has static LDS; the pivot table must start at 0");
+    if (fa.sharedSizeBytes != 0) fail(QV_EHIP, "search kernel has static LDS; the LUT or pivot table must start at 0");
   }
   int nb = 0;
   HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, kWave * waves, (size_t)lds));

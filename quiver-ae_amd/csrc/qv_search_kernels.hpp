@@ -241,6 +241,9 @@ struct Query {
   // Loop-invariant byte offsets of this lane's loads inside a record: its
   // neighbour slot (past the degree word) and its first vector element.
   uint32_t off_nbr[NPL], off_x;
+  // (kD == 0) byte offsets of this lane's first vector elements,
+  // min((lane & 31) + 32 k, dim - 1)
+  uint32_t off_xk[kD > 0 ? 1 : kVecPre];
   uint32_t off_blk;  // this lane's row in a node's neighbour-code block
 
   // smem: this query's LDS area.
@@ -263,6 +266,11 @@ struct Query {
     for (int j = 0; j < NPL; j++)  // slots >= max_m are masked by the degree
       off_nbr[j] = 4u * (uint32_t)(1 + min(lane + kWave * j, a.max_m - 1));
     off_x = (uint32_t)(lane & 31) * (uint32_t)sizeof(T);
+    if constexpr (kD == 0) {
+#pragma unroll
+      for (int k = 0; k < kVecPre; k++)
+        off_xk[k] = (uint32_t)min((lane & 31) + 32 * k, a.dim - 1) * (uint32_t)sizeof(T);
+    }
     off_blk = (uint32_t)(min(lane, a.max_m - 1) * a.num_chunks);
   }
 
@@ -290,7 +298,7 @@ struct Query {
     if constexpr (kD > 0)
       load_vec_pre_buf<T, kD>(r, off_x, nr.xv);
     else
-      load_vec_pre<T>(rec, a.dim, lane, nr.xv);
+      load_vec_pre_offs<T>(r, off_xk, nr.xv);
   }
 
   // The values a hop reads first from the record in nr.  Taken at the end
@@ -385,7 +393,7 @@ struct Query {
       if constexpr (SC > 0)
         d = adc_recompute<MC, SC, kQd>(cr, qd);
       else
-        d = adc_sum<MC>(cr, lut);
+        d = adc_sum_at0<MC>(cr);
       // the next node's code rows (lanes past its degree read row 0): the
       // guessed successor's (PF = 1) or nxt's (PF = 2)
       if constexpr (PF != 0) {
@@ -441,8 +449,8 @@ struct Query {
         d0 = adc_recompute<MC, SC, kQd>(c0, qd);
         d1 = adc_recompute<MC, SC, kQd>(c1, qd);
       } else {
-        d0 = adc_sum<MC>(c0, lut);
-        d1 = adc_sum<MC>(c1, lut);
+        d0 = adc_sum_at0<MC>(c0);
+        d1 = adc_sum_at0<MC>(c1);
       }
     } else {
       if (PF && spec) fetch((int32_t)key_id(bu), lane, nr);
