@@ -216,7 +216,9 @@ struct Query {
   // for the scatter of each merge.  Which entries are unvisited is um's to
   // say (bit k: slot k of this lane, below sz): marking an entry visited
   // clears its bit only, and the visited bits of ck are brought up to date
-  // from um when a merge writes the beam back.
+  // from um when a merge writes the beam back.  At Q = 1 marking clears the
+  // visited bit of ck itself and um is derived from it when needed (one slot
+  // per lane: that is as cheap, and the scatter needs no restoring).
   uint64_t ck[Q];
   uint32_t um;
   int u;
@@ -522,8 +524,10 @@ struct Query {
   }
 
   // First unvisited entry of the beam: the first lane L with a bit in um, and
-  // its lowest such slot kk, position L Q + kk.
+  // its lowest such slot kk, position L Q + kk.  (Q = 1: um is read off the
+  // register beam here, whose visited bits are kept current instead.)
   __device__ __forceinline__ void find_unvisited(int lane) {
+    if constexpr (Q == 1) unvisited_mask(lane);
     const uint64_t any = __ballot(um != 0);
     if (any) {
       const int L = __ffsll((long long)any) - 1;
@@ -551,8 +555,12 @@ struct Query {
   // um (bit pos % Q of lane pos / Q).
   __device__ __forceinline__ void mark_visited(int pos, uint64_t key, int lane) {
     if (lane == 0) beam[pos] = key & ~1ull;
-    const uint32_t owner = (uint32_t)pos / Q, bit = 1u << ((uint32_t)pos - owner * Q);
-    um &= (uint32_t)lane == owner ? ~bit : ~0u;
+    if constexpr (Q == 1) {
+      ck[0] &= lane == pos ? ~1ull : ~0ull;
+    } else {
+      const uint32_t owner = (uint32_t)pos / Q, bit = 1u << ((uint32_t)pos - owner * Q);
+      um &= (uint32_t)lane == owner ? ~bit : ~0u;
+    }
   }
 
   // persistent_merge_data's result after persistent_visit_select_dualwarp's
@@ -747,7 +755,7 @@ struct Query {
     for (int k = 0; k < Q; k++) {
       const int pos = lane * Q + k;
       const int g = pos + (int)sh[k];
-      const uint64_t e = (ck[k] & ~1ull) | ((um >> k) & 1u);
+      const uint64_t e = Q == 1 ? ck[k] : (ck[k] & ~1ull) | ((um >> k) & 1u);
       if (pos < sz && g < ef) beam[g] = g == selpos ? (e & ~1ull) : e;
     }
     const int f = r + t;
@@ -763,7 +771,7 @@ struct Query {
     }
     lastk = sz >= ef ? beam[ef - 1] : ~0ull;
     if constexpr (kRank8) block_keys();
-    unvisited_mask(lane);
+    if constexpr (Q > 1) unvisited_mask(lane);
     find_unvisited(lane);
     return SEL ? (int32_t)key_id(selkey) : -1;
   }
