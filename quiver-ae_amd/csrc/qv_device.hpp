@@ -84,6 +84,15 @@ __device__ __forceinline__ uint64_t read_lane_u64(uint64_t v, int l) {
   return ((uint64_t)read_lane_u32((uint32_t)(v >> 32), l) << 32) | read_lane_u32((uint32_t)v, l);
 }
 
+// Element i of a query.  The queries of a host-buffer call sit in pinned
+// host memory that the host fills while the kernel runs, so they are read at
+// system scope (relaxed: coherent with the host's writes, no cache holding an
+// older copy, no fence); each element is read once per query.
+__device__ __forceinline__ float query_elem(const float* q, int i) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<float*>(q)) + i, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_SYSTEM));
+}
+
 // LDS byte address of a pointer into the dynamic LDS area, and the 8-byte
 // word at byte address min(a, lim) + 8 OFF: one v_min against a wave-uniform
 // bound, the offset in the instruction (min(x + k, t) = min(x, t - k) + k).
@@ -869,7 +878,7 @@ __device__ __forceinline__ int32_t nav_entry(const float* __restrict__ q, const 
 #pragma unroll
   for (int k = 0; k < kNavPre; k++) {
     const int i = (lane & 31) + 32 * k;
-    qn[k] = q[min(i, dims - 1)];
+    qn[k] = query_elem(q, min(i, dims - 1));
   }
   int idx = 0;
   while (idx != -1) {

@@ -53,6 +53,7 @@ struct qv_index {
   int32_t* h_ctrl = nullptr;   // [0] feed_count, [1] terminate (host-coherent)
   int32_t* h_ring = nullptr;   // [cap_q] completion ring (host-coherent)
   int32_t* h_stage = nullptr;  // pinned: counters[4], hops, stopped, evals [cap_q each]
+  float* h_qstage = nullptr;   // pinned, coherent: a host-buffer call's queries [cap_q][d], read in place
   std::vector<int32_t> last_hops;
   std::vector<double> last_lat_ms;  // per-query latency of the last search, query order
   // host copies of the PQ tables (for saving the index)

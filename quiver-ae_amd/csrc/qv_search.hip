@@ -300,12 +300,14 @@ static void free_scratch(qv_index* ix) {
   hipFree(ix->d_tend);
   hipHostFree(ix->h_ring);
   hipHostFree(ix->h_stage);
+  hipHostFree(ix->h_qstage);
   ix->d_queries = nullptr;
   ix->d_ids = ix->d_found = ix->d_hops = ix->d_stopped = ix->d_evals = nullptr;
   ix->d_dists = nullptr;
   ix->d_tstart = ix->d_tend = nullptr;
   ix->h_ring = nullptr;
   ix->h_stage = nullptr;
+  ix->h_qstage = nullptr;
   ix->cap_q = 0;
   ix->cap_k = 0;
 }
@@ -340,6 +342,10 @@ static void ensure_scratch(qv_index* ix, int64_t nq, int k) {
   // coherent: the search kernel writes the per-query hop, stop and evaluation
   // counts straight into it
   HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_stage), sizeof(int32_t) * (size_t)(4 + 3 * cq),
+                       hipHostMallocCoherent));
+  // coherent (not cached by the GPU): a host-buffer call copies its queries
+  // here while the kernel already runs, and the kernel reads them in place
+  HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_qstage), sizeof(float) * (size_t)cq * d,
                        hipHostMallocCoherent));
   ix->cap_q = cq;
   ix->cap_k = ck;
@@ -960,7 +966,16 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
                                      : (int)std::min<int64_t>(
                                            nq, o.admission == QV_ADMIT_STATIC ? slots : slots + std::max(0, o.prefeed));
 
-  const float* d_q = o.device_buffers ? queries : ix->d_queries;
+  // Host queries under host-fed admission are not uploaded ahead of the
+  // launch: the host copies them into the pinned, GPU-uncached staging buffer
+  // a chunk at a time while the kernel already runs, feeds each query once
+  // its chunk is there, and the kernel reads every query in place, once (its
+  // 4 d bytes, read at system scope).  Only the first chunk's copy precedes
+  // the first feed.
+  const bool stage_q = !o.device_buffers && (o.admission == QV_ADMIT_STREAMING || o.admission == QV_ADMIT_STATIC);
+  float* dev_qstage = nullptr;
+  if (stage_q) HIP_OK(hipHostGetDevicePointer(reinterpret_cast<void**>(&dev_qstage), ix->h_qstage, 0));
+  const float* d_q = o.device_buffers ? queries : (stage_q ? dev_qstage : ix->d_queries);
   int32_t* d_ids = o.device_buffers ? ids : ix->d_ids;
   float* d_dists = o.device_buffers ? dists : ix->d_dists;
   int32_t* d_found = (o.device_buffers && found) ? found : ix->d_found;
@@ -1053,10 +1068,11 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   using clock = std::chrono::steady_clock;
   // The clock starts before the queries leave host memory and before the
   // launch: the reference takes t0 ahead of H2D_initial and stamps the whole
-  // initial window with it (search.cu:865-877).  The upload and the launch
-  // share the stream, so the kernel starts once its queries are in HBM.
+  // initial window with it (search.cu:865-877).  Without staging the upload
+  // and the launch share the stream, so the kernel starts once its queries
+  // are in HBM.
   const auto t0 = clock::now();
-  if (!o.device_buffers)
+  if (!o.device_buffers && !stage_q)
     HIP_OK(hipMemcpyAsync(ix->d_queries, queries, sizeof(float) * (size_t)nq * dim, hipMemcpyHostToDevice,
                           ix->stream));
   HIP_OK(hipEventRecord(ix->ev0, ix->stream));
@@ -1083,6 +1099,19 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     auto arrival_time = [&](int64_t j) {
       return t0 + std::chrono::duration_cast<clock::duration>(std::chrono::duration<double>((double)j * arr_gap));
     };
+    // Staged queries [0, staged): copied into h_qstage, each copy ordered
+    // (full fence, which also orders streaming stores) before the feed word
+    // that admits them.
+    int64_t staged = stage_q ? 0 : nq;
+    auto stage_to = [&](int64_t upto) {
+      upto = std::min<int64_t>(upto, nq);
+      if (upto <= staged) return;
+      std::memcpy(ix->h_qstage + (size_t)staged * dim, queries + (size_t)staged * dim,
+                  sizeof(float) * (size_t)(upto - staged) * dim);
+      std::atomic_thread_fence(std::memory_order_seq_cst);
+      staged = upto;
+    };
+    constexpr int64_t kStageChunk = 256;  // queries per copy (128 KB at d = 128)
     int64_t fed = static_batches ? stride : (open_loop ? std::min<int64_t>(nq, arr_b) : max_inflight);
     int64_t batch_begin = 0;  // static batches: the batch in flight is [batch_begin, fed)
     auto batch_t = t0;
@@ -1092,11 +1121,22 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
       for (int64_t i = batch_begin; i < fed; i++) lat_ms[(size_t)i] = ms;
     };
     for (int64_t i = 0; i < fed; i++) admit[(size_t)i] = t0;
+    // the initial window, a chunk at a time when staging
+    for (int64_t f = stage_q ? 0 : fed; f < fed;) {
+      f = std::min<int64_t>(fed, f + kStageChunk);
+      stage_to(f);
+      __atomic_store_n(ix->h_ctrl, (int32_t)f, __ATOMIC_RELEASE);
+    }
     __atomic_store_n(ix->h_ctrl, (int32_t)fed, __ATOMIC_RELEASE);
     int64_t done = 0;
     const int min_batch = std::max(1, o.admit_min_batch);
     while (done < nq) {
       bool progressed = false;
+      // copy ahead of the feeds while the kernel runs
+      if (staged < nq) {
+        stage_to(staged + kStageChunk);
+        progressed = true;
+      }
       while (done < nq) {
         const int32_t e = __atomic_load_n(ix->h_ring + done, __ATOMIC_ACQUIRE);
         if (e == 0) break;
@@ -1117,6 +1157,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
             to = end;
           }
           if (to > fed) {
+            stage_to(to);
             fed = to;
             __atomic_store_n(ix->h_ctrl, (int32_t)fed, __ATOMIC_RELEASE);
             progressed = true;
@@ -1130,11 +1171,13 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
           fed = std::min<int64_t>(nq, fed + stride);
           batch_t = now;
           for (int64_t i = batch_begin; i < fed; i++) admit[(size_t)i] = now;
+          stage_to(fed);
           __atomic_store_n(ix->h_ctrl, (int32_t)fed, __ATOMIC_RELEASE);
         }
       } else if (target > fed && (target - fed >= min_batch || target == nq || fed - done == 0)) {
         const auto now = clock::now();
         for (int64_t i = fed; i < target; i++) admit[(size_t)i] = now;
+        stage_to(target);
         fed = target;
         __atomic_store_n(ix->h_ctrl, (int32_t)fed, __ATOMIC_RELEASE);
       }

@@ -998,7 +998,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     // ---- query into LDS: q - mu for the LUT, fl(fl(q - mu) + mu) for the exact
     // distance (pq_device.cuh:18-20, 33-35).
     for (int i = lane; i < a.dim; i += kWave) {
-      const float c = q[i] - a.centroid[i];
+      const float c = query_elem(q, i) - a.centroid[i];
       Qy.qc[i] = c;
       Qy.qu[i] = c + a.centroid[i];
     }

@@ -333,3 +333,36 @@ def test_c1_open_loop_arrival(c1, batch, rate):
     rc = L.qv_search(c1["h"], q.ctypes.data, 16, DIM, K, 128, C.byref(o), ids.ctypes.data, dists.ctypes.data,
                      None, None)
     assert rc == lib.QV_EINVAL and b"open-loop" in L.qv_last_error()
+
+
+@pytest.mark.parametrize("admission", ["streaming", "static"])
+def test_c1_host_queries_change_between_calls(c1, admission):
+    """A host-buffer call copies its queries into the index's pinned staging
+    buffer a chunk at a time while the kernel already runs, and the kernel
+    reads each query there.  Consecutive calls with different queries (a later
+    slice, another one, then the first queries in reverse order; 1,500, 1,000
+    and 700 queries, so both kernels) must each return what the device-buffer
+    path returns for the same queries."""
+    lib, L = c1["lib"], c1["L"]
+    adm = lib.QV_ADMIT_STREAMING if admission == "streaming" else lib.QV_ADMIT_STATIC
+    sets = [c1["q"][NQ:NQ + 1500], c1["q"][NQ + 1500:NQ + 2500], c1["q"][:700][::-1]]
+    for i, qs in enumerate(sets):
+        qs = np.ascontiguousarray(qs, np.float32)
+        n = qs.shape[0]
+        _say(f"[gpu] host queries call {i}: {n} queries, admission={admission}")
+        o = lib.default_search_opts()
+        o.early_exit = lib.QV_EXIT_NONE
+        o.admission = adm
+        ids = np.empty((n, K), np.int32)
+        dists = np.empty((n, K), np.float32)
+        rep = lib.SearchReport()
+        lib.check(L.qv_search(c1["h"], qs.ctypes.data, n, DIM, K, 128, C.byref(o), ids.ctypes.data,
+                              dists.ctypes.data, None, C.byref(rep)))
+        d_q = lib.DeviceBuffer(qs.nbytes).upload(qs)
+        d_i, d_d = lib.DeviceBuffer(n * K * 4), lib.DeviceBuffer(n * K * 4)
+        o.device_buffers = 1
+        lib.check(L.qv_search(c1["h"], d_q.ptr, n, DIM, K, 128, C.byref(o), d_i.ptr, d_d.ptr, None, None))
+        want_i, want_d = d_i.download(np.int32, (n, K)), d_d.download(np.float32, (n, K))
+        for b in (d_q, d_i, d_d):
+            b.close()
+        assert np.array_equal(ids, want_i) and np.array_equal(dists, want_d), f"call {i}"
