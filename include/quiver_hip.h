@@ -240,6 +240,10 @@ typedef struct {
   int32_t kernel;            /* the search kernel that ran: QV_KERNEL_LUT or QV_KERNEL_SHARED_PIVOTS */
   double total_hops;         /* expanded nodes over all queries */
   double total_evals;        /* neighbour ADC evaluations over all queries */
+  int32_t tail_queries;      /* queries finished in tail mode (shared pivots: the
+                                workgroup's last wave, the pivot table turned
+                                into its own LUT); no reference counterpart */
+  int32_t reserved1;
 } qv_search_report;
 
 void qv_search_opts_default(qv_search_opts* opts);

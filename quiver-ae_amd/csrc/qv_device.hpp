@@ -328,20 +328,27 @@ __device__ __forceinline__ float adc_sum(const CodeRow<MC>& cr, const float* __r
 }
 
 // adc_sum for a LUT at LDS address 0 (the first bytes of the dynamic LDS
-// area, with no static LDS before it): entry (m, c) is at byte 1024 m + 4 c,
-// so its address is one shift of the code byte (an SDWA source selects the
-// byte) and the chunk's 1024 m is the instruction's offset.
-template <int MC>
+// area, with no static LDS before it): entry (m, c) is at byte
+// 4 (STRIDE m + c) (STRIDE = 256: a packed table), so its address is one
+// shift of the code byte (an SDWA source selects the byte) and the chunk's
+// 4 STRIDE m is the instruction's offset.
+template <int MC, int STRIDE = kPivots>
 __device__ __forceinline__ float adc_sum_at0(const CodeRow<MC>& cr) {
   typedef const __attribute__((address_space(3))) float lds_f32;
   float dist = 0.f;
 #pragma unroll
   for (int j = 0; j < MC; j++) {
     const uint32_t c = (cr.w[j >> 2] >> ((j & 3) * 8)) & 0xffu;
-    dist += ((lds_f32*)(uintptr_t)(c << 2))[j * kPivots];
+    dist += ((lds_f32*)(uintptr_t)(c << 2))[j * STRIDE];
   }
   return dist;
 }
+
+// A compile-time flag as an argument (for generic lambdas).
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
 
 typedef float qv_float4 __attribute__((ext_vector_type(4)));
 typedef float qv_float2 __attribute__((ext_vector_type(2)));

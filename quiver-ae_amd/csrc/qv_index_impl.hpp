@@ -52,7 +52,7 @@ struct qv_index {
   uint32_t feed_epoch = 0;            // epoch of the last search that used them
   int32_t* h_ctrl = nullptr;   // [0] feed_count, [1] terminate (host-coherent)
   int32_t* h_ring = nullptr;   // [cap_q] completion ring (host-coherent)
-  int32_t* h_stage = nullptr;  // pinned: counters[4], hops, stopped, evals [cap_q each]
+  int32_t* h_stage = nullptr;  // pinned: counters [kStageHead], hops, stopped, evals [cap_q each]
   float* h_qstage = nullptr;   // pinned, coherent: a host-buffer call's queries [cap_q][d], read in place
   std::vector<int32_t> last_hops;
   std::vector<double> last_lat_ms;  // per-query latency of the last search, query order

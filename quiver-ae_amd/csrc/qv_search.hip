@@ -314,7 +314,9 @@ static void free_scratch(qv_index* ix) {
 
 static void ensure_scratch(qv_index* ix, int64_t nq, int k) {
   if (!ix->d_counters) {
-    HIP_OK(hipMalloc(&ix->d_counters, 64));
+    // 64 bytes of launch counters, then the shared-pivot kernel's count of
+    // ended waves per workgroup (tail mode)
+    HIP_OK(hipMalloc(&ix->d_counters, 64 + 4 * kMaxTailWorkgroups));
     HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_ctrl), 64, hipHostMallocCoherent));
   }
   if (!ix->d_feed_mirror) {
@@ -341,7 +343,7 @@ static void ensure_scratch(qv_index* ix, int64_t nq, int k) {
                        hipHostMallocCoherent));
   // coherent: the search kernel writes the per-query hop, stop and evaluation
   // counts straight into it
-  HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_stage), sizeof(int32_t) * (size_t)(4 + 3 * cq),
+  HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_stage), sizeof(int32_t) * (size_t)(kStageHead + 3 * cq),
                        hipHostMallocCoherent));
   // coherent (not cached by the GPU): a host-buffer call copies its queries
   // here while the kernel already runs, and the kernel reads them in place
@@ -980,7 +982,12 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   float* d_dists = o.device_buffers ? dists : ix->d_dists;
   int32_t* d_found = (o.device_buffers && found) ? found : ix->d_found;
 
-  HIP_OK(hipMemsetAsync(ix->d_counters, 0, 64, ix->stream));
+  // Shared-pivot launches count the ended waves of each workgroup, so that a
+  // workgroup's last wave can take the pivot table over for its own LUT.
+  // Only with two waves or more per workgroup: the others' end then says that
+  // every ticket is out, so the last wave gets no further query.
+  const bool tail = lp.variant == QV_KERNEL_SHARED_PIVOTS && grid <= kMaxTailWorkgroups && ls.waves > 1;
+  HIP_OK(hipMemsetAsync(ix->d_counters, 0, 64 + (tail ? 4 * (size_t)grid : 0), ix->stream));
   // Static batches (StaticDispatch, search.cu:1703-1796): sequential batches of
   // num_blocks x queries_per_block queries, each admitted once the previous
   // one has completed; served by the same persistent launch, the host gating
@@ -1016,13 +1023,14 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   {
     int32_t* dev_stage = nullptr;
     HIP_OK(hipHostGetDevicePointer(reinterpret_cast<void**>(&dev_stage), ix->h_stage, 0));
-    a.out_hops = dev_stage + 4;
-    a.out_stopped = dev_stage + 4 + ix->cap_q;
-    a.out_evals = dev_stage + 4 + 2 * (size_t)ix->cap_q;
+    a.out_hops = dev_stage + kStageHead;
+    a.out_stopped = dev_stage + kStageHead + ix->cap_q;
+    a.out_evals = dev_stage + kStageHead + 2 * (size_t)ix->cap_q;
   }
   a.t_start = ix->d_tstart;
   a.t_end = ix->d_tend;
   a.counters = ix->d_counters;
+  a.wg_done = tail ? ix->d_counters + 16 : nullptr;
   a.feed_count = dev_ctrl;
   a.terminate = dev_ctrl + 1;
   a.ring = dev_ring;
@@ -1229,12 +1237,12 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   // The counters through the pinned staging buffer; the kernel wrote the hop
   // counts, stop flags and evaluation counts into it directly.
   int32_t* const st_counters = ix->h_stage;
-  int32_t* const st_hops = ix->h_stage + 4;
+  int32_t* const st_hops = ix->h_stage + kStageHead;
   int32_t* const st_stopped = st_hops + ix->cap_q;
   int32_t* const st_evals = st_stopped + ix->cap_q;
-  HIP_OK(hipMemcpyAsync(st_counters, ix->d_counters, 4 * sizeof(int32_t), hipMemcpyDeviceToHost, ix->stream));
+  HIP_OK(hipMemcpyAsync(st_counters, ix->d_counters, 5 * sizeof(int32_t), hipMemcpyDeviceToHost, ix->stream));
   HIP_OK(hipStreamSynchronize(ix->stream));
-  int32_t counters[4];
+  int32_t counters[5];
   std::memcpy(counters, st_counters, sizeof(counters));
   if (counters[2] & kErrSpinTimeout) fail(QV_ETIMEDOUT, "search kernel watchdog: feed wait exceeded its limit");
   if (timed_out || counters[1] < nq) {
@@ -1279,6 +1287,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     double ev_sum = 0;
     for (int64_t i = 0; i < nq; i++) ev_sum += st_evals[i];
     rep->total_evals = ev_sum;
+    rep->tail_queries = counters[4];
     rep->lat_avg_ms = std::accumulate(lat_ms.begin(), lat_ms.end(), 0.0) / (double)nq;
     // Order statistics by successive selection (linear time; a full sort of
     // 10k latencies costs about half a millisecond of host time per search).

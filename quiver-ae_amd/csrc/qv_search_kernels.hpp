@@ -53,7 +53,8 @@ struct SearchArgs {
   uint64_t* t_start;
   uint64_t* t_end;
   // dispatch
-  int32_t* counters;               // [0] next ticket, [1] done count, [2] error bits
+  int32_t* counters;               // [0] next ticket, [1] done count, [2] error bits, [3] ring
+                                   // position, [4] queries that entered tail mode
   const int32_t* feed_count;       // host-coherent, may be null (then nq)
   const int32_t* terminate;        // host-coherent, may be null
   int32_t* ring;                   // host-coherent completion ring, may be null
@@ -83,6 +84,9 @@ struct SearchArgs {
   // neighbour code table (optional, null: off): node v's neighbours' code
   // rows, slot order, at nbr_codes + v * max_m * num_chunks (zero past its degree)
   const uint8_t* nbr_codes;
+  // shared pivots: [gridDim.x] waves of each workgroup that have ended, zero
+  // at launch (null: no tail mode; never set for one-wave workgroups)
+  int32_t* wg_done;
 };
 
 enum : int32_t { kErrSpinTimeout = 1 };
@@ -93,6 +97,14 @@ enum : int32_t { kErrSpinTimeout = 1 };
 constexpr int kFeedLines = 64;  // one per lane of the publishing wave
 constexpr int64_t kFeedStride = 4352 / 8;  // in 8-byte words
 constexpr int64_t kFeedMirrorBytes = kFeedLines * kFeedStride * 8;
+
+// Workgroups of a shared-pivot launch whose ended waves are counted for
+// tail mode (one 32-bit count each, after the 64 bytes of launch counters).
+constexpr int kMaxTailWorkgroups = 4096;
+
+// 32-bit words ahead of the per-query counts in the host's pinned staging
+// buffer: the launch counters copied back after a search.
+constexpr int kStageHead = 8;
 
 // Dynamic LDS carve-up of one query (one wave), shared by the kernel and its
 // launcher.  Q = beam positions per lane: the register beam holds Q * 64 >= ef
@@ -238,6 +250,17 @@ struct Query {
   // rank search, renewed whenever the beam changes.
   uint64_t pk[Q > 1 ? Q - 1 : 1];
 
+  // Tail mode (shared pivots, 32 chunks of 4 dims): once this wave is the
+  // last of its workgroup with a query -- the ticket queue is empty and its
+  // workgroup mates have ended -- nothing else reads the pivot table, so the
+  // wave builds its own LUT over it (enter_tail) and finishes the query with
+  // table lookups instead of recomputing every entry: a lone wave's hop then
+  // costs what it costs in the per-query-LUT kernel.  The search loop has a
+  // copy for tail mode (hop<PF, true>), so the other copy keeps its hop.
+  // (Not at Q = 1: a beam of at most 64 ends its queries soon, and the
+  // probe's registers cost more there than the tail saves.)
+  static constexpr bool kTail = SC == 4 && MC == 32 && NPL == 1 && Q > 1;
+
   // The shared-pivot kernels serve dim = MC SC only (uniform chunks).
   static constexpr int kD = SC > 0 ? MC * SC : 0;
   // Loop-invariant byte offsets of this lane's loads inside a record: its
@@ -352,7 +375,8 @@ struct Query {
   // in cr.  Only loads move: every result is the same.
   static constexpr bool kRows = MC > 0 && MC % 16 == 0;  // code rows in registers (adc_load)
 
-  template <int PF>
+  // TL: the wave is in tail mode (kTail): the ADC reads its own LUT.
+  template <int PF, bool TL = false>
   __device__ __forceinline__ int32_t hop(int32_t v, Tk& tk, Rec& nr, CodeRow<MC>& cr, bool& have,
                                          int32_t nxt = -1) {
     if constexpr (NPL == 2) return hop2<PF == 1>(v, tk, nr);
@@ -392,10 +416,14 @@ struct Query {
       if constexpr (PF == 1) fetch(spec ? (int32_t)key_id(bu) : v, lane, nr);
       if constexpr (PF == 2) fetch(nxt >= 0 ? nxt : v, lane, nr);
       exact_and_topk(v, tk.part, rec, lane);
-      if constexpr (SC > 0)
-        d = adc_recompute<MC, SC, kQd>(cr, qd);
-      else
+      if constexpr (SC > 0) {
+        if constexpr (kTail && TL)
+          d = adc_sum_at0<MC, 1024>(cr);  // the tail LUT: chunk m's entries 4 KB apart
+        else
+          d = adc_recompute<MC, SC, kQd>(cr, qd);
+      } else {
         d = adc_sum_at0<MC>(cr);
+      }
       // the next node's code rows (lanes past its degree read row 0): the
       // guessed successor's (PF = 1) or nxt's (PF = 2)
       if constexpr (PF != 0) {
@@ -502,6 +530,59 @@ struct Query {
       rb += 8u * (uint32_t)(((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * S);
       rank_levels<S / 4>(rb, top8, c0);
     }
+  }
+
+  // The tail LUT over the pivot table at LDS address 0: entry (m, c) at byte
+  // 4096 m + 4 c, inside chunk m's own 4 KB of pivots (pivot (m, c) at
+  // 4096 m + 16 c).  Lane l computes codes l, l + 64, l + 128, l + 192 of each
+  // chunk; a chunk's 256 pivots are all read before any of its entries is
+  // written (the wavefront fence keeps the compiler from moving a write, which
+  // never aliases the writing lane's own reads, above another lane's read; the
+  // wave's LDS accesses complete in order), and other chunks' bytes are not
+  // touched.  An entry is the recompute's own chain (d = q' - p per dimension,
+  // acc = d0 d0, then fma in dimension order), so every sum keeps its bits.
+  __device__ __forceinline__ void build_tail_lut(int lane) {
+    typedef __attribute__((address_space(3))) qv_float4 lds_f4;
+    typedef __attribute__((address_space(3))) float lds_f32;
+#pragma unroll 1
+    for (int m = 0; m < MC; m++) {
+      // q' of the chunk's 4 dims: qd[m / 4], lanes 4 (m % 4) .. + 3 (load_query_dpp);
+      // the register is selected among values (opaque, so the select does not
+      // become an indexed access of qd, which only memory could serve)
+      float qr = qd[0];
+#pragma unroll
+      for (int k = 1; k < kQd; k++) {
+        float t = qd[k];
+        asm volatile("" : "+v"(t));
+        qr = (m >> 2) == k ? t : qr;
+      }
+      const int l0 = 4 * (m & 3);
+      const float q0 = read_lane_f32(qr, l0), q1 = read_lane_f32(qr, l0 + 1);
+      const float q2 = read_lane_f32(qr, l0 + 2), q3 = read_lane_f32(qr, l0 + 3);
+      lds_f4* const blk4 = (lds_f4*)(uintptr_t)(4096u * (uint32_t)m);
+      lds_f32* const blk1 = (lds_f32*)(uintptr_t)(4096u * (uint32_t)m);
+      qv_float4 p[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) p[j] = blk4[lane + 64 * j];
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      float e[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float d0 = q0 - p[j].x, d1 = q1 - p[j].y, d2 = q2 - p[j].z, d3 = q3 - p[j].w;
+        float acc = d0 * d0;
+        acc = __fmaf_rn(d1, d1, acc);
+        acc = __fmaf_rn(d2, d2, acc);
+        acc = __fmaf_rn(d3, d3, acc);
+        e[j] = acc;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) blk1[lane + 64 * j] = e[j];
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    }
+  }
+
+  __device__ __forceinline__ void enter_tail(int lane) {
+    if constexpr (kTail) build_tail_lut(lane);
   }
 
   // pk from the register copy.
@@ -1061,17 +1142,50 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     Taken<NPL> tk;
     CodeRow<MC> cr;
     bool have = false;
+    // Tail mode probe (kTail): from every 32nd hop on, the wave requests its
+    // workgroup's count of ended waves and reads it at its next probe, so the
+    // load never stalls a hop.  With every other wave of the workgroup ended
+    // it builds its LUT (enter_tail) and returns true, and the search goes on
+    // in the loop's tail-mode copy.  A wave ends once its ticket is past nq
+    // or the search is terminated (or its feed wait timed out, which fails the
+    // search), so this query is then the wave's last as well: the launcher
+    // passes wg_done only for workgroups of two waves or more, where that
+    // holds.  (The address goes through an opaque lane value so the load is a
+    // vector one: a scalar load's wait would also wait for the LDS traffic.
+    // Also reading the ticket counter here measured up to a fifth slower.)
+    constexpr bool kTail = Query<T, Q, MC, SC, NPL>::kTail;
+    int32_t probe_w = 0, probe_at = 32;
+    bool probing = false;
+    auto tail_probe = [&]() -> bool {
+      if constexpr (kTail) {
+        if (!a.wg_done) return false;
+        if (probing) {
+          probing = false;
+          if (read_lane_i32(probe_w, 0) >= (int)(blockDim.x / kWave) - 1) {
+            Qy.enter_tail(lane);
+            if (lane == 0) atomicAdd(&a.counters[4], 1);
+            return true;
+          }
+        } else if (step >= probe_at) {
+          const int z = opaque_lane() >> 8;  // 0
+          probe_w = __hip_atomic_load(a.wg_done + blockIdx.x + z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          probing = true;
+          probe_at = step + 32;
+        }
+      }
+      return false;
+    };
     // Expansion for the pipe lanes: nxt is the expansion expected next (-1:
     // not known), whose record (and rows) the hop requests once it has read
     // v's; pf is the node so requested, fetched again when the guess was wrong.
     int32_t pf = -1;
-    auto expand = [&](int32_t v, int32_t nxt) -> int32_t {
+    auto expand = [&](int32_t v, int32_t nxt, auto tl) -> int32_t {
       if (v != pf) {
         Qy.fetch(v, lane, nr);
         Qy.take(nr, tk, lane);
         have = false;
       }
-      const int32_t nx = Qy.template hop<2>(v, tk, nr, cr, have, nxt);
+      const int32_t nx = Qy.template hop<2, decltype(tl)::value>(v, tk, nr, cr, have, nxt);
       pf = NPL == 1 ? nxt : -1;
       return nx;
     };
@@ -1083,32 +1197,42 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       Qy.fetch(entry, lane, nr);
       Qy.take(nr, tk, lane);
       int32_t v = entry;
-      while (true) {
-        const int32_t nx = Qy.template hop<1>(v, tk, nr, cr, have);
-        log_hop(v);
-        ++step;
-        if (gpr && check()) {
-          stop = true;
-          break;
-        }
-        // per-step recall, after the early-exit test (kernel_q1.cuh:354-364)
-        if (sr) {
-          const int h = sr_hits();
-          if (h >= a.sr_required) {
-            sr_at = step;
-            sr_h = h;
+      // true: go on from v in tail mode
+      auto w1_loop = [&](auto tl) -> bool {
+        constexpr bool TL = decltype(tl)::value;
+        while (true) {
+          const int32_t nx = Qy.template hop<1, TL>(v, tk, nr, cr, have);
+          log_hop(v);
+          ++step;
+          bool to_tail = false;
+          if constexpr (!TL) to_tail = tail_probe();
+          if (gpr && check()) {
             stop = true;
-            break;
+            return false;
           }
+          // per-step recall, after the early-exit test (kernel_q1.cuh:354-364)
+          if (sr) {
+            const int h = sr_hits();
+            if (h >= a.sr_required) {
+              sr_at = step;
+              sr_h = h;
+              stop = true;
+              return false;
+            }
+          }
+          if (nx < 0) return false;
+          v = nx;
+          if (to_tail) return true;
         }
-        if (nx < 0) break;
-        v = nx;
+      };
+      if (w1_loop(BoolC<false>{})) {
+        if constexpr (kTail) w1_loop(BoolC<true>{});
       }
       goto finish;
     }
     {
     // ---- boot (kernel_q1.cuh:199-397)
-    int32_t first = expand(entry, -1);
+    int32_t first = expand(entry, -1, BoolC<false>{});
     log_hop(entry);
     step = 1;
     if (gpr && check()) {
@@ -1126,7 +1250,9 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     }
     uint32_t ready = stop ? 0u : (uint32_t)__ballot(lane < W && pipe_node != -1);
 
-    // ---- pipe loop, every issued lane served at once (kernel_q1.cuh:407-670)
+    // ---- pipe loop, every issued lane served at once (kernel_q1.cuh:407-670);
+    // tail mode is entered between rounds.  true: go on in tail mode
+    auto pipe_loop = [&](auto tl) -> bool {
     while (!stop && ready) {
       const uint32_t cur = ready;
       for (int w = 0; w < W; w++) {
@@ -1139,7 +1265,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
         const int f = __builtin_ctz(cur);
         const int32_t nxt = later ? read_lane_i32(pipe_node, __builtin_ctz(later))
                                   : (f == w ? -1 : read_lane_i32(pipe_node, f));
-        int32_t nx = expand(v, nxt);
+        int32_t nx = expand(v, nxt, tl);
         log_hop(v);
         ++step;
         if (gpr && check()) {
@@ -1155,6 +1281,14 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
         pipe_node = lane == w ? nx : pipe_node;
       }
       ready = (uint32_t)__ballot(lane < W && pipe_node != -1);
+      if constexpr (!decltype(tl)::value) {
+        if (ready && tail_probe()) return true;
+      }
+    }
+    return false;
+    };
+    if (pipe_loop(BoolC<false>{})) {
+      if constexpr (kTail) pipe_loop(BoolC<true>{});
     }
     }
 
@@ -1186,6 +1320,13 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       }
     }
     query_sync<SC>();
+  }
+  // This wave has no more queries: one more ended wave of its workgroup (the
+  // tail-mode probe of the others reads it).  Release at workgroup scope: the
+  // count is published after this wave's last pivot reads are done.
+  if constexpr (Query<T, Q, MC, SC, NPL>::kTail) {
+    if (a.wg_done && lane == 0)
+      __hip_atomic_fetch_add(a.wg_done + blockIdx.x, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 }
 

@@ -112,6 +112,8 @@ class SearchReport(C.Structure):
         ("kernel", C.c_int32),
         ("total_hops", C.c_double),
         ("total_evals", C.c_double),
+        ("tail_queries", C.c_int32),
+        ("reserved1", C.c_int32),
     ]
 
     def as_dict(self) -> dict:

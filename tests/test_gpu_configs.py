@@ -229,15 +229,18 @@ def test_c1_step_recall_matches_oracle(c1, threshold):
         assert 0 < (step >= 0).sum() < n  # both outcomes occur
 
 
+@pytest.mark.parametrize("blocks", [64, 640])
 @pytest.mark.parametrize("kernel", ["lut", "shared-pivots"])
-def test_c1_static_batches(c1, kernel):
+def test_c1_static_batches(c1, kernel, blocks):
     """Static dispatch (run_static_batch_search, search.cu:1703-1796): batches
     of num_blocks queries, each admitted when the previous has completed, every
     query of a batch taking the batch's wall time as its latency; answers equal
-    the oracle's."""
+    the oracle's.  64 slots are one-wave workgroups of the shared-pivot kernel
+    (no tail mode: a wave whose workgroup has no other wave may still get
+    queries), 640 slots three-wave ones (tail mode in the last batch)."""
     lib, L = c1["lib"], c1["L"]
-    n, blocks = 1000, 64
-    _say(f"[gpu] C1 static batches kernel={kernel}")
+    n = 1000
+    _say(f"[gpu] C1 static batches kernel={kernel} blocks={blocks}")
     o = lib.default_search_opts()
     o.early_exit = lib.QV_EXIT_NONE
     o.kernel = KERNEL[kernel]
@@ -254,10 +257,12 @@ def test_c1_static_batches(c1, kernel):
     lib.check(L.qv_last_hops(c1["h"], hops.ctypes.data, n))
     _same((ids, dists, found, hops), _oracle(c1, 128, "none", n=n), f"static {kernel}")
     assert rep.max_inflight == blocks
+    if kernel == "lut" or blocks == 64:
+        assert rep.tail_queries == 0
     lat = np.empty(n, np.float64)
     lib.check(L.qv_last_latencies(c1["h"], lat.ctypes.data, n))
     batches = [lat[b:b + blocks] for b in range(0, n, blocks)]
-    assert len(batches) == 16
+    assert len(batches) == (n + blocks - 1) // blocks
     for bl in batches:
         assert bl.min() == bl.max() > 0  # one wall time per batch
 
@@ -268,7 +273,10 @@ def test_c1_headline_path_with_code_table(c1, pipe, ef):
     """The path the throughput benchmark times: uint8, R = 64, M = 32, the
     neighbour code table (2 KB blocks of the 64 neighbours' code rows), the
     shared-pivot kernel (forced, and picked by `auto` for 2000 queries), pipe
-    widths 1 and 2, both early-exit policies."""
+    widths 1 and 2, both early-exit policies.  Beams past 64 (ef 288, 416)
+    finish the last query of a workgroup in tail mode (the pivot table turned
+    into that wave's own LUT): the report counts such queries, and their
+    answers are the oracle's like every other."""
     with _CodeTable(c1):
         for kernel in ("shared-pivots", "auto"):
             for policy in ("none", "gpruning"):
@@ -276,6 +284,10 @@ def test_c1_headline_path_with_code_table(c1, pipe, ef):
                 rc, got = _search(c1, c1["q"][:NQ], ef, policy, kernel, pipe=pipe)
                 assert rc == 0, c1["lib"].load().qv_last_error()
                 assert got[4].kernel == KERNEL["shared-pivots"]
+                if ef > 64:
+                    assert 0 < got[4].tail_queries < NQ, got[4].tail_queries
+                else:
+                    assert got[4].tail_queries == 0
                 want = _oracle(c1, ef, policy, pipe=pipe)
                 _same(got, want, f"table {kernel} ef={ef} W={pipe} {policy}")
                 assert abs(O.recall(got[0], c1["gt"], K) - O.recall(want[0], c1["gt"], K)) <= 0.002
@@ -298,6 +310,8 @@ def test_c1_topk_matches_oracle(c1, k):
                 rc, got = _search(c1, c1["q"][:n], 128, "none", kernel, k=k)
             assert rc == 0, c1["lib"].load().qv_last_error()
             _same(got, want, f"topk={k} {kernel} table={table}")
+            if kernel == "lut":
+                assert got[4].tail_queries == 0
 
 
 @pytest.mark.parametrize("batch,rate", [(1, 2e5), (16, 1e6), (256, 4e6)])
