@@ -54,6 +54,9 @@ struct qv_index {
   int32_t* h_ring = nullptr;   // [cap_q] completion ring (host-coherent)
   int32_t* h_stage = nullptr;  // pinned: counters [kStageHead], hops, stopped, evals [cap_q each]
   float* h_qstage = nullptr;   // pinned, coherent: a host-buffer call's queries [cap_q][d], read in place
+  // pinned, coherent: a host-buffer call's results as the kernel writes them,
+  // ids [cap_q][cap_k] int32, dists [cap_q][cap_k] float, found [cap_q] int32
+  void* h_results = nullptr;
   std::vector<int32_t> last_hops;
   std::vector<double> last_lat_ms;  // per-query latency of the last search, query order
   // host copies of the PQ tables (for saving the index)

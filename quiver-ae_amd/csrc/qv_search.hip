@@ -301,6 +301,7 @@ static void free_scratch(qv_index* ix) {
   hipHostFree(ix->h_ring);
   hipHostFree(ix->h_stage);
   hipHostFree(ix->h_qstage);
+  hipHostFree(ix->h_results);
   ix->d_queries = nullptr;
   ix->d_ids = ix->d_found = ix->d_hops = ix->d_stopped = ix->d_evals = nullptr;
   ix->d_dists = nullptr;
@@ -308,6 +309,7 @@ static void free_scratch(qv_index* ix) {
   ix->h_ring = nullptr;
   ix->h_stage = nullptr;
   ix->h_qstage = nullptr;
+  ix->h_results = nullptr;
   ix->cap_q = 0;
   ix->cap_k = 0;
 }
@@ -349,6 +351,10 @@ static void ensure_scratch(qv_index* ix, int64_t nq, int k) {
   // here while the kernel already runs, and the kernel reads them in place
   HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&ix->h_qstage), sizeof(float) * (size_t)cq * d,
                        hipHostMallocCoherent));
+  // coherent: a host-buffer call's kernel writes its results here, and the
+  // host copies them out once the launch has ended (one host memcpy instead of
+  // a device-to-pageable copy through the runtime's bounce buffers)
+  HIP_OK(hipHostMalloc(&ix->h_results, sizeof(int32_t) * (size_t)cq * (2 * (size_t)ck + 1), hipHostMallocCoherent));
   ix->cap_q = cq;
   ix->cap_k = ck;
 }
@@ -978,9 +984,21 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   float* dev_qstage = nullptr;
   if (stage_q) HIP_OK(hipHostGetDevicePointer(reinterpret_cast<void**>(&dev_qstage), ix->h_qstage, 0));
   const float* d_q = o.device_buffers ? queries : (stage_q ? dev_qstage : ix->d_queries);
+  // Host buffers: the kernel writes ids, distances and found counts straight
+  // into pinned host memory (h_results), laid out [nq][topk] as the caller's.
   int32_t* d_ids = o.device_buffers ? ids : ix->d_ids;
   float* d_dists = o.device_buffers ? dists : ix->d_dists;
   int32_t* d_found = (o.device_buffers && found) ? found : ix->d_found;
+  int32_t* const h_ids = static_cast<int32_t*>(ix->h_results);
+  float* const h_dists = reinterpret_cast<float*>(h_ids + (size_t)ix->cap_q * ix->cap_k);
+  int32_t* const h_found = h_ids + (size_t)ix->cap_q * ix->cap_k * 2;
+  if (!o.device_buffers) {
+    int32_t* dev_res = nullptr;
+    HIP_OK(hipHostGetDevicePointer(reinterpret_cast<void**>(&dev_res), ix->h_results, 0));
+    d_ids = dev_res;
+    d_dists = reinterpret_cast<float*>(dev_res + (size_t)ix->cap_q * ix->cap_k);
+    d_found = dev_res + (size_t)ix->cap_q * ix->cap_k * 2;
+  }
 
   // Shared-pivot launches count the ended waves of each workgroup, so that a
   // workgroup's last wave can take the pivot table over for its own LUT.
@@ -1087,6 +1105,10 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   hipLaunchKernelGGL(lp.kern, dim3(grid), dim3(kWave * ls.waves), (size_t)ls.lds, ix->stream, a);
   HIP_OK(hipGetLastError());
   HIP_OK(hipEventRecord(ix->ev1, ix->stream));
+  // The launch counters follow the kernel into pinned memory on its stream, so
+  // they are there once the stream is idle (no round trip after the wait).
+  int32_t* const st_counters = ix->h_stage;
+  HIP_OK(hipMemcpyAsync(st_counters, ix->d_counters, 5 * sizeof(int32_t), hipMemcpyDeviceToHost, ix->stream));
 
   const bool has_deadline = o.timeout_s > 0;
   const auto deadline = t0 + std::chrono::duration_cast<clock::duration>(
@@ -1225,23 +1247,21 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     else
       std::this_thread::sleep_for(std::chrono::microseconds(50));
   }
+  // The stream is idle: the kernel's writes to pinned memory (results, counts)
+  // and the counters' copy behind it are all visible.
+  HIP_OK(hipStreamSynchronize(ix->stream));
   if (!o.device_buffers) {
-    HIP_OK(hipMemcpyAsync(ids, d_ids, sizeof(int32_t) * (size_t)nq * topk, hipMemcpyDeviceToHost, ix->stream));
-    HIP_OK(hipMemcpyAsync(dists, d_dists, sizeof(float) * (size_t)nq * topk, hipMemcpyDeviceToHost, ix->stream));
-    if (found)
-      HIP_OK(hipMemcpyAsync(found, d_found, sizeof(int32_t) * (size_t)nq, hipMemcpyDeviceToHost, ix->stream));
-    HIP_OK(hipStreamSynchronize(ix->stream));
+    std::memcpy(ids, h_ids, sizeof(int32_t) * (size_t)nq * topk);
+    std::memcpy(dists, h_dists, sizeof(float) * (size_t)nq * topk);
+    if (found) std::memcpy(found, h_found, sizeof(int32_t) * (size_t)nq);
   }
   const auto t1 = clock::now();
 
-  // The counters through the pinned staging buffer; the kernel wrote the hop
-  // counts, stop flags and evaluation counts into it directly.
-  int32_t* const st_counters = ix->h_stage;
+  // The kernel wrote the hop counts, stop flags and evaluation counts into the
+  // pinned staging buffer directly.
   int32_t* const st_hops = ix->h_stage + kStageHead;
   int32_t* const st_stopped = st_hops + ix->cap_q;
   int32_t* const st_evals = st_stopped + ix->cap_q;
-  HIP_OK(hipMemcpyAsync(st_counters, ix->d_counters, 5 * sizeof(int32_t), hipMemcpyDeviceToHost, ix->stream));
-  HIP_OK(hipStreamSynchronize(ix->stream));
   int32_t counters[5];
   std::memcpy(counters, st_counters, sizeof(counters));
   if (counters[2] & kErrSpinTimeout) fail(QV_ETIMEDOUT, "search kernel watchdog: feed wait exceeded its limit");
