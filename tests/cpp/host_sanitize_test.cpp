@@ -3,11 +3,13 @@
 // with AddressSanitizer and UndefinedBehaviorSanitizer (g++/gcc only; no GPU
 // code is compiled or run).  It builds small uint8 and float indexes and a nav
 // graph, reads them back through the same readers the library uses, searches
-// them with the oracle (plain, gpruning, pipe width 2, nav entry), and drives
-// the error paths with malformed files and arguments.  Any sanitizer report
+// them with the oracle (plain, gpruning, pipe width 2, nav entry), drives
+// the error paths with malformed files and arguments, and checks the search
+// report's order statistics (qv_order_stats.hpp) against a full sort.  Any sanitizer report
 // aborts the program (-fno-sanitize-recover=all); a failed check exits 1.
 //
 // usage: host_sanitize_test WORK_DIR
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -19,6 +21,7 @@
 
 #include "qv_common.hpp"
 #include "qv_oracle.h"
+#include "qv_order_stats.hpp"
 #include "quiver_hip.h"
 
 namespace {
@@ -112,6 +115,55 @@ void truncate_copy(const std::string& from, const std::string& to, size_t keep) 
 }
 
 }  // namespace
+
+// select_ranks against std::sort: n from 1 to 100k; latencies spread and
+// clustered, integer-valued with many ties, all equal, zeros, negatives and
+// denormals; ranks at the report's percentiles, both ends and at random.
+void check_order_stats() {
+  uint64_t s = 0x0DDBA11;
+  auto next = [&]() {
+    s ^= s << 13;
+    s ^= s >> 7;
+    s ^= s << 17;
+    return s;
+  };
+  auto unit = [&]() { return (double)(next() >> 11) * (1.0 / 9007199254740992.0); };
+  int cases = 0, bad = 0;
+  for (size_t n : {(size_t)1, (size_t)2, (size_t)3, (size_t)17, (size_t)1000, (size_t)10000, (size_t)100000}) {
+    for (int kind = 0; kind < 7; kind++) {
+      std::vector<double> v(n);
+      for (size_t i = 0; i < n; i++) {
+        const double u = unit();
+        switch (kind) {
+          case 0: v[i] = 0.3 + 4.0 * u; break;                             // a batch's latencies
+          case 1: v[i] = std::exp(8.0 * u - 4.0); break;                   // many binades
+          case 2: v[i] = (double)(next() % 7); break;                      // few values, many ties
+          case 3: v[i] = 1.25; break;                                      // all equal
+          case 4: v[i] = u < 0.5 ? 0.0 : u; break;                         // zeros
+          case 5: v[i] = 2.0 * u - 1.0; break;                             // negatives
+          default: v[i] = (u < 0.3 ? 4.9e-324 * (double)(next() % 5) : u * 1e-300); break;  // denormals
+        }
+      }
+      std::vector<double> sorted = v;
+      std::sort(sorted.begin(), sorted.end());
+      std::vector<size_t> r = {n / 2, (size_t)(0.9 * (double)n), (size_t)(0.99 * (double)n),
+                               (size_t)(0.999 * (double)n), n - 1, 0, (size_t)(next() % n), (size_t)(next() % n)};
+      for (size_t& x : r) x = std::min(x, n - 1);
+      std::vector<double> out(r.size());
+      const std::vector<double> before = v;
+      qv::select_ranks(v.data(), n, r.data(), (int)r.size(), out.data());
+      cases++;
+      bool ok = v == before;
+      for (size_t j = 0; j < r.size(); j++) ok = ok && out[j] == sorted[r[j]];
+      if (!ok) {
+        bad++;
+        std::fprintf(stderr, "order statistics differ: n=%zu kind=%d\n", n, kind);
+      }
+    }
+  }
+  expect(bad == 0, "select_ranks equals the sorted order statistics");
+  expect(cases == 49, "order statistics cases run");
+}
 
 int main(int argc, char** argv) {
   if (argc != 2) {
@@ -228,6 +280,8 @@ int main(int argc, char** argv) {
   expect(qv_read_layout((work / "missing_disk.index").c_str(), "bogus", &info) != QV_OK, "bad type name");
   char a[8], b2[8];
   expect(qv_find_index_files(work.c_str(), a, b2, sizeof(a)) != QV_OK, "short path buffer or no index");
+
+  check_order_stats();
 
   if (g_failures) {
     std::fprintf(stderr, "%d check(s) failed\n", g_failures);

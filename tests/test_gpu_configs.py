@@ -121,6 +121,20 @@ class _CodeTable:
         return False
 
 
+def _percentiles_are_order_statistics(rep, lat):
+    """The report's P50 / P90 / P99 / P99.9 / max are the per-query latencies'
+    elements of ranks n 50 / 100, n 90 / 100, n 99 / 100 (integer), floor(n 0.999)
+    and n - 1 in ascending order, exactly as the reference indexes its sorted
+    latencies (search.cu:1141-1145)."""
+    s = np.sort(lat)
+    n = len(s)
+    for r, got in ((n * 50 // 100, rep.lat_p50_ms), (n * 90 // 100, rep.lat_p90_ms),
+                   (n * 99 // 100, rep.lat_p99_ms), (min(n - 1, int(n * 0.999)), rep.lat_p999_ms)):
+        assert got == s[r], (r, got)
+    assert rep.lat_max_ms == s[-1]
+    assert abs(rep.lat_avg_ms - s.mean()) <= 1e-9 * s.mean()
+
+
 def _same(got, want, what):
     ids, dists, found, hops = got[:4]
     oids, odists, ofound, ohops = want
@@ -342,6 +356,7 @@ def test_c1_open_loop_arrival(c1, batch, rate):
     lat = np.empty(n, np.float64)
     lib.check(L.qv_last_latencies(c1["h"], lat.ctypes.data, n))
     assert lat.min() > 0 and rep.lat_p99_ms > 0
+    _percentiles_are_order_statistics(rep, lat)
     # the static and batch admissions refuse an arrival rate
     o.admission = lib.QV_ADMIT_STATIC
     rc = L.qv_search(c1["h"], q.ctypes.data, 16, DIM, K, 128, C.byref(o), ids.ctypes.data, dists.ctypes.data,
@@ -356,7 +371,10 @@ def test_c1_host_queries_change_between_calls(c1, admission):
     reads each query there.  Consecutive calls with different queries (a later
     slice, another one, then the first queries in reverse order; 1,500, 1,000
     and 700 queries, so both kernels) must each return what the device-buffer
-    path returns for the same queries."""
+    path returns for the same queries; the results come back through the
+    pinned buffer the kernel writes them into, and the report's percentiles are
+    the order statistics of the per-query latencies (ties included: a static
+    batch's queries share one latency)."""
     lib, L = c1["lib"], c1["L"]
     adm = lib.QV_ADMIT_STREAMING if admission == "streaming" else lib.QV_ADMIT_STATIC
     sets = [c1["q"][NQ:NQ + 1500], c1["q"][NQ + 1500:NQ + 2500], c1["q"][:700][::-1]]
@@ -372,6 +390,9 @@ def test_c1_host_queries_change_between_calls(c1, admission):
         rep = lib.SearchReport()
         lib.check(L.qv_search(c1["h"], qs.ctypes.data, n, DIM, K, 128, C.byref(o), ids.ctypes.data,
                               dists.ctypes.data, None, C.byref(rep)))
+        lat = np.empty(n, np.float64)
+        lib.check(L.qv_last_latencies(c1["h"], lat.ctypes.data, n))
+        _percentiles_are_order_statistics(rep, lat)
         d_q = lib.DeviceBuffer(qs.nbytes).upload(qs)
         d_i, d_d = lib.DeviceBuffer(n * K * 4), lib.DeviceBuffer(n * K * 4)
         o.device_buffers = 1
