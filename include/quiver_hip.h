@@ -262,9 +262,9 @@ int qv_search(qv_index* index, const float* queries, int64_t nq, int32_t dim,
  * serving loops, harnesses that forbid hipMalloc): qv_search with every query
  * admitted at launch, all of d_queries / d_ids / d_dists / d_found (may be
  * NULL) device pointers, and the search's scratch (dispatch counters,
- * per-query hop, evaluation and early-exit counts) taken from one fixed
- * device array of QV_NOALLOC_SCRATCH_BYTES per GPU, held until the process
- * ends.  It calls no hipMalloc, hipHostMalloc, hipFree or memset of any kind.
+ * per-query hop, evaluation and early-exit counts, the shared-pivot kernel's
+ * count of ended waves per workgroup) taken from one fixed device array of
+ * QV_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends.  It calls no hipMalloc, hipHostMalloc, hipFree or memset of any kind.
  * It is synchronous: it runs on the handle's own stream and returns once the
  * results are in the caller's device buffers, so it cannot be captured into
  * a caller's HIP graph.  Limits: 1..QV_NOALLOC_MAX_QUERIES queries per call
@@ -274,7 +274,7 @@ int qv_search(qv_index* index, const float* queries, int64_t nq, int32_t dim,
  * GPU share its array and are serialised by a lock per GPU; calls on
  * different GPUs run independently.  The report has no latency percentiles
  * (queries are not stamped). */
-#define QV_NOALLOC_SCRATCH_BYTES (12 * 1024 * 1024 + 256)
+#define QV_NOALLOC_SCRATCH_BYTES (12 * 1024 * 1024 + 256 + 16 * 1024)
 #define QV_NOALLOC_MAX_QUERIES (1024 * 1024)
 int qv_search_noalloc(qv_index* index, const float* d_queries, int64_t nq, int32_t dim,
                       int32_t topk, int32_t ef_search, const qv_search_opts* opts,

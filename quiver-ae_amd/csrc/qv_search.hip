@@ -243,6 +243,7 @@ LaunchShape shape_launch(const LaunchPlan& lp, int64_t slots, int num_cus) {
 //   [256, +4 kNoAllocMaxQueries) per-query hop counts
 //   [.., +4 kNoAllocMaxQueries)  per-query ADC evaluation counts
 //   [.., +4 kNoAllocMaxQueries)  per-query early-exit flags
+//   [.., +4 kMaxTailWorkgroups)  ended waves per workgroup (shared-pivot tail mode)
 // Host code never uses the symbol's name as an address: each device's copy is
 // looked up once with hipGetSymbolAddress.
 constexpr int64_t kNoAllocBytes = QV_NOALLOC_SCRATCH_BYTES;
@@ -250,7 +251,8 @@ constexpr int64_t kNoAllocMaxQueries = QV_NOALLOC_MAX_QUERIES;
 constexpr int64_t kNoAllocHopsOff = 256;
 constexpr int64_t kNoAllocEvalsOff = kNoAllocHopsOff + 4 * kNoAllocMaxQueries;
 constexpr int64_t kNoAllocStoppedOff = kNoAllocEvalsOff + 4 * kNoAllocMaxQueries;
-static_assert(kNoAllocStoppedOff + 4 * kNoAllocMaxQueries <= kNoAllocBytes, "scratch holds every count");
+constexpr int64_t kNoAllocWgDoneOff = kNoAllocStoppedOff + 4 * kNoAllocMaxQueries;
+static_assert(kNoAllocWgDoneOff + 4 * kMaxTailWorkgroups <= kNoAllocBytes, "scratch holds every count");
 __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
 
 // Zero fill by vector stores: the allocation-free entry point calls no
@@ -1403,6 +1405,10 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
   int32_t* const evals = reinterpret_cast<int32_t*>(base + kNoAllocEvalsOff);
   int32_t* const stopped = reinterpret_cast<int32_t*>(base + kNoAllocStoppedOff);
   zero_words(base, kNoAllocHopsOff, ix->stream);  // counters and the 64-bit totals
+  // tail mode as in search(): workgroups of two waves or more
+  const bool tail = lp.variant == QV_KERNEL_SHARED_PIVOTS && ls.grid <= kMaxTailWorkgroups && ls.waves > 1;
+  int32_t* const wg_done = reinterpret_cast<int32_t*>(base + kNoAllocWgDoneOff);
+  if (tail) zero_words(base + kNoAllocWgDoneOff, 4 * (int64_t)ls.grid, ix->stream);
 
   SearchArgs a = base_args(ix);
   a.queries = d_queries;
@@ -1423,6 +1429,7 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
   a.t_start = nullptr;
   a.t_end = nullptr;
   a.counters = counters;
+  a.wg_done = tail ? wg_done : nullptr;
   a.feed_count = nullptr;  // every query admitted at launch
   a.terminate = nullptr;
   a.ring = nullptr;
@@ -1442,7 +1449,7 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
   HIP_OK(hipGetLastError());
   HIP_OK(hipStreamSynchronize(ix->stream));
   const auto t1 = std::chrono::steady_clock::now();
-  int32_t c[4] = {0, 0, 0, 0};
+  int32_t c[5] = {0, 0, 0, 0, 0};
   unsigned long long tot[3] = {0, 0, 0};
   HIP_OK(hipMemcpy(c, counters, sizeof(c), hipMemcpyDeviceToHost));
   HIP_OK(hipMemcpy(tot, totals, sizeof(tot), hipMemcpyDeviceToHost));
@@ -1462,6 +1469,7 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
     rep->total_evals = (double)tot[1];
     rep->avg_hops = (double)tot[0] / (double)nq;
     rep->early_stopped = (int32_t)tot[2];
+    rep->tail_queries = c[4];
   }
 }
 

@@ -34,7 +34,7 @@ QV_ADMIT_STATIC = 2
 QV_GRAPH_HBM = 0
 QV_GRAPH_HOST = 1
 QV_STREAM_READ_BLOCKS = 4096
-QV_NOALLOC_SCRATCH_BYTES = 12 * 1024 * 1024 + 256
+QV_NOALLOC_SCRATCH_BYTES = 12 * 1024 * 1024 + 256 + 16 * 1024
 QV_NOALLOC_MAX_QUERIES = 1024 * 1024
 QV_KERNEL_AUTO = 0
 QV_KERNEL_LUT = 1

@@ -139,7 +139,9 @@ def test_noalloc_equals_search_float(lib, small_f32_index):
 def test_noalloc_many_slots_on_a_larger_index(lib):
     """600k points and 1024 requested query slots: each kernel launches all of
     them (the scratch holds only counts, nothing per slot or per point) and
-    equals qv_search."""
+    equals qv_search; at ef = 128 the shared-pivot launch (four-wave
+    workgroups) finishes queries in tail mode, its ended-wave counts in the
+    fixed array too."""
     import quiver  # noqa: F401
 
     L = lib.load()
@@ -163,6 +165,11 @@ def test_noalloc_many_slots_on_a_larger_index(lib):
                 want, got, r0, r1 = _pair(lib, h, dev, n_q, 64, kernel, num_blocks=1024)
                 _check(want, got, r0, r1, f"{kernel} 1024 slots n={n_q}")
                 assert r0.num_blocks == r1.num_blocks == 1024
+        for n_q in (3000, 1500):
+            _say(f"[gpu] noalloc 600k points shared-pivots ef=128 1024 slots n={n_q}")
+            want, got, r0, r1 = _pair(lib, h, dev, n_q, 128, "shared-pivots", num_blocks=1024)
+            _check(want, got, r0, r1, f"shared-pivots ef=128 1024 slots n={n_q}")
+            assert 0 < r1.tail_queries < n_q and 0 < r0.tail_queries < n_q, (r0.tail_queries, r1.tail_queries)
     finally:
         L.qv_index_close(h)
 
