@@ -16,7 +16,7 @@ constexpr int kNumPivots = 256;       // PQSearchData::num_pivots (pq_search.hpp
 constexpr int kMaxDegree = 128;       // two neighbour slots per wavefront lane
 constexpr int kMaxBuildDegree = 128;  // the GPU builder: a list in two slots per lane
 constexpr int kMaxEf = 1024;          // 16 beam positions per lane
-constexpr int kMaxTopk = 64;          // one top-k entry per lane
+constexpr int kMaxTopk = 1024;        // 64 in registers, the rest in LDS (per-query-LUT kernel)
 constexpr int kMaxPipeWidth = 16;     // bin/common/cli_validation.hpp:9
 constexpr int kMaxQueriesPerBlock = 8; // bin/common/cli_validation.hpp:10
 

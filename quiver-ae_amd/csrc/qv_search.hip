@@ -764,19 +764,29 @@ static int occupancy(int device, int lds_cu, KernelFn k, int waves, int lds) {
 // table read per code byte instead of a recompute); the shared pivots pay
 // when twice the queries per CU keep twice the random rows in flight.
 // `want` (QV_KERNEL_*) forces one; a forced shared-pivot plan the index or the
-// CU cannot take is QV_EUNSUPPORTED.
-LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
+// CU cannot take is QV_EUNSUPPORTED.  A top-k above 64 runs on the
+// per-query-LUT kernel only (entries past 64 in its LDS).
+LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need, int topk) {
   if (want != QV_KERNEL_AUTO && want != QV_KERNEL_LUT && want != QV_KERNEL_SHARED_PIVOTS)
     fail(QV_EINVAL, "search kernel must be QV_KERNEL_AUTO, QV_KERNEL_LUT or QV_KERNEL_SHARED_PIVOTS");
-  const int P = beam_chunks(ef);
+  const bool wide = topk > kRegTopk;
+  const int P = wide ? wide_beam_chunks(ef) : beam_chunks(ef);
   const int M = ix->M, d = (int)ix->lay.num_dims;
   LaunchPlan lut;
-  lut.kern = pick_kernel(ix->lay.data_type, P, M, slots_per_lane(ix->lay.max_m0));
+  lut.kern = wide ? pick_kernel_wide(ix->lay.data_type, P, M, slots_per_lane(ix->lay.max_m0))
+                  : pick_kernel(ix->lay.data_type, P, M, slots_per_lane(ix->lay.max_m0));
+  if (!lut.kern) fail(QV_EUNSUPPORTED, "no search kernel for this top-k, degree and ef");
   lut.waves = 1;
-  lut.lds = lds_plan(M, d, P, true, ef).total;
+  lut.lds = lds_plan(M, d, P, true, ef, topk).total;
   lut.slots_per_cu = occupancy(ix->device, ix->lds_cu, lut.kern, 1, lut.lds);
   if (want == QV_KERNEL_LUT) return lut;
   const bool forced = want == QV_KERNEL_SHARED_PIVOTS;
+  if (wide) {
+    if (forced)
+      fail(QV_EUNSUPPORTED, "the shared-pivot kernel keeps at most 64 results per query; topk=" +
+                                std::to_string(topk) + " runs on the per-query-LUT kernel");
+    return lut;
+  }
   if (!forced && lut.slots_per_cu > 0 && need <= (int64_t)lut.slots_per_cu * ix->num_cus) return lut;
   const int sc = M == 32 ? 4 : (M == 48 ? 2 : 0);
   bool uniform = sc > 0 && d == M * sc && (int)ix->h_chunk_off.size() == M + 1;
@@ -787,7 +797,7 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
   }
   const int lds_cu = ix->lds_cu;
   const int Psp = beam_chunks_sp(ef);
-  const int per_wave = lds_plan(M, d, Psp, false, ef).total;
+  const int per_wave = lds_plan(M, d, Psp, false, ef, topk).total;
   const int waves = std::min(sp_max_waves(Psp, slots_per_lane(ix->lay.max_m0)), (lds_cu - piv_bytes(d)) / per_wave);
   if (!forced && waves <= lut.slots_per_cu) return lut;
   LaunchPlan sp;
@@ -805,7 +815,7 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need) {
   return sp;
 }
 
-int slots_per_cu(qv_index* ix, int ef) { return launch_plan(ix, ef, QV_KERNEL_AUTO, INT64_MAX).slots_per_cu; }
+int slots_per_cu(qv_index* ix, int ef) { return launch_plan(ix, ef, QV_KERNEL_AUTO, INT64_MAX, 10).slots_per_cu; }
 
 // page = floor(v / npp) as (v * m) >> k with k = 32 + ceil(log2 npp) and
 // m = ceil(2^k / npp): the error term v (m npp - 2^k) / (npp 2^k) stays below
@@ -857,7 +867,8 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
   if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 1024]");
   HIP_OK(hipSetDevice(ix->device));
   ensure_scratch(ix, nq, 1);
-  const LaunchPlan lp = launch_plan(ix, ef, QV_KERNEL_AUTO, num_blocks > 0 ? std::min<int64_t>(nq, num_blocks) : nq);
+  const LaunchPlan lp =
+      launch_plan(ix, ef, QV_KERNEL_AUTO, num_blocks > 0 ? std::min<int64_t>(nq, num_blocks) : nq, 1);
   if (lp.slots_per_cu <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
   int nb = num_blocks > 0 ? num_blocks : lp.slots_per_cu * ix->num_cus;
   nb = (int)std::min<int64_t>(std::min<int64_t>(nb, nq), (int64_t)lp.slots_per_cu * ix->num_cus);
@@ -918,7 +929,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   if (dim != L.num_dims)
     fail(QV_EINVAL, "Query dimension mismatch: queries have " + std::to_string(dim) +
                         " dims, but the index expects " + std::to_string(L.num_dims));
-  if (topk <= 0 || topk > kMaxTopk) fail(QV_EINVAL, "topk must be in [1, 64]");
+  if (topk <= 0 || topk > kMaxTopk) fail(QV_EINVAL, "topk must be in [1, 1024]");
   if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 1024]");
   if (o.pipe_width < 1 || o.pipe_width > kMaxPipeWidth) fail(QV_EINVAL, "--pipe-width must be in [1, 16]");
   if (o.queries_per_block < 1 || o.queries_per_block > kMaxQueriesPerBlock)
@@ -958,7 +969,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
   // offered rate times a nominal 1.5 ms in the system, plus one arrival.
   int64_t need = std::min<int64_t>(nq, requested);
   if (open_loop) need = std::min<int64_t>(need, (int64_t)std::ceil(o.arrival_qps * 1.5e-3) + o.arrival_batch);
-  const LaunchPlan lp = launch_plan(ix, ef, o.kernel, need);
+  const LaunchPlan lp = launch_plan(ix, ef, o.kernel, need, topk);
   const int spc = lp.slots_per_cu;
   if (spc <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
   // Query slots (search.cu:393-399): num_blocks x queries_per_block.  Each slot
@@ -1377,7 +1388,7 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
   if (dim != L.num_dims)
     fail(QV_EINVAL, "Query dimension mismatch: queries have " + std::to_string(dim) +
                         " dims, but the index expects " + std::to_string(L.num_dims));
-  if (topk <= 0 || topk > kMaxTopk) fail(QV_EINVAL, "topk must be in [1, 64]");
+  if (topk <= 0 || topk > kMaxTopk) fail(QV_EINVAL, "topk must be in [1, 1024]");
   if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 1024]");
   if (o.pipe_width < 1 || o.pipe_width > kMaxPipeWidth) fail(QV_EINVAL, "--pipe-width must be in [1, 16]");
   if (o.queries_per_block < 1 || o.queries_per_block > kMaxQueriesPerBlock)
@@ -1394,7 +1405,7 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
   std::lock_guard<std::mutex> dlk(nd.mu);  // calls on one GPU share its array
   uint8_t* const base = nd.ptr;
   const int64_t requested = o.num_blocks > 0 ? (int64_t)o.num_blocks * o.queries_per_block : INT64_MAX;
-  const LaunchPlan lp = launch_plan(ix, ef, o.kernel, std::min<int64_t>(nq, requested));
+  const LaunchPlan lp = launch_plan(ix, ef, o.kernel, std::min<int64_t>(nq, requested), topk);
   if (lp.slots_per_cu <= 0) fail(QV_EUNSUPPORTED, "search kernel does not fit on a compute unit");
   const int64_t slots = (int64_t)(o.num_blocks > 0 ? o.num_blocks : lp.slots_per_cu * ix->num_cus) * o.queries_per_block;
   const int64_t launched = std::min<int64_t>(std::min<int64_t>(slots, (int64_t)lp.slots_per_cu * ix->num_cus), nq);

@@ -115,8 +115,15 @@ constexpr int kStageHead = 8;
 // are only read once, into registers (load_query_dpp, load_query_pre),
 // before the first hop.
 struct LdsPlan {
-  int lut_off, qc_off, qu_off, beam_off, count_off, total;
+  int lut_off, qc_off, qu_off, beam_off, count_off, wide_off, total;
 };
+
+// Top-k entries a wave holds in its registers: entry i in lane i.  The
+// per-query-LUT kernel keeps entries 64 .. k - 1 of a larger k in LDS after
+// the rest of the query's area (wide_topk entries of 8 bytes: the distances,
+// then the ids); the shared-pivot kernel takes k <= 64 only.
+constexpr int kRegTopk = 64;
+__host__ __device__ inline int wide_topk(int topk) { return topk > kRegTopk ? (topk - kRegTopk + 7) & ~7 : 0; }
 
 // LDS beam entries: Q * 64 with the per-query LUT (its table, not the beam,
 // limits the queries per CU); ef rounded up to 8 with shared pivots, where the
@@ -129,7 +136,7 @@ __host__ __device__ inline int beam_cap(int ef, int Q, bool lut) { return lut ? 
 // CU.  The other kernels add the candidates one at a time.
 __host__ __device__ constexpr bool rank_counts(bool lut, int Q) { return lut && Q <= 7; }
 
-__host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool lut, int ef) {
+__host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool lut, int ef, int topk) {
   LdsPlan p;
   p.lut_off = 0;
   p.qc_off = p.lut_off + (lut ? num_chunks * kPivots * 4 : 0);
@@ -141,6 +148,8 @@ __host__ __device__ inline LdsPlan lds_plan(int num_chunks, int dim, int Q, bool
   p.count_off = p.beam_off + beam_bytes;  // (rank_counts: no overlay)
   p.total = p.beam_off + (overlay && 2 * dpad * 4 > beam_bytes ? 2 * dpad * 4 : beam_bytes) +
             (rank_counts(lut, Q) ? beam_cap(ef, Q, lut) * 4 : 0);
+  p.wide_off = p.total;
+  if (lut) p.total += wide_topk(topk) * 8;
   return p;
 }
 
@@ -165,6 +174,12 @@ KernelFn pick_kernel_r128(int dtype, int Q, int M);
 KernelFn pick_kernel_sp_r128(int dtype, int Q, int M);
 KernelFn pick_kernel_deep(int dtype, int Q, int M);
 KernelFn pick_kernel_sp_deep(int dtype, int Q, int M);
+// Per-query-LUT kernels for a top-k above 64 (qv_search_wide.hip): Q = 2, 4,
+// 7, 10 or 16 (from wide_beam_chunks), one or two neighbour slots per lane.
+KernelFn pick_kernel_wide(int dtype, int Q, int M, int npl);
+__host__ __device__ inline int wide_beam_chunks(int ef) {
+  return ef <= 128 ? 2 : (ef <= 256 ? 4 : (ef <= 448 ? 7 : (ef <= 640 ? 10 : 16)));
+}
 
 }  // namespace sk
 }  // namespace qv
@@ -198,10 +213,12 @@ struct Taken {
 
 // SC = 0: per-query LUT in LDS; SC > 0: LUT entries recomputed from the
 // shared pivots (chunks of SC dimensions).  NPL = 1: R <= 64, lane l owns
-// neighbour l; NPL = 2: R <= 128, lane l also owns neighbour l + 64.
-template <class T, int Q, int MC, int SC, int NPL>
+// neighbour l; NPL = 2: R <= 128, lane l also owns neighbour l + 64.  WK: a
+// top-k above 64 (per-query LUT only), entries past the 64th in LDS.
+template <class T, int Q, int MC, int SC, int NPL, bool WK = false>
 struct Query {
   static_assert(NPL == 1 || NPL == 2, "one or two neighbours per lane");
+  static_assert(!WK || SC == 0, "a top-k above 64 runs on the per-query-LUT kernel");
   using Rec = NodeRec<T, NPL>;
   using Tk = Taken<NPL>;
   const SearchArgs& a;
@@ -237,6 +254,9 @@ struct Query {
   uint64_t bu;
   float td;      // top-k entry of this lane
   int32_t ti;
+  // (WK) top-k entries 64 .. topk - 1 in LDS
+  float* wd;
+  int32_t* wi;
   int fc;        // found count
   int evals;     // ADC evaluations so far
   float last_e;  // exact distance of the node expanded by the last hop
@@ -279,8 +299,10 @@ struct Query {
     for (int k = 0; k < Q; k++) ck[k] = kPadKey;
 #pragma unroll
     for (int j = 0; j < Q - 1; j++) pk[j] = kPadKey;
-    LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, SC == 0, a.ef);
+    LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, SC == 0, a.ef, a.topk);
     cap = beam_cap(a.ef, Q, SC == 0);
+    wd = reinterpret_cast<float*>(smem + pl.wide_off);
+    wi = reinterpret_cast<int32_t*>(wd + wide_topk(a.topk));
     lut = reinterpret_cast<float*>(smem + pl.lut_off);
     qc = reinterpret_cast<float*>(smem + pl.qc_off);
     qu = reinterpret_cast<float*>(smem + pl.qu_off);
@@ -352,8 +374,111 @@ struct Query {
     else
       e = exact_l2_rest<T>(part, rec, qu, a.dim, lane);
     last_e = e;
+    if constexpr (WK) {
+      wide_insert(e, v, lane);
+      return;
+    }
     const float dlast = read_lane_f32(td, a.topk - 1);
     if (fc < a.topk || e < dlast) topk_insert(td, ti, fc, a.topk, e, v);
+  }
+
+  // Top-k insert for k > 64 (retset_push_32, gpu_primitives.cuh:99-138; the
+  // same order as topk_insert: after every entry <= e, the entry at k - 1
+  // dropping out of a full list), called for every expansion; it applies the
+  // fc < k || e < D[k - 1] guard itself.  Entries 0 .. 63 are the lanes'
+  // registers, entries 64 .. k - 1 the LDS list wd / wi.  The LDS part moves
+  // up one place from the insert position in chunks of 64, the highest chunk
+  // first, so that every entry is read before the write that replaces it;
+  // lane 63's register entry moves to LDS entry 0 when the insert lands in
+  // the registers.
+  __device__ __forceinline__ void wide_insert(float e, int32_t v, int lane) {
+    const int k = a.topk;
+    const int f = read_lane_i32(fc, 0);  // equal in every lane
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (f >= k && !(e < wd[k - kRegTopk - 1])) return;
+    int pos = __popcll(__ballot(lane < min(f, kRegTopk) && td <= e));
+    const int fx = f - kRegTopk;  // LDS entries in use
+    if (pos == kRegTopk) {
+      for (int b = 0; b < fx; b += kWave) {
+        const int j = b + lane;
+        const int c = __popcll(__ballot(j < fx && wd[j] <= e));
+        pos += c;
+        if (c < kWave) break;  // sorted: the rest are above e
+      }
+    }
+    const int ns = min(f + 1, k);
+    const int nx = ns - kRegTopk;  // LDS entries after the insert
+    if (nx > 0) {
+      const float r63d = read_lane_f32(td, kRegTopk - 1);
+      const int32_t r63i = read_lane_i32(ti, kRegTopk - 1);
+      const int lo = max(pos - kRegTopk, 0);  // first LDS entry that changes
+      for (int b = (nx - 1) & ~(kWave - 1); b >= 0 && b + kWave > lo; b -= kWave) {
+        const int j = b + lane;
+        const bool w = j >= lo && j < nx;
+        float dv = e;
+        int32_t iv = v;
+        if (w && kRegTopk + j != pos) {
+          if (j == 0) {
+            dv = r63d;
+            iv = r63i;
+          } else {
+            dv = wd[j - 1];
+            iv = wi[j - 1];
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (w) {
+          wd[j] = dv;
+          wi[j] = iv;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      }
+    }
+    if (pos < kRegTopk) {
+      int fr = min(f, kRegTopk);
+      topk_insert(td, ti, fr, kRegTopk, e, v);
+    }
+    fc = ns;
+  }
+
+  // Top-k entry k - 1's distance (+inf while fewer than k are found), the
+  // same in every lane.
+  __device__ __forceinline__ float kth_dist() const {
+    if constexpr (WK) {
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      const float d = wd[a.topk - kRegTopk - 1];
+      return read_lane_i32(fc, 0) >= a.topk ? d : __int_as_float(0x7f800000);
+    }
+    return read_lane_f32(td, a.topk - 1);
+  }
+
+  // Top-k entry i's id (-1: not found yet), the same in every lane.
+  __device__ __forceinline__ int32_t id_at(int i) const {
+    if constexpr (WK) {
+      if (i >= kRegTopk) {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        const int32_t id = wi[i - kRegTopk];
+        return i < read_lane_i32(fc, 0) ? id : -1;
+      }
+    }
+    return read_lane_i32(ti, i);
+  }
+
+  // Entries 64 .. k - 1 of the query's results (k > 64), -1 / +inf past fc.
+  __device__ __forceinline__ void write_wide(int32_t qid, int lane) const {
+    if constexpr (WK) {
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      const int f = read_lane_i32(fc, 0);
+      int32_t* const oi = a.out_ids + (int64_t)qid * a.topk + kRegTopk;
+      float* const od = a.out_dists + (int64_t)qid * a.topk + kRegTopk;
+      for (int j = lane; j < a.topk - kRegTopk; j += kWave) {
+        const bool ok = kRegTopk + j < f;
+        const int32_t id = wi[j];
+        const float d = wd[j];
+        oi[j] = ok ? id : -1;
+        od[j] = ok ? d : __int_as_float(0x7f800000);
+      }
+    }
   }
 
   // One expansion of node v: persistent_merge_data (kernel_helpers.cuh:232-357)
@@ -995,7 +1120,7 @@ __device__ __forceinline__ void query_sync() {
 
 // The persistent query loop of one wave: smem is its LDS area, piv the
 // shared pivots (SC > 0).
-template <class T, int Q, int MC, int SC, int NPL>
+template <class T, int Q, int MC, int SC, int NPL, bool WK = false>
 __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, const float* piv) {
   const int lane = lane_id();
 
@@ -1069,7 +1194,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     }
     if (a.t_start && lane == 0) a.t_start[qid] = wall_ticks();
 
-    Query<T, Q, MC, SC, NPL> Qy(a, smem, piv);
+    Query<T, Q, MC, SC, NPL, WK> Qy(a, smem, piv);
     const float* q = a.queries + (int64_t)qid * a.dim;
     // ---- entry node: the nav-graph search on the raw query when a nav graph is
     // loaded (kernel_q1.cuh:148-174, 199-206), else the medoid.
@@ -1101,7 +1226,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
     const bool gpr = a.early_exit == QV_EXIT_GPRUNING;
     auto check = [&]() -> bool {
       const float top1 = read_lane_f32(Qy.td, 0);
-      const float topk = read_lane_f32(Qy.td, a.topk - 1);
+      const float topk = Qy.kth_dist();
       const int fc = read_lane_i32(Qy.fc, 0);  // equal in every lane; read as uniform
       const bool improved = fc > g.last_fc || top1 < g.last_top1 || topk < g.last_topk;
       if (step < a.warmup) g.no_improve = 0;
@@ -1124,7 +1249,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       for (int t = 0; t < 4; t++) g[t] = lane + kWave * t < a.sr_width ? row[lane + kWave * t] : -1;
       int hits = 0;
       for (int i = 0; i < a.topk; i++) {
-        const int32_t id = read_lane_i32(Qy.ti, i);
+        const int32_t id = Qy.id_at(i);
         if (id < 0) continue;
         hits += __ballot(g[0] == id || g[1] == id || g[2] == id || g[3] == id) != 0 ? 1 : 0;
       }
@@ -1305,6 +1430,7 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
       a.out_ids[(int64_t)qid * a.topk + lane] = Qy.ti;
       a.out_dists[(int64_t)qid * a.topk + lane] = Qy.td;
     }
+    if constexpr (WK) Qy.write_wide(qid, lane);
     if (lane == 0) {
       if (a.out_found) a.out_found[qid] = Qy.fc;
       if (a.out_hops) a.out_hops[qid] = step;
@@ -1330,11 +1456,12 @@ __device__ __forceinline__ void run_queries(const SearchArgs& a, char* smem, con
   }
 }
 
-// One query per workgroup of one wave, its LUT in LDS.
-template <class T, int Q, int MC, int NPL>
+// One query per workgroup of one wave, its LUT in LDS.  WK: top-k above 64
+// (entries past the 64th in LDS after the query's area).
+template <class T, int Q, int MC, int NPL, bool WK = false>
 __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
   extern __shared__ __align__(16) char smem[];
-  run_queries<T, Q, MC, 0, NPL>(a, smem, nullptr);
+  run_queries<T, Q, MC, 0, NPL, WK>(a, smem, nullptr);
 }
 
 // One workgroup per CU, one query per wave: the workgroup holds the pivots
@@ -1355,7 +1482,7 @@ __global__ __launch_bounds__(kWave * sp_max_waves(Q, NPL)) void search_kernel_sp
   }
   __syncthreads();
   const int w = threadIdx.x / kWave;
-  const LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, false, a.ef);
+  const LdsPlan pl = lds_plan(a.num_chunks, a.dim, Q, false, a.ef, a.topk);
   run_queries<T, Q, MC, SC, NPL>(a, smem + piv_bytes(a.dim) + w * pl.total, piv);
 }
 

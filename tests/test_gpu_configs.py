@@ -328,6 +328,69 @@ def test_c1_topk_matches_oracle(c1, k):
                 assert got[4].tail_queries == 0
 
 
+@pytest.mark.parametrize("k", [65, 100, 200, 1024])
+def test_c1_wide_topk_matches_oracle(c1, k):
+    """top-k above 64 (retset_push_32, gpu_primitives.cuh:99-138, for any k):
+    the per-query-LUT kernel keeps entries 64 .. k - 1 in LDS.  `auto` takes
+    that kernel whatever the number of queries; a forced shared-pivot search
+    is refused.  Pipe widths 1 and 2, both early-exit policies (gpruning reads
+    entry k - 1), ef below and above k (k = 1024 at ef = 64 leaves most of the
+    list as -1 / +inf padding), and the code table on."""
+    n = 300 if k < 1024 else 100
+    cases = [(1, "none", 128), (2, "gpruning", 256), (2, "none", 64)]
+    if k == 100:
+        cases.append((1, "gpruning", 416))
+    for pipe, policy, ef in cases:
+        _say(f"[gpu] C1 wide topk={k} W={pipe} {policy} ef={ef}")
+        want = _oracle(c1, ef, policy, pipe=pipe, n=n, k=k)
+        rc, got = _search(c1, c1["q"][:n], ef, policy, "auto", pipe=pipe, k=k)
+        assert rc == 0, c1["lib"].load().qv_last_error()
+        assert got[4].kernel == KERNEL["lut"]
+        _same(got, want, f"wide topk={k} W={pipe} {policy} ef={ef}")
+        assert np.all(got[2] <= k)
+        pad = np.arange(k)[None, :] >= got[2][:, None]
+        assert np.all(got[0][pad] == -1) and np.all(np.isinf(got[1][pad]))
+    with _CodeTable(c1):
+        rc, got = _search(c1, c1["q"][:n], 128, "none", "auto", k=k)
+        assert rc == 0, c1["lib"].load().qv_last_error()
+        _same(got, _oracle(c1, 128, "none", n=n, k=k), f"wide topk={k} table")
+    rc, _ = _search(c1, c1["q"][:8], 128, "none", "shared-pivots", k=k)
+    assert rc == c1["lib"].QV_EUNSUPPORTED
+    assert "at most 64 results" in c1["lib"].load().qv_last_error().decode()
+
+
+def test_c1_wide_topk_per_step_recall(c1):
+    """Per-step recall over a top-100 (its entries past 64 read from LDS):
+    each query stops once 50 of its top-100 ids are in its ground-truth row,
+    here the oracle's top-128 at ef = 512; steps, hits and results equal the
+    oracle's."""
+    lib, L = c1["lib"], c1["L"]
+    n, k, width, need = 200, 100, 128, 50
+    gt = np.ascontiguousarray(_oracle(c1, 512, "none", n=n, k=width)[0])
+    want = O.search(c1["host"], c1["q"][:n], k, 256, early_exit=O.EXIT_NONE, step_recall=(gt, need))
+    o = lib.default_search_opts()
+    o.early_exit = lib.QV_EXIT_NONE
+    o.pipe_width = 1
+    o.kernel = KERNEL["auto"]
+    step, hits = np.full(n, -7, np.int32), np.full(n, -7, np.int32)
+    o.step_recall_gt, o.step_recall_gt_width, o.step_recall_gt_count = gt.ctypes.data, width, n
+    o.step_recall_threshold = need / k
+    o.step_recall_step, o.step_recall_hits = step.ctypes.data, hits.ctypes.data
+    ids = np.empty((n, k), np.int32)
+    dists = np.empty((n, k), np.float32)
+    found = np.empty(n, np.int32)
+    q = np.ascontiguousarray(c1["q"][:n], np.float32)
+    _say("[gpu] C1 wide topk=100 per-step recall")
+    lib.check(L.qv_search(c1["h"], q.ctypes.data, n, DIM, k, 256, C.byref(o), ids.ctypes.data,
+                          dists.ctypes.data, found.ctypes.data, None))
+    hops = np.empty(n, np.int32)
+    lib.check(L.qv_last_hops(c1["h"], hops.ctypes.data, n))
+    _same((ids, dists, found, hops), want[:4], "wide topk per-step recall")
+    np.testing.assert_array_equal(step, want[4])
+    np.testing.assert_array_equal(hits, want[5])
+    assert np.any(step > 0) and np.any(hits >= need)
+
+
 @pytest.mark.parametrize("batch,rate", [(1, 2e5), (16, 1e6), (256, 4e6)])
 def test_c1_open_loop_arrival(c1, batch, rate):
     """Open-loop arrival into one launch: groups of `batch` queries admitted on

@@ -47,15 +47,16 @@ def lib():
 class _Dev:
     """Device query and output buffers for up to n queries."""
 
-    def __init__(self, lib, queries):
+    def __init__(self, lib, queries, k=K):
         self.n, self.dim = queries.shape
+        self.k = k
         self.q = lib.DeviceBuffer(queries.nbytes).upload(np.ascontiguousarray(queries, np.float32))
-        self.ids = lib.DeviceBuffer(self.n * K * 4)
-        self.dists = lib.DeviceBuffer(self.n * K * 4)
+        self.ids = lib.DeviceBuffer(self.n * k * 4)
+        self.dists = lib.DeviceBuffer(self.n * k * 4)
         self.found = lib.DeviceBuffer(self.n * 4)
 
     def fetch(self, n):
-        return (self.ids.download(np.int32, (n, K)), self.dists.download(np.float32, (n, K)),
+        return (self.ids.download(np.int32, (n, self.k)), self.dists.download(np.float32, (n, self.k)),
                 self.found.download(np.int32, (n,)))
 
 
@@ -75,14 +76,14 @@ def _pair(lib, h, dev, n, ef, kernel, num_blocks=0, policy="none"):
     o = _opts(lib, kernel, num_blocks, policy)
     r0, r1 = lib.SearchReport(), lib.SearchReport()
     dev.ids.clear()
-    lib.check(L.qv_search(h, dev.q.ptr, n, dev.dim, K, ef, C.byref(o), dev.ids.ptr, dev.dists.ptr,
+    lib.check(L.qv_search(h, dev.q.ptr, n, dev.dim, dev.k, ef, C.byref(o), dev.ids.ptr, dev.dists.ptr,
                           dev.found.ptr, C.byref(r0)))
     want = dev.fetch(n)
     dev.ids.clear()
     dev.dists.clear()
     dev.found.clear()
     free0 = _free_bytes(lib)
-    lib.check(L.qv_search_noalloc(h, dev.q.ptr, n, dev.dim, K, ef, C.byref(o), dev.ids.ptr, dev.dists.ptr,
+    lib.check(L.qv_search_noalloc(h, dev.q.ptr, n, dev.dim, dev.k, ef, C.byref(o), dev.ids.ptr, dev.dists.ptr,
                                   dev.found.ptr, C.byref(r1)))
     free1 = _free_bytes(lib)
     if _WARM["calls"] > 0:
@@ -132,6 +133,23 @@ def test_noalloc_equals_search_float(lib, small_f32_index):
             for n in (dev.n, 5):
                 _say(f"[gpu] noalloc float kernel={kernel} n={n}")
                 _check(*_pair(lib, h, dev, n, 96, kernel), f"float {kernel} n={n}")
+    finally:
+        lib.load().qv_index_close(h)
+
+
+def test_noalloc_wide_topk(lib, small_u8_index):
+    """A top-100 (entries past the 64th in the per-query-LUT kernel's LDS,
+    no scratch of their own): equal to qv_search on two calls in a row, the
+    second smaller, both policies."""
+    ix = small_u8_index
+    h = _open_small(lib, ix)
+    dev = _Dev(lib, ix["queries"].astype(np.float32), k=100)
+    try:
+        for n, ef, policy in ((dev.n, 128, "none"), (23, 256, "gpruning")):
+            _say(f"[gpu] noalloc u8 topk=100 n={n} ef={ef} {policy}")
+            want, got, r0, r1 = _pair(lib, h, dev, n, ef, "auto", policy=policy)
+            _check(want, got, r0, r1, f"u8 topk=100 n={n}")
+            assert r1.kernel == 1
     finally:
         lib.load().qv_index_close(h)
 
