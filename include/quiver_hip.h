@@ -253,9 +253,10 @@ void qv_search_opts_default(qv_search_opts* opts);
  * load_queries_as_float does, bin/common/data_io.hpp:73-108).
  * ids [nq][topk] int32 (-1 padded), dists [nq][topk] float (+inf padded),
  * found [nq] int32 (may be NULL), report may be NULL.
- * topk in [1, 1024]; above 64 the search runs on the per-query-LUT kernel
- * (QV_KERNEL_SHARED_PIVOTS is QV_EUNSUPPORTED there), which keeps entries past
- * the 64th in LDS.
+ * topk in [1, 1024], ef_search in [1, 2048]; with topk above 64 or ef_search
+ * above 1024 the search runs on the per-query-LUT kernel (a forced
+ * QV_KERNEL_SHARED_PIVOTS is QV_EUNSUPPORTED there), which keeps top-k entries
+ * past the 64th in LDS.
  * With opts->device_buffers, queries/ids/dists/found are device pointers. */
 int qv_search(qv_index* index, const float* queries, int64_t nq, int32_t dim,
               int32_t topk, int32_t ef_search, const qv_search_opts* opts,

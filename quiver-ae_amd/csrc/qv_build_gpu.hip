@@ -1237,7 +1237,7 @@ qv_index* build_gpu_t(const T* d_base, int dtype, int64_t n, int dim, const qv_b
       rec.ids = d_rec.as<int32_t>();
       rec.dists = d_recd.as<float>();
       rec.cap = rec_cap;
-      search_record(ix.get(), d_q.as<float>(), nb, std::min(prm.L, kMaxEf), rec, d_hops.as<int32_t>(), 0);
+      search_record(ix.get(), d_q.as<float>(), nb, std::min(prm.L, kMaxEfShared), rec, d_hops.as<int32_t>(), 0);
 
       PruneArgs pa{};
       pa.L = G;

@@ -15,7 +15,8 @@ constexpr int64_t kPageSize = 4096;   // shared::PAGE_SIZE (src/shared/io/loader
 constexpr int kNumPivots = 256;       // PQSearchData::num_pivots (pq_search.hpp:14)
 constexpr int kMaxDegree = 128;       // two neighbour slots per wavefront lane
 constexpr int kMaxBuildDegree = 128;  // the GPU builder: a list in two slots per lane
-constexpr int kMaxEf = 1024;          // 16 beam positions per lane
+constexpr int kMaxEf = 2048;          // 32 beam positions per lane (per-query-LUT kernel)
+constexpr int kMaxEfShared = 1024;    // 16 beam positions per lane (shared-pivot kernel)
 constexpr int kMaxTopk = 1024;        // 64 in registers, the rest in LDS (per-query-LUT kernel)
 constexpr int kMaxPipeWidth = 16;     // bin/common/cli_validation.hpp:9
 constexpr int kMaxQueriesPerBlock = 8; // bin/common/cli_validation.hpp:10

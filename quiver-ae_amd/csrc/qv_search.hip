@@ -190,15 +190,16 @@ KernelFn pick_kernel_sp(int dtype, int Q, int M, int npl) {
   return k;
 }
 
-// Beam positions per lane for ef (beam capacity 64 Q >= ef; kMaxEf = 1024 = 64 * 16).
-// The per-query-LUT kernel comes in Q = 1, 2, 4, 7, 10, 16 (its 32 KB LUT, not
-// the beam, sets how many queries a CU holds); the shared-pivot kernel in
+// Beam positions per lane for ef (beam capacity 64 Q >= ef; kMaxEf = 2048 = 64 * 32).
+// The per-query-LUT kernel comes in Q = 1, 2, 4, 7, 10, 16 and 32 (its 32 KB LUT,
+// not the beam, sets how many queries a CU holds up to Q = 16); the shared-pivot
+// kernel stops at ef = 1024 (kMaxEfShared) and comes in
 // every Q from 1 to 7, then 10 and 16 (its LDS beam holds ef rounded up to 8
 // entries, and that decides how many queries a CU holds: at d = 128, 16 up to
 // ef = 192, then 15 at 208, 13 at 240, 12 at 256, 11 at 288, 10 at 320, 9 at
 // 384, 8 at 448, 7 at 512 and 3 at 1024).
 int beam_chunks(int ef) {
-  return ef <= 64 ? 1 : (ef <= 128 ? 2 : (ef <= 256 ? 4 : (ef <= 448 ? 7 : (ef <= 640 ? 10 : 16))));
+  return ef <= 64 ? 1 : (ef <= 128 ? 2 : (ef <= 256 ? 4 : (ef <= 448 ? 7 : (ef <= 640 ? 10 : (ef <= 1024 ? 16 : kXlQ)))));
 }
 int beam_chunks_sp(int ef) {
   const int q = (std::max(ef, 1) + kWave - 1) / kWave;
@@ -773,8 +774,10 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need, int topk) {
   const int P = wide ? wide_beam_chunks(ef) : beam_chunks(ef);
   const int M = ix->M, d = (int)ix->lay.num_dims;
   LaunchPlan lut;
-  lut.kern = wide ? pick_kernel_wide(ix->lay.data_type, P, M, slots_per_lane(ix->lay.max_m0))
-                  : pick_kernel(ix->lay.data_type, P, M, slots_per_lane(ix->lay.max_m0));
+  const int npl = slots_per_lane(ix->lay.max_m0);
+  lut.kern = P == kXlQ ? pick_kernel_xl(ix->lay.data_type, M, npl, wide)
+                       : (wide ? pick_kernel_wide(ix->lay.data_type, P, M, npl)
+                               : pick_kernel(ix->lay.data_type, P, M, npl));
   if (!lut.kern) fail(QV_EUNSUPPORTED, "no search kernel for this top-k, degree and ef");
   lut.waves = 1;
   lut.lds = lds_plan(M, d, P, true, ef, topk).total;
@@ -785,6 +788,12 @@ LaunchPlan launch_plan(qv_index* ix, int ef, int want, int64_t need, int topk) {
     if (forced)
       fail(QV_EUNSUPPORTED, "the shared-pivot kernel keeps at most 64 results per query; topk=" +
                                 std::to_string(topk) + " runs on the per-query-LUT kernel");
+    return lut;
+  }
+  if (ef > kMaxEfShared) {
+    if (forced)
+      fail(QV_EUNSUPPORTED, "the shared-pivot kernel holds beams of at most 1024; ef_search=" + std::to_string(ef) +
+                                " runs on the per-query-LUT kernel");
     return lut;
   }
   if (!forced && lut.slots_per_cu > 0 && need <= (int64_t)lut.slots_per_cu * ix->num_cus) return lut;
@@ -864,7 +873,7 @@ void search_record(qv_index* ix, const float* d_queries, int64_t nq, int ef, con
                    int32_t* d_hops, int num_blocks) {
   std::lock_guard<std::mutex> lk(ix->mu);
   if (nq <= 0 || nq > INT32_MAX - 1) fail(QV_EINVAL, "number of queries out of range: " + std::to_string(nq));
-  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 1024]");
+  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 2048]");
   HIP_OK(hipSetDevice(ix->device));
   ensure_scratch(ix, nq, 1);
   const LaunchPlan lp =
@@ -930,7 +939,7 @@ void search(qv_index* ix, const float* queries, int64_t nq, int dim, int topk, i
     fail(QV_EINVAL, "Query dimension mismatch: queries have " + std::to_string(dim) +
                         " dims, but the index expects " + std::to_string(L.num_dims));
   if (topk <= 0 || topk > kMaxTopk) fail(QV_EINVAL, "topk must be in [1, 1024]");
-  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 1024]");
+  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 2048]");
   if (o.pipe_width < 1 || o.pipe_width > kMaxPipeWidth) fail(QV_EINVAL, "--pipe-width must be in [1, 16]");
   if (o.queries_per_block < 1 || o.queries_per_block > kMaxQueriesPerBlock)
     fail(QV_EINVAL, "--queries-per-block must be in [1, 8]");
@@ -1389,7 +1398,7 @@ void search_noalloc(qv_index* ix, const float* d_queries, int64_t nq, int dim, i
     fail(QV_EINVAL, "Query dimension mismatch: queries have " + std::to_string(dim) +
                         " dims, but the index expects " + std::to_string(L.num_dims));
   if (topk <= 0 || topk > kMaxTopk) fail(QV_EINVAL, "topk must be in [1, 1024]");
-  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 1024]");
+  if (ef <= 0 || ef > kMaxEf) fail(QV_EINVAL, "ef_search must be in [1, 2048]");
   if (o.pipe_width < 1 || o.pipe_width > kMaxPipeWidth) fail(QV_EINVAL, "--pipe-width must be in [1, 16]");
   if (o.queries_per_block < 1 || o.queries_per_block > kMaxQueriesPerBlock)
     fail(QV_EINVAL, "--queries-per-block must be in [1, 8]");

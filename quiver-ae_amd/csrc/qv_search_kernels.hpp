@@ -162,6 +162,9 @@ __host__ __device__ inline int piv_bytes(int dim) { return kPivots * dim * 4; }
 
 using KernelFn = void (*)(SearchArgs);
 
+// Beam positions per lane of the kernels for ef above 1024.
+constexpr int kXlQ = 32;
+
 // Waves (queries) one shared-pivot workgroup holds at most, by beam positions
 // per lane and neighbour slots per lane: 16 (128 registers per wave), or 8
 // (256) for beams of more than 7 positions per lane and for two slots.
@@ -178,8 +181,11 @@ KernelFn pick_kernel_sp_deep(int dtype, int Q, int M);
 // 7, 10 or 16 (from wide_beam_chunks), one or two neighbour slots per lane.
 KernelFn pick_kernel_wide(int dtype, int Q, int M, int npl);
 __host__ __device__ inline int wide_beam_chunks(int ef) {
-  return ef <= 128 ? 2 : (ef <= 256 ? 4 : (ef <= 448 ? 7 : (ef <= 640 ? 10 : 16)));
+  return ef <= 128 ? 2 : (ef <= 256 ? 4 : (ef <= 448 ? 7 : (ef <= 640 ? 10 : (ef <= 1024 ? 16 : kXlQ))));
 }
+// Per-query-LUT kernels for ef in (1024, 2048] (qv_search_xl.hip): Q = 32,
+// any top-k.
+KernelFn pick_kernel_xl(int dtype, int M, int npl, bool wide);
 
 }  // namespace sk
 }  // namespace qv
@@ -860,7 +866,7 @@ struct Query {
           // comparison, since a below candidate is under the last key of a
           // full beam.  Visited bits do not matter: e < c0 ignores them.
           constexpr int kCap = Q * kWave;
-          constexpr int kTop = kCap <= 64 ? 16 : (kCap <= 256 ? 64 : 256);
+          constexpr int kTop = kCap <= 64 ? 16 : (kCap <= 256 ? 64 : (kCap <= 1024 ? 256 : 1024));
           {
             const uint64_t e1 = reg_pos<kTop - 1>(), e2 = reg_pos<2 * kTop - 1>(), e3 = reg_pos<3 * kTop - 1>();
             r = ((e1 < c0 ? 1 : 0) + (e2 < c0 ? 1 : 0) + (e3 < c0 ? 1 : 0)) * kTop;
@@ -868,7 +874,8 @@ struct Query {
           // LDS byte addresses: rb = beam + 8 r, and the read of position
           // min(r + k, cap - 1) at min(rb, top8 - 8 k) + 8 k, the 8 k in the
           // instruction (every beam lies past the LUT or the pivot table, at
-          // least 8 KB in, so top8 - 8 k stays above 0 for k < 3 kTop).  The
+          // least 8 KB in, so top8 - 8 k stays above 0 for the LDS levels'
+          // k < 3 kTop / 4 <= 768).  The
           // address is wave-uniform: held in a scalar register, opaque, so the
           // bounds are scalar work of each merge rather than vector registers
           // held across the loop.

@@ -1,4 +1,4 @@
-"""Indexes of max degree up to 128 and beams of up to 1024 entries on the GPU,
+"""Indexes of max degree up to 128 and beams of up to 2048 entries on the GPU,
 against the oracle: ids, distances, found counts and hop counts identical
 (runs on the MI355X).
 
@@ -10,7 +10,9 @@ against the oracle: ids, distances, found counts and hop counts identical
   merge's result) to 800; the star of degree 128 whose answers are derived
   by hand in test_oracle_wide.py.
 * ef in (448, 1024] (Q = 10 and 16 beam positions per lane) on the R = 32
-  and R = 64 fixtures and on the R = 128 index.
+  and R = 64 fixtures and on the R = 128 index; ef in (1024, 2048] (Q = 32,
+  per-query-LUT kernel only) on the uint8, float and R = 128 indexes.
+* The ef limits: 2048 overall, 1024 for a forced shared-pivot search.
 * Graph validation at open on R = 128 records (slots 64..127).
 """
 from __future__ import annotations
@@ -50,10 +52,10 @@ class Opened:
         lib.check(self.L.qv_index_open(str(directory).encode(), dtype.encode(), b"heap", None, 0, C.byref(self.h)))
         self.host = O.HostIndex.from_files(directory, dtype)
 
-    def search(self, q, ef, policy="none", kernel="auto", pipe=1):
+    def search(self, q, ef, policy="none", kernel="auto", pipe=1, k=K):
         n, dim = q.shape
-        ids = np.empty((n, K), np.int32)
-        dists = np.empty((n, K), np.float32)
+        ids = np.empty((n, k), np.int32)
+        dists = np.empty((n, k), np.float32)
         found = np.empty(n, np.int32)
         hops = np.empty(n, np.int32)
         o = self.lib.default_search_opts()
@@ -63,7 +65,7 @@ class Opened:
         o.num_blocks = 256
         rep = self.lib.SearchReport()
         qq = np.ascontiguousarray(q, np.float32)
-        self.lib.check(self.L.qv_search(self.h, qq.ctypes.data, n, dim, K, ef, C.byref(o), ids.ctypes.data,
+        self.lib.check(self.L.qv_search(self.h, qq.ctypes.data, n, dim, k, ef, C.byref(o), ids.ctypes.data,
                                         dists.ctypes.data, found.ctypes.data, C.byref(rep)))
         self.lib.check(self.L.qv_last_hops(self.h, hops.ctypes.data, n))
         return ids, dists, found, hops, rep
@@ -200,11 +202,53 @@ def test_deep_beam_f32(lib, small_f32_index, ef, kernel):
         ix.close()
 
 
-def test_ef_above_1024_is_rejected(lib, small_u8_index):
+@pytest.mark.parametrize("policy", ["none", "gpruning"])
+@pytest.mark.parametrize("ef", [1025, 1500, 2048])
+def test_xl_beam_u8(lib, small_u8_index, ef, policy):
+    """ef in (1024, 2048] (the reference sizes its frontier from ef,
+    search.cu:391): 32 beam positions per lane in the per-query-LUT kernel,
+    which `auto` takes; pipe widths 1 and 2, and a top-100 at ef = 1500."""
     ix = Opened(lib, small_u8_index["dir"], "uint8")
     try:
-        with pytest.raises(lib.QuiverError, match=r"ef_search must be in \[1, 1024\]"):
-            ix.search(small_u8_index["queries"][:4].astype(np.float32), 1025)
+        q = small_u8_index["queries"][:120].astype(np.float32)
+        for pipe in (1, 2):
+            _say(f"[gpu] xl beam u8 ef={ef} policy={policy} W={pipe}")
+            got = ix.search(q, ef, policy, "auto", pipe=pipe)
+            assert got[4].kernel == ix.lib.KERNEL_NAMES["lut"]
+            _same(got, O.search(ix.host, q, K, ef, pipe_width=pipe, early_exit=_policy(policy)),
+                  f"xl u8 ef={ef} {policy} W={pipe}")
+        if ef == 1500:
+            _say(f"[gpu] xl beam u8 ef={ef} policy={policy} topk=100")
+            _same(ix.search(q, ef, policy, "auto", k=100), O.search(ix.host, q, 100, ef, early_exit=_policy(policy)),
+                  f"xl u8 ef={ef} {policy} topk=100")
+    finally:
+        ix.close()
+
+
+def test_xl_beam_f32_and_r128(lib, small_f32_index, r128_u8):
+    q = np.ascontiguousarray(small_f32_index["queries"][:100], np.float32)
+    ix = Opened(lib, small_f32_index["dir"], "float")
+    try:
+        _say("[gpu] xl beam f32 ef=2048")
+        _same(ix.search(q, 2048, "none"), O.search(ix.host, q, K, 2048, early_exit=O.EXIT_NONE), "xl f32 ef=2048")
+    finally:
+        ix.close()
+    ix, q = r128_u8
+    _say("[gpu] xl beam R=128 u8 ef=1200")
+    _same(ix.search(q[:100], 1200, "gpruning"), O.search(ix.host, q[:100], K, 1200, early_exit=O.EXIT_GPRUNING),
+          "xl R=128 ef=1200")
+
+
+def test_ef_limits(lib, small_u8_index):
+    """ef above 2048 is rejected; a forced shared-pivot search above 1024 is
+    unsupported (its beams stop at 1024)."""
+    ix = Opened(lib, small_u8_index["dir"], "uint8")
+    try:
+        q = small_u8_index["queries"][:4].astype(np.float32)
+        with pytest.raises(lib.QuiverError, match=r"ef_search must be in \[1, 2048\]"):
+            ix.search(q, 2049)
+        with pytest.raises(lib.QuiverError, match=r"beams of at most 1024"):
+            ix.search(q, 1025, kernel="shared-pivots")
     finally:
         ix.close()
 

@@ -208,7 +208,7 @@ def test_noalloc_rejects_out_of_range_calls(lib, small_u8_index):
                                  None, None)
         assert rc == lib.QV_EINVAL and b"no deadline" in L.qv_last_error()
         o.timeout_s = 0.0
-        rc = L.qv_search_noalloc(h, dev.q.ptr, 4, dev.dim, K, 1025, C.byref(o), dev.ids.ptr, dev.dists.ptr,
+        rc = L.qv_search_noalloc(h, dev.q.ptr, 4, dev.dim, K, 2049, C.byref(o), dev.ids.ptr, dev.dists.ptr,
                                  None, None)
         assert rc == lib.QV_EINVAL
         # still usable afterwards
