@@ -6,13 +6,18 @@ Workload (default): 100M uint8 vectors of dimension 128 from the seeded
 Gaussian mixture (65536 centres uniform in [32, 224], sigma 20, clipped), a
 Vamana graph R=64 / L=100 / alpha=1.2 and PQ 32x256 built on the GPU, 10k
 queries from the same mixture, top-10.  Setup (data, build, ground truth, the
-sweep over ef, early exit and pipe width) is untimed; a step is one search of
-all queries with the queries and results in host memory, the transfers inside
-each step's clock as the reference times a search.  Beside it: the same steps
-with the queries resident in HBM, the latency mode (one search call per batch
-of 1, 16 and 256 queries at Recall@10 0.90 and 0.95), open-loop arrival
-(batches of 1, 16 and 256 offered at fixed rates into one launch), the PQ-ADC
-microbenchmark and the CPU oracle on the same index.  Prints one JSON line.
+sweep over ef, early exit and pipe width) is untimed; a step is one search
+call over the query set repeated 20 times (200k queries), as the reference's
+quiver_search runs its query file (--repeat 20 by default, the file repeated in
+memory before one run_persistent_search call: bin/common/cli_shared.hpp:24,
+data_io.hpp:94-104; ae/scripts/common.sh:70), with the queries resident in HBM
+and the results left there.  Beside it: the same steps with the queries and
+results in host memory (their transfers inside each step's clock, as the
+reference's clock runs), single 10k-query calls both ways, the latency mode
+(one search call per batch of 1, 16 and 256 queries at Recall@10 0.90 and
+0.95), open-loop arrival (batches of 1, 16 and 256 offered at fixed rates into
+one launch), the PQ-ADC microbenchmark and the CPU oracle on the same index.
+Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -53,6 +58,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--repeat", type=int, default=20,
+                    help="the query set repeated this many times in each step's search call, as the reference's "
+                         "--repeat (default 20, bin/common/cli_shared.hpp:24)")
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="large-100M-u8", choices=sorted(WORKLOADS))
     ap.add_argument("--n", type=int, default=0, help="override the number of base vectors")
@@ -268,58 +276,92 @@ def main() -> int:
         log(f"calibration copy: {args.copy_mib} MiB read + {args.copy_mib} MiB written")
 
     # ---- warmup + timed steps ------------------------------------------------
-    # A step is one search of all queries with the queries and results in host
-    # memory: the clock of each call starts before the queries are uploaded and
-    # stops once the results are back in host memory, as the reference times a
-    # search (src/quiver/search.cu:865-877, 1121-1129, 1186).
-    h_ids = np.empty((nq, 10), np.int32)
-    h_dists = np.empty((nq, 10), np.float32)
+    # A step is one search call over the query set repeated `repeat` times, as
+    # the reference's quiver_search searches its query file repeated --repeat
+    # times (20 by default) in one run_persistent_search call
+    # (bin/common/data_io.hpp:94-104), with the queries resident in HBM and
+    # the results left there.  Every repetition of a query must return the
+    # same answer.
+    R = max(1, args.repeat)
+    nqr = nq * R
+    qr = np.ascontiguousarray(np.tile(qf, (R, 1))) if R > 1 else qf
+    d_qr = _lib.DeviceBuffer(qr.nbytes).upload(qr) if R > 1 else d_q
+    d_ids_r = _lib.DeviceBuffer(nqr * 10 * 4) if R > 1 else d_ids
+    d_dists_r = _lib.DeviceBuffer(nqr * 10 * 4) if R > 1 else d_dists
+    h_ids = np.empty((nqr, 10), np.int32)
+    h_dists = np.empty((nqr, 10), np.float32)
 
-    def run_host(ef: int, policy: int, pipe: int = 1):
+    def run_rep(ef: int, policy: int, pipe: int, device: bool, count: int = nqr):
         o = _lib.default_search_opts()
         o.early_exit = policy
         o.pipe_width = pipe
         o.kernel = _lib.KERNEL_NAMES[args.search_kernel]
+        o.device_buffers = 1 if device else 0
         o.admission = _lib.QV_ADMIT_STREAMING
         rep = _lib.SearchReport()
-        _lib.check(L.qv_search(h, qf.ctypes.data, nq, dim, 10, ef, C.byref(o), h_ids.ctypes.data,
-                               h_dists.ctypes.data, None, C.byref(rep)))
+        if device:
+            _lib.check(L.qv_search(h, d_qr.ptr, count, dim, 10, ef, C.byref(o), d_ids_r.ptr, d_dists_r.ptr, None,
+                                   C.byref(rep)))
+        else:
+            _lib.check(L.qv_search(h, qr.ctypes.data, count, dim, 10, ef, C.byref(o), h_ids.ctypes.data,
+                                   h_dists.ctypes.data, None, C.byref(rep)))
         return rep
 
-    for _ in range(args.warmup):
-        run_host(ef, policy, pipe)
-    reps = []
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        reps.append(run_host(ef, policy, pipe))
-    t1 = time.perf_counter()
-    elapsed = t1 - t0
-    timed_ids = h_ids.copy()
-    timed_dists = h_dists.copy()
+    def timed(device: bool, steps: int, warmup: int, count: int = nqr):
+        for _ in range(warmup):
+            run_rep(ef, policy, pipe, device, count)
+        t0 = time.perf_counter()
+        reps = [run_rep(ef, policy, pipe, device, count) for _ in range(steps)]
+        secs = time.perf_counter() - t0
+        if device:
+            ids = d_ids_r.download(np.int32, (nqr, 10))[:count]
+            dists = d_dists_r.download(np.float32, (nqr, 10))[:count]
+        else:
+            ids, dists = h_ids[:count].copy(), h_dists[:count].copy()
+        return reps, secs, ids, dists
+
+    def summary(reps, secs, steps, count):
+        return {"value": round(steps * count / secs, 1), "unit": "queries/s", "steps": steps,
+                "queries_per_step": count, "ms_per_step": round(secs / steps * 1e3, 3),
+                "p50_ms": round(float(np.median([r.lat_p50_ms for r in reps])), 3),
+                "p99_ms": round(float(np.median([r.lat_p99_ms for r in reps])), 3),
+                "kernel_ms": round(float(np.median([r.kernel_ms for r in reps])), 3)}
+
+    reps, elapsed, all_ids, all_dists = timed(True, args.steps, args.warmup)
+    timed_ids, timed_dists = all_ids[:nq].copy(), all_dists[:nq].copy()
+    repeats_identical = all(np.array_equal(all_ids[k * nq:(k + 1) * nq], timed_ids)
+                            and np.array_equal(all_dists[k * nq:(k + 1) * nq], timed_dists) for k in range(R))
     recall = sum(len(set(timed_ids[i]) & set(gt[i])) for i in range(nq)) / (nq * 10.0)
-    qps = args.steps * nq / elapsed
+    qps = args.steps * nqr / elapsed
     p99 = float(np.median([r.lat_p99_ms for r in reps]))
     p50 = float(np.median([r.lat_p50_ms for r in reps]))
     last = reps[-1]
-    log(f"timed (host buffers): ef={ef} {pname} W={pipe} steps={args.steps} qps={qps:.0f} recall={recall:.4f} "
-        f"p50={p50:.3f} p99={p99:.3f}")
+    log(f"timed (device-resident, {R} x {nq} queries per step): ef={ef} {pname} W={pipe} steps={args.steps} "
+        f"qps={qps:.0f} recall={recall:.4f} p50={p50:.3f} p99={p99:.3f} repeats_identical={repeats_identical}")
 
-    # the same steps with the queries already in HBM and the results left there
-    dev_steps = max(1, min(args.steps, 10))
-    run(ef, policy, pipe)
-    t0d = time.perf_counter()
-    dreps = [run(ef, policy, pipe) for _ in range(dev_steps)]
-    dev_s = time.perf_counter() - t0d
-    device_resident = {"value": round(dev_steps * nq / dev_s, 1), "unit": "queries/s", "steps": dev_steps,
-                       "ms_per_step": round(dev_s / dev_steps * 1e3, 3),
-                       "p50_ms": round(float(np.median([r.lat_p50_ms for r in dreps])), 3),
-                       "p99_ms": round(float(np.median([r.lat_p99_ms for r in dreps])), 3),
-                       "kernel_ms": round(float(np.median([r.kernel_ms for r in dreps])), 3),
-                       "same_results": bool(np.array_equal(d_ids.download(np.int32, (nq, 10)), timed_ids)
-                                            and np.array_equal(d_dists.download(np.float32, (nq, 10)),
-                                                               timed_dists)),
-                       "note": "queries resident in HBM and results left there; no host transfer in a step"}
-    log(f"device-resident: {device_resident['value']:.0f} queries/s ({device_resident['ms_per_step']} ms per step)")
+    # the same steps with the queries and results in host memory: the clock of
+    # each call starts before the queries are uploaded and stops once the
+    # results are back in host memory, as the reference times a search
+    # (src/quiver/search.cu:865-877, 1121-1129, 1186)
+    host_steps = max(1, min(args.steps, 10))
+    hreps, hsecs, hids, hdists = timed(False, host_steps, 1)
+    host_buffers = summary(hreps, hsecs, host_steps, nqr)
+    host_buffers["same_results"] = bool(np.array_equal(hids, all_ids) and np.array_equal(hdists, all_dists))
+    host_buffers["note"] = ("queries and results in host memory; each call's clock includes their transfer "
+                            "(the reference's clock)")
+    log(f"host buffers: {host_buffers['value']:.0f} queries/s ({host_buffers['ms_per_step']} ms per step)")
+
+    # single calls of the 10k queries (no repetition), both ways: each call
+    # ends with the drain of its last queries
+    single = {}
+    for dev, key in ((True, "device_resident"), (False, "host_buffers")):
+        sreps, ssecs, sids, sdists = timed(dev, 10, 1, nq)
+        single[key] = summary(sreps, ssecs, 10, nq)
+        single[key]["same_results"] = bool(np.array_equal(sids, timed_ids) and np.array_equal(sdists, timed_dists))
+    log(f"single 10k-query calls: device-resident {single['device_resident']['value']:.0f}, "
+        f"host buffers {single['host_buffers']['value']:.0f} queries/s")
+    device_resident = single["device_resident"]  # the closed-loop rate of one 10k batch
+    run(ef, policy, pipe)  # d_ids / d_dists hold the 10k answer for the legs below
 
     # with a nav graph: the same steps from the medoid, to price the nav search
     medoid_entry = None
@@ -335,17 +377,18 @@ def main() -> int:
     kernel_ms = float(np.median([r.kernel_ms for r in reps]))
     kname = "search_kernel_sp" if last.kernel == _lib.QV_KERNEL_SHARED_PIVOTS else "search_kernel"
     alg_bytes = (last.total_hops * info.node_size + last.total_evals * (info.num_chunks + 4)
-                 + nq * (info.num_chunks * 256 * 4 + dim * 4 + 10 * 8))
+                 + nqr * (info.num_chunks * 256 * 4 + dim * 4 + 10 * 8))
     achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
     traffic, traffic_pipe = measured_traffic(args.workload, ef, pname,
-                                             kname + (" neighbour-codes" if nbr_codes else ""), pipe, log)
+                                             kname + (" neighbour-codes" if nbr_codes else ""), pipe, R, log)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": traffic,
                 "traffic_pipe_width": traffic_pipe,
                 "kernel": kname, "kernel_ms": round(kernel_ms, 3),
                 "bytes_per_launch": int(alg_bytes),
-                "bytes_per_launch_without_lut": int(alg_bytes - nq * info.num_chunks * 256 * 4),
+                "bytes_per_launch_without_lut": int(alg_bytes - nqr * info.num_chunks * 256 * 4),
+                "queries_per_launch": nqr,
                 "hops_per_launch": int(last.total_hops),
                 "evals_per_launch": int(last.total_evals)}
 
@@ -355,18 +398,22 @@ def main() -> int:
         "scaling": "weak", "vs_baseline": None, "dtype": "u8" if is_u8 else "f32",
         "data": "synthetic: seeded Gaussian mixture generated on the GPU; index built on the GPU",
         "config": {"workload": f"{args.workload}: {n} x {dim} {w['dtype']} mixture ({w['centers']} centres), "
-                               f"Vamana R={w['R']} L={w['L']} alpha=1.2, PQ {w['M']}x256, {nq} queries, top-10",
+                               f"Vamana R={w['R']} L={w['L']} alpha=1.2, PQ {w['M']}x256, {nq} queries, top-10"
+                               + (f", the query set repeated {R} times per search call" if R > 1 else ""),
                    "ef_search": ef, "early_exit": pname, "pipe_width": pipe, "num_blocks": last.num_blocks,
                    "graph_placement": args.graph_placement, "nav_nodes": int(info.nav_nodes),
                    "neighbour_codes": nbr_codes,
                    "admission": "streaming (window = num_blocks)",
-                   "buffers": "queries and results in host memory; each step's clock includes their transfer",
+                   "repeat": R, "queries_per_step": nqr, "repeats_identical": repeats_identical,
+                   "buffers": "queries resident in HBM, results left there (host_buffers: the same steps with "
+                              "their transfers inside each call's clock)",
                    "recall_at_10": round(recall, 4),
                    "p50_ms": round(p50, 3), "p99_ms": round(p99, 3), "avg_hops": round(last.avg_hops, 2),
                    "build_s": round(build_s, 1),
                    **({"medoid_entry": medoid_entry} if medoid_entry else {})},
         "roofline": roofline,
-        "device_resident": device_resident,
+        "host_buffers": host_buffers,
+        "single_batch": single,
         "sweep": sweep,
     }
 
@@ -395,19 +442,25 @@ def main() -> int:
             _lib.check(L.qv_index_neighbour_codes(h, 0))  # room for the 32 GB code table
         result["adc"] = adc_leg(_lib, L, args.adc_codes, log)
 
-    # The search kernel is bound by random accesses, not by HBM bytes: one code
-    # row per neighbour evaluation and the 64-byte lines of each expanded
-    # record, against the rate the gather-alone kernel reaches for random rows
-    # in the same run.
-    acc = last.total_evals + last.total_hops * ((info.node_size + 63) // 64)
+    # Random accesses of the search kernel: the 64-byte lines of each expanded
+    # record, plus one code row per neighbour evaluation gathered by id, against
+    # the rate the gather-alone kernel reaches for random 32-byte rows in the
+    # same run.  With the neighbour code table a hop reads its neighbours' rows
+    # as one contiguous block instead (one request of R * M bytes), which that
+    # ceiling does not price, so no fraction is given then.
+    rec_lines = (info.node_size + 63) // 64
+    acc = last.total_hops * (rec_lines + 1) if nbr_codes else last.total_evals + last.total_hops * rec_lines
     rate = acc / (kernel_ms * 1e-3)
     ceil_rate = result.get("adc", {}).get("gather_alone_rows_per_s")
     if "adc" in result:
         roofline["measured_read_peak_gbs"] = result["adc"]["stream_read_gbs"]
     roofline["random_access"] = {
         "accesses_per_launch": int(acc), "achieved_per_s": round(rate, 1),
-        "ceiling_per_s": ceil_rate, "frac": round(rate / ceil_rate, 4) if ceil_rate else None,
-        "ceiling": "gather_kernel: random 32-byte rows of the 1B-code table, same run"}
+        "ceiling_per_s": ceil_rate,
+        "frac": round(rate / ceil_rate, 4) if ceil_rate and not nbr_codes else None,
+        "ceiling": "gather_kernel: random 32-byte rows of the 1B-code table, same run",
+        "counted": ("per hop: the record's 64-byte lines and one contiguous code block" if nbr_codes else
+                    "per hop: the record's 64-byte lines; per evaluation: one 32-byte code row by id")}
 
     # ---- CPU baseline: the oracle (CPU restatement) on a bounded sample -------
     if not args.no_cpu:
@@ -516,14 +569,15 @@ def open_loop_leg(_lib, L, h, qf, dim, nq, ref_ids, ef, policy, pname, pipe, cap
     return out
 
 
-def measured_traffic(workload: str, ef: int, policy: str, kernel: str, pipe: int, log):
+def measured_traffic(workload: str, ef: int, policy: str, kernel: str, pipe: int, repeat: int, log):
     """HBM bytes per search-kernel launch for this configuration and kernel, as
     measured by the FETCH_SIZE and WRITE_SIZE counter runs summarised under
     profiles/ (scaled by a copy kernel of known size), and the pipe width it
     was measured at: this one's if measured, else another's (the same nodes
     and code blocks are read whatever the pipe width); (None, None) when not
-    measured."""
-    base = f"traffic_bytes_per_launch[{workload} ef={ef} {policy} {kernel}"
+    measured.  A launch over the query set repeated R > 1 times is looked up
+    under its own ` repeat=R` key."""
+    base = f"traffic_bytes_per_launch[{workload} ef={ef} {policy} {kernel}" + (f" repeat={repeat}" if repeat > 1 else "")
     found = {}
     for f in sorted((Path(__file__).resolve().parent / "profiles").glob("*.md")):
         for line in f.read_text().splitlines():
