@@ -40,7 +40,7 @@ HBM_PEAK_GBS = 8000.0
 WORKLOADS = {
     # name: n, dim, dtype, centres, sigma, R, L, M, queries, ef sweep (finer near Recall@10 0.90 and 0.95)
     "mid-10M-u8": dict(n=10_000_000, dim=128, dtype="uint8", centers=8192, sigma=20.0, R=64, L=100, M=32,
-                       nq=10_000, efs=(64, 96, 128, 160, 192, 224, 232, 240, 248, 256, 288, 320, 352, 384, 448)),
+                       nq=10_000, efs=(32, 45, 64, 96, 128, 160, 192, 224, 232, 240, 248, 256, 288, 320, 352, 384, 448)),
     "small-1M-u8": dict(n=1_000_000, dim=128, dtype="uint8", centers=1024, sigma=20.0, R=64, L=100, M=32,
                         nq=10_000, efs=(45, 64, 96, 128, 160, 192, 200, 208, 216, 224, 256, 288, 320, 384, 448)),
     "float-10M-d96": dict(n=10_000_000, dim=96, dtype="float", centers=4096, sigma=1.0, R=64, L=100, M=48,
