@@ -239,6 +239,23 @@ def test_xl_beam_f32_and_r128(lib, small_f32_index, r128_u8):
           "xl R=128 ef=1200")
 
 
+def test_wide_topk_r128_and_float(lib, small_f32_index, r128_u8):
+    """A top-k above 64 (entries past the 64th in LDS) with two neighbour
+    slots per lane and with 2-dim PQ chunks."""
+    ix, q = r128_u8
+    _say("[gpu] R=128 u8 topk=100 ef=300 W=2 gpruning")
+    _same(ix.search(q[:120], 300, "gpruning", pipe=2, k=100),
+          O.search(ix.host, q[:120], 100, 300, pipe_width=2, early_exit=O.EXIT_GPRUNING), "R=128 topk=100")
+    qf = np.ascontiguousarray(small_f32_index["queries"][:100], np.float32)
+    fx = Opened(lib, small_f32_index["dir"], "float")
+    try:
+        _say("[gpu] float topk=80 ef=200")
+        _same(fx.search(qf, 200, "none", k=80), O.search(fx.host, qf, 80, 200, early_exit=O.EXIT_NONE),
+              "float topk=80")
+    finally:
+        fx.close()
+
+
 def test_ef_limits(lib, small_u8_index):
     """ef above 2048 is rejected; a forced shared-pivot search above 1024 is
     unsupported (its beams stop at 1024)."""
