@@ -189,3 +189,28 @@ def test_cli_static_batches_fill_the_gpu(small_u8_index, tmp_path):
     host = O.HostIndex.from_files(ix["dir"], "uint8")
     oids, _, _, _ = O.search(host, q.astype(np.float32), 10, 64, early_exit=O.EXIT_NONE)
     np.testing.assert_array_equal(ids, oids)
+
+
+@pytest.mark.gpu
+def test_cli_wide_topk_and_deep_beam(small_u8_index, tmp_path):
+    """--topk 100 --ef-search 1500 (entries past the 64th top-k in LDS, a beam
+    of 32 positions per lane): the result files hold the oracle's ids and
+    distances for every repetition of the query set."""
+    import qv_oracle as O
+
+    ix = small_u8_index
+    q = ix["queries"][:40]
+    qf = tmp_path / "q.u8bin"
+    qf.write_bytes(struct.pack("<ii", *q.shape) + q.tobytes())
+    print("[gpu] CLI --topk 100 --ef-search 1500 --repeat 2", flush=True)
+    r = run("--index-dir", ix["dir"], "--query", qf, "--data-type", "uint8", "--topk", "100", "--ef-search", "1500",
+            "--repeat", "2", "--pipe-width", "2", "--early-exit-policy", "gpruning", "--result-prefix",
+            tmp_path / "w")
+    assert r.returncode == 0, r.stderr
+    ids = np.fromfile(tmp_path / "w_ids.bin", dtype="<i4")
+    dists = np.fromfile(tmp_path / "w_distances.bin", dtype="<f4")
+    assert tuple(ids[:2]) == (80, 100) and tuple(dists[:2].view("<i4")) == (80, 100)
+    host = O.HostIndex.from_files(ix["dir"], "uint8")
+    oids, odists, _, _ = O.search(host, q.astype(np.float32), 100, 1500, pipe_width=2, early_exit=O.EXIT_GPRUNING)
+    np.testing.assert_array_equal(ids[2:].reshape(80, 100), np.concatenate([oids, oids]))
+    np.testing.assert_array_equal(dists[2:].reshape(80, 100), np.concatenate([odists, odists]))
