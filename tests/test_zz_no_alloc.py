@@ -139,13 +139,14 @@ def test_noalloc_equals_search_float(lib, small_f32_index):
 
 def test_noalloc_wide_topk(lib, small_u8_index):
     """A top-100 (entries past the 64th in the per-query-LUT kernel's LDS,
-    no scratch of their own): equal to qv_search on two calls in a row, the
-    second smaller, both policies."""
+    no scratch of their own): equal to qv_search on calls in a row, each
+    smaller than the one before, both policies, the last with a beam of 1500
+    (32 positions per lane)."""
     ix = small_u8_index
     h = _open_small(lib, ix)
     dev = _Dev(lib, ix["queries"].astype(np.float32), k=100)
     try:
-        for n, ef, policy in ((dev.n, 128, "none"), (23, 256, "gpruning")):
+        for n, ef, policy in ((dev.n, 128, "none"), (23, 256, "gpruning"), (17, 1500, "none")):
             _say(f"[gpu] noalloc u8 topk=100 n={n} ef={ef} {policy}")
             want, got, r0, r1 = _pair(lib, h, dev, n, ef, "auto", policy=policy)
             _check(want, got, r0, r1, f"u8 topk=100 n={n}")
